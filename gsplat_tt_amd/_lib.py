@@ -1,0 +1,304 @@
+"""ctypes binding of the C ABI in include/gsplat_hip.h (libgsplat_hip.so).
+
+This is the Python-side mirror of the reference's per-stage operators
+(_gsplat_cpu.project / tile_assign / sort / cull_and_blend / render_full,
+backends/cpu_cpp/pybind_module.cpp) running on the GPU. There is no CPU
+fallback: if the library is missing, importing raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgsplat_hip.so")
+
+GS_OK, GS_E_INVALID, GS_E_DEVICE, GS_E_CAPACITY = 0, -1, -2, -3
+OUT_FORMATS = {"u8": 0, "bf16": 1, "f32": 2}
+
+EXPORTED = (
+    "gs_create", "gs_destroy", "gs_last_error", "gs_set_timing", "gs_device_info",
+    "gs_scene_set", "gs_render", "gs_project", "gs_tile_assign", "gs_sort_and_bin",
+    "gs_cull_and_blend", "gs_sort_pairs_u64_dev", "gs_last_sort_pass_ms", "gs_dev_alloc",
+    "gs_dev_free", "gs_memcpy_h2d", "gs_memcpy_d2h", "gs_sync",
+)
+
+
+class GsScene(ctypes.Structure):
+    _fields_ = [("means", ctypes.c_void_p), ("cov3d", ctypes.c_void_p),
+                ("cov3d_stride", ctypes.c_int), ("opacities", ctypes.c_void_p),
+                ("colors", ctypes.c_void_p), ("sh_degree", ctypes.c_int),
+                ("n", ctypes.c_int64), ("version", ctypes.c_uint64)]
+
+
+class GsView(ctypes.Structure):
+    _fields_ = [("extrinsics", ctypes.c_float * 16), ("intrinsics", ctypes.c_float * 9),
+                ("image_height", ctypes.c_int), ("image_width", ctypes.c_int),
+                ("tile_size", ctypes.c_int), ("min_opacity", ctypes.c_float),
+                ("contrib_floor", ctypes.c_float), ("mb_contrib_floor", ctypes.c_float),
+                ("cull_disabled", ctypes.c_int), ("transmittance_threshold", ctypes.c_float),
+                ("max_radius", ctypes.c_int), ("k_cap", ctypes.c_float),
+                ("use_isoellipse", ctypes.c_int), ("out_format", ctypes.c_int),
+                ("sh_clamp_hi", ctypes.c_int)]
+
+
+class GsStats(ctypes.Structure):
+    _fields_ = [("num_visible", ctypes.c_int64), ("num_entries", ctypes.c_int64),
+                ("pairs_pre", ctypes.c_int64), ("ms_project", ctypes.c_float),
+                ("ms_depth_sort", ctypes.c_float), ("ms_tile_assign", ctypes.c_float),
+                ("ms_tile_sort", ctypes.c_float), ("ms_blend", ctypes.c_float),
+                ("ms_total", ctypes.c_float)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+_LIB = None
+
+
+def load_library():
+    """Load libgsplat_hip.so (raises OSError when it was not built)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise OSError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+        L = ctypes.CDLL(LIB_PATH)
+        L.gs_last_error.restype = ctypes.c_char_p
+        L.gs_destroy.restype = None
+        for name in EXPORTED:
+            getattr(L, name)  # every declared symbol must resolve
+        _LIB = L
+    return _LIB
+
+
+class GsError(RuntimeError):
+    pass
+
+
+def _check(rc):
+    if rc != GS_OK:
+        msg = load_library().gs_last_error().decode()
+        if rc == GS_E_INVALID:
+            raise ValueError(msg)
+        raise GsError(f"[{rc}] {msg}")
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def make_view(extrinsics, intrinsics, H, W, tile_size=16, min_opacity=1.0 / 255.0,
+              contrib_floor=1.0 / 16384.0, mb_contrib_floor=1.0 / 16384.0, cull_disabled=False,
+              transmittance_threshold=1.0 / 255.0, max_radius=0, k_cap=3.0,
+              use_isoellipse=False, output="f32", sh_clamp=True) -> GsView:
+    v = GsView()
+    e = _f32(extrinsics).reshape(16)
+    k = _f32(intrinsics).reshape(9)
+    for i in range(16):
+        v.extrinsics[i] = float(e[i])
+    for i in range(9):
+        v.intrinsics[i] = float(k[i])
+    v.image_height, v.image_width, v.tile_size = int(H), int(W), int(tile_size)
+    v.min_opacity, v.contrib_floor = float(min_opacity), float(contrib_floor)
+    v.mb_contrib_floor, v.cull_disabled = float(mb_contrib_floor), int(bool(cull_disabled))
+    v.transmittance_threshold, v.max_radius = float(transmittance_threshold), int(max_radius)
+    v.k_cap, v.use_isoellipse = float(k_cap), int(bool(use_isoellipse))
+    v.out_format, v.sh_clamp_hi = OUT_FORMATS[output], int(bool(sh_clamp))
+    return v
+
+
+_OUT_DTYPE = {0: np.uint8, 1: np.uint16, 2: np.float32}
+
+
+class Context:
+    """One GPU context (device + stream + resident scene)."""
+
+    def __init__(self, device: int = 0, timing: bool = False):
+        self._L = load_library()
+        self._c = ctypes.c_void_p()
+        _check(self._L.gs_create(int(device), ctypes.byref(self._c)))
+        if timing:
+            _check(self._L.gs_set_timing(self._c, 1))
+        self._keep = None
+        self._version = 0
+
+    def close(self):
+        if self._c:
+            self._L.gs_destroy(self._c)
+            self._c = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._c
+
+    def device_info(self):
+        cus, minor = ctypes.c_int(), ctypes.c_int()
+        _check(self._L.gs_device_info(self._c, ctypes.byref(cus), ctypes.byref(minor)))
+        return cus.value, minor.value
+
+    # ---- scene + frame
+    @staticmethod
+    def _scene_struct(means, cov3d, opacities, colors, sh_degree=None, version=0):
+        means = _f32(means)
+        n = means.shape[0]
+        cov3d = _f32(cov3d).reshape(n, -1)
+        stride = cov3d.shape[1]
+        colors = _f32(colors)
+        if sh_degree is None:
+            sh_degree = -1 if (colors.ndim == 2 and colors.shape[1] == 3) else \
+                {1: 0, 4: 1, 9: 2, 16: 3}[colors.reshape(n, -1, 3).shape[1]]
+        opac = None if opacities is None else _f32(opacities)
+        s = GsScene(_ptr(means), _ptr(cov3d), stride, _ptr(opac), _ptr(colors), int(sh_degree),
+                    n, int(version))
+        return s, (means, cov3d, opac, colors)
+
+    def set_scene(self, means, cov3d, opacities, colors, sh_degree=None):
+        self._version += 1
+        s, keep = self._scene_struct(means, cov3d, opacities, colors, sh_degree, self._version)
+        _check(self._L.gs_scene_set(self._c, ctypes.byref(s)))
+        self._keep = keep  # keep the host arrays alive for the pointer-keyed cache
+
+    def render(self, view: GsView, out=None):
+        H, W = view.image_height, view.image_width
+        if out is None:
+            out = np.empty((H, W, 3), _OUT_DTYPE[view.out_format])
+        st = GsStats()
+        _check(self._L.gs_render(self._c, ctypes.byref(view), _ptr(out), 0, ctypes.byref(st)))
+        return out, st.as_dict()
+
+    def render_dev(self, view: GsView, dev_out_ptr: int):
+        st = GsStats()
+        _check(self._L.gs_render(self._c, ctypes.byref(view), ctypes.c_void_p(dev_out_ptr), 1,
+                                 ctypes.byref(st)))
+        return st.as_dict()
+
+    # ---- stages (host arrays)
+    def project(self, means, cov3d, opacities, colors, view: GsView, sh_degree=None):
+        self._version += 1
+        s, keep = self._scene_struct(means, cov3d, opacities, colors, sh_degree, self._version)
+        n = s.n
+        valid = np.empty(n, np.uint8)
+        m2 = np.empty((n, 2), np.float32)
+        c2 = np.empty((n, 4), np.float32)
+        dp = np.empty(n, np.float32)
+        rd = np.empty((n, 2), np.float32)
+        co = np.empty((n, 3), np.float32)
+        op = np.empty(n, np.float32)
+        M = ctypes.c_int64()
+        _check(self._L.gs_project(self._c, ctypes.byref(s), ctypes.byref(view), _ptr(valid),
+                                  _ptr(m2), _ptr(c2), _ptr(dp), _ptr(rd), _ptr(co), _ptr(op),
+                                  ctypes.byref(M)))
+        self._keep = keep
+        M = M.value
+        return dict(valid=valid.astype(bool), means2d=m2[:M], covs2d=c2[:M], depths=dp[:M],
+                    radii=rd[:M], colors=co[:M], opacities=op[:M])
+
+    def tile_assign(self, means2d, radii, H, W, tile_size, covs2d=None, opac=None,
+                    contrib_floor=1.0 / 16384.0):
+        means2d, radii = _f32(means2d), _f32(radii)
+        m = means2d.shape[0]
+        covs2d = None if covs2d is None else _f32(covs2d).reshape(m, 4)
+        opac = None if opac is None else _f32(opac)
+        P, Ppre = ctypes.c_int64(), ctypes.c_int64()
+        rc = self._L.gs_tile_assign(self._c, _ptr(means2d), _ptr(radii), ctypes.c_int64(m),
+                                    int(H), int(W), int(tile_size), _ptr(covs2d), _ptr(opac),
+                                    ctypes.c_float(contrib_floor), None, None, ctypes.c_int64(0),
+                                    ctypes.byref(P), ctypes.byref(Ppre))
+        if rc not in (GS_OK, GS_E_CAPACITY):
+            _check(rc)
+        g = np.empty(max(P.value, 1), np.int64)
+        t = np.empty(max(P.value, 1), np.int64)
+        if P.value > 0:
+            _check(self._L.gs_tile_assign(self._c, _ptr(means2d), _ptr(radii), ctypes.c_int64(m),
+                                          int(H), int(W), int(tile_size), _ptr(covs2d),
+                                          _ptr(opac), ctypes.c_float(contrib_floor), _ptr(g),
+                                          _ptr(t), ctypes.c_int64(P.value), ctypes.byref(P),
+                                          ctypes.byref(Ppre)))
+        return g[:P.value], t[:P.value], Ppre.value
+
+    def sort_and_bin(self, gids, tids, depths, tiles_x, tiles_y):
+        gids = np.ascontiguousarray(gids, np.int64)
+        tids = np.ascontiguousarray(tids, np.int64)
+        depths = _f32(depths)
+        P = gids.shape[0]
+        s = np.empty(max(P, 1), np.int64)
+        r = np.empty((tiles_x * tiles_y, 2), np.int64)
+        _check(self._L.gs_sort_and_bin(self._c, _ptr(gids), _ptr(tids), _ptr(depths),
+                                       ctypes.c_int64(P), ctypes.c_int64(depths.shape[0]),
+                                       int(tiles_x), int(tiles_y), _ptr(s), _ptr(r)))
+        return s[:P], r
+
+    def cull_and_blend(self, means2d, covs2d, colors, opac, sorted_ids, tile_ranges,
+                       view: GsView):
+        means2d, colors, opac = _f32(means2d), _f32(colors), _f32(opac)
+        m = means2d.shape[0]
+        covs2d = _f32(covs2d).reshape(m, 4)
+        sorted_ids = np.ascontiguousarray(sorted_ids, np.int64)
+        tile_ranges = np.ascontiguousarray(tile_ranges, np.int64)
+        out = np.empty((view.image_height, view.image_width, 3), _OUT_DTYPE[view.out_format])
+        _check(self._L.gs_cull_and_blend(self._c, _ptr(means2d), _ptr(covs2d), _ptr(colors),
+                                         _ptr(opac), _ptr(sorted_ids), _ptr(tile_ranges),
+                                         ctypes.c_int64(m), ctypes.c_int64(sorted_ids.shape[0]),
+                                         ctypes.byref(view), _ptr(out)))
+        return out
+
+    # ---- device memory + standalone sort
+    def dev_alloc(self, nbytes: int) -> int:
+        p = ctypes.c_void_p()
+        _check(self._L.gs_dev_alloc(self._c, ctypes.c_int64(nbytes), ctypes.byref(p)))
+        return p.value
+
+    def dev_free(self, ptr: int):
+        _check(self._L.gs_dev_free(self._c, ctypes.c_void_p(ptr)))
+
+    def h2d(self, dst: int, arr: np.ndarray):
+        arr = np.ascontiguousarray(arr)
+        _check(self._L.gs_memcpy_h2d(self._c, ctypes.c_void_p(dst), _ptr(arr),
+                                     ctypes.c_int64(arr.nbytes)))
+
+    def d2h(self, arr: np.ndarray, src: int):
+        _check(self._L.gs_memcpy_d2h(self._c, _ptr(arr), ctypes.c_void_p(src),
+                                     ctypes.c_int64(arr.nbytes)))
+        return arr
+
+    def sort_pairs_u64_dev(self, keys_ptr: int, vals_ptr: int, n: int, begin_bit=0, end_bit=64):
+        passes = ctypes.c_int()
+        _check(self._L.gs_sort_pairs_u64_dev(self._c, ctypes.c_void_p(keys_ptr),
+                                             ctypes.c_void_p(vals_ptr), ctypes.c_int64(n),
+                                             int(begin_bit), int(end_bit), ctypes.byref(passes)))
+        return passes.value
+
+    def last_sort_pass_ms(self):
+        buf = (ctypes.c_float * 8)()
+        k = self._L.gs_last_sort_pass_ms(self._c, buf, 8)
+        return [buf[i] for i in range(k)]
+
+    def sort_pairs_u64(self, keys, vals, begin_bit=0, end_bit=64):
+        """Host convenience: stable sort of (u64 key, u32 value) on the GPU."""
+        keys = np.ascontiguousarray(keys, np.uint64)
+        vals = np.ascontiguousarray(vals, np.uint32)
+        n = keys.shape[0]
+        dk, dv = self.dev_alloc(max(n, 1) * 8), self.dev_alloc(max(n, 1) * 4)
+        try:
+            self.h2d(dk, keys)
+            self.h2d(dv, vals)
+            passes = self.sort_pairs_u64_dev(dk, dv, n, begin_bit, end_bit)
+            ko, vo = np.empty_like(keys), np.empty_like(vals)
+            self.d2h(ko, dk)
+            self.d2h(vo, dv)
+        finally:
+            self.dev_free(dk)
+            self.dev_free(dv)
+        return ko, vo, passes

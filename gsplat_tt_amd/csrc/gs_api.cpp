@@ -1,0 +1,866 @@
+// gs_api.cpp - host orchestration behind the C ABI of include/gsplat_hip.h.
+//
+// Mirrors the stage order and failure policy of the reference's render_view
+// (render/host/render.cpp:263-615): project -> visibility gather ->
+// tile_assign -> sort -> cull+blend, all resident in HBM, no CPU fallback
+// (a device failure is an error, render.cpp:252-259,570-578), M == 0 gives a
+// black image (:389-396). The frame path sorts the visible Gaussians by depth
+// once and then emits their pairs in depth order, so a stable sort of the
+// pairs by tile id alone yields the reference's (tile, depth, id) order.
+//
+// Compiled with -ffp-contract=off: the per-Gaussian log terms computed here
+// are the C library's logf values the reference uses (types.h:141-144,
+// tile_assign.cpp:174-183, cull_and_blend.cpp:743-753).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <climits>
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/gsplat_hip.h"
+#include "gs_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+struct GsError : std::runtime_error {
+    int code;
+    GsError(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+#define HIPCHK(x)                                                                        \
+    do {                                                                                 \
+        hipError_t e_ = (x);                                                             \
+        if (e_ != hipSuccess)                                                            \
+            throw GsError(GS_E_DEVICE, std::string(#x) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define REQUIRE(cond, msg)                                  \
+    do {                                                    \
+        if (!(cond)) throw GsError(GS_E_INVALID, (msg));    \
+    } while (0)
+
+template <class F>
+int guard(F&& f) {
+    try {
+        f();
+        return GS_OK;
+    } catch (const GsError& e) {
+        g_err = e.what();
+        return e.code;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return GS_E_DEVICE;
+    }
+}
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    // Grows to at least `bytes`; callers guarantee the stream is idle.
+    void ensure(size_t bytes) {
+        if (bytes <= cap && p != nullptr) return;
+        size_t want = std::max<size_t>(bytes, 256);
+        if (cap > 0) want = std::max(want, cap + cap / 2);
+        want = (want + 4095) & ~size_t(4095);
+        if (p) HIPCHK(hipFree(p));
+        p = nullptr;
+        cap = 0;
+        HIPCHK(hipMalloc(&p, want));
+        cap = want;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+    template <class T>
+    T* as() const { return static_cast<T*>(p); }
+};
+
+template <class F>
+void parallel_for(int64_t n, F&& f) {
+    const int64_t hw = std::max(1u, std::thread::hardware_concurrency());
+    const int64_t workers = std::min<int64_t>(hw, std::max<int64_t>(1, n / 65536));
+    if (workers <= 1) {
+        f(0, n);
+        return;
+    }
+    std::vector<std::thread> ts;
+    const int64_t chunk = (n + workers - 1) / workers;
+    for (int64_t w = 0; w < workers; ++w) {
+        const int64_t lo = w * chunk, hi = std::min(n, lo + chunk);
+        if (lo < hi) ts.emplace_back([&f, lo, hi] { f(lo, hi); });
+    }
+    for (auto& t : ts) t.join();
+}
+
+// Per-Gaussian opacity terms with the C library's logf (types.h:141-176,
+// tile_assign.cpp:171-197, cull_and_blend.cpp:743-753).
+void opacity_terms(const float* op, int64_t n, bool has_opac, float cf, float mbf, float k_cap,
+                   float* kfac, float* m2thr, float* lthr) {
+    parallel_for(n, [&](int64_t lo, int64_t hi) {
+        for (int64_t i = lo; i < hi; ++i) {
+            float k = 3.0f;
+            if (has_opac) {
+                const float q = op[i] / cf;
+                const float arg = (q < 1.0f) ? 1.0f : q;
+                k = std::sqrt(2.0f * std::log(arg));
+            }
+            if (k_cap > 0.0f) k = (k_cap < k) ? k_cap : k;
+            kfac[i] = k;
+            if (m2thr) {
+                const float o = has_opac ? op[i] : 1.0f;
+                m2thr[i] = (o > cf) ? -2.0f * std::log(cf / o) : -1.0f;
+            }
+            if (lthr) {
+                const float o = has_opac ? op[i] : 1.0f;
+                lthr[i] = (o <= mbf) ? 0.0f : std::log(mbf / o);
+            }
+        }
+    });
+}
+
+int tile_bits(int64_t num_tiles) {
+    int b = 0;
+    while (((int64_t)1 << b) < num_tiles) ++b;
+    return std::max(b, 1);
+}
+
+}  // namespace
+
+struct gs_ctx {
+    int device = 0;
+    hipStream_t st = nullptr;
+    bool timing = false;
+    hipEvent_t ev[12] = {};
+    hipEvent_t sort_ev[16] = {};
+    int last_sort_passes = 0;
+    int num_cus = 0;
+
+    // scene
+    struct {
+        const void *means = nullptr, *cov = nullptr, *opac = nullptr, *col = nullptr;
+        int64_t n = -1;
+        int stride = 0, deg = -2;
+        uint64_t ver = 0;
+        bool valid = false;
+    } skey;
+    struct {
+        float cf = 0, mbf = 0, kcap = 0;
+        bool has_opac = false;
+        uint64_t gen = 0;
+        bool valid = false;
+    } tkey;
+    uint64_t scene_gen = 0;
+    gs::SceneDev sd;
+    bool has_opac = false;
+    std::vector<float> h_opac;
+    DevBuf b_mean, b_cov, b_opac, b_col, b_terms, b_upload;
+
+    // frame
+    DevBuf b_rect, b_covc, b_dkey, b_brec, b_src, b_valid;
+    DevBuf b_offs, b_pair_tile, b_pair_id, b_ranges, b_out;
+    DevBuf b_kalt, b_valt, b_hist, b_state, b_lb, b_cnt;
+    DevBuf b_tmp_a, b_tmp_b, b_tmp_c;
+    uint32_t* h_pin = nullptr;  // pinned: counters + histograms
+    gs::SortTemp sort;
+
+    ~gs_ctx() {
+        if (st) (void)hipStreamSynchronize(st);
+        for (DevBuf* b : {&b_mean, &b_cov, &b_opac, &b_col, &b_terms, &b_upload, &b_rect, &b_covc,
+                          &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_pair_tile, &b_pair_id,
+                          &b_ranges, &b_out, &b_kalt, &b_valt, &b_hist, &b_state, &b_lb, &b_cnt,
+                          &b_tmp_a, &b_tmp_b, &b_tmp_c})
+            b->release();
+        if (h_pin) (void)hipHostFree(h_pin);
+        for (auto& e : ev)
+            if (e) (void)hipEventDestroy(e);
+        for (auto& e : sort_ev)
+            if (e) (void)hipEventDestroy(e);
+        if (st) (void)hipStreamDestroy(st);
+    }
+
+    void sync() { HIPCHK(hipStreamSynchronize(st)); }
+
+    // ------------------------------------------------------------ scene
+    void set_scene(const gs_scene* s) {
+        REQUIRE(s != nullptr && s->means != nullptr && s->cov3d != nullptr, "scene: null arrays");
+        REQUIRE(s->n >= 0 && s->n < ((int64_t)1 << 31), "scene: n out of range");
+        REQUIRE(s->cov3d_stride == 9 || s->cov3d_stride == 6, "scene: cov3d_stride must be 9 or 6");
+        REQUIRE(s->sh_degree >= -1 && s->sh_degree <= 3, "scene: sh_degree must be -1..3");
+        REQUIRE(s->colors != nullptr || s->n == 0, "scene: colors required");
+        if (skey.valid && skey.means == s->means && skey.cov == s->cov3d &&
+            skey.opac == s->opacities && skey.col == s->colors && skey.n == s->n &&
+            skey.stride == s->cov3d_stride && skey.deg == s->sh_degree && skey.ver == s->version)
+            return;
+        const int64_t n = s->n;
+        sync();
+        const int K = s->sh_degree < 0 ? 1 : (s->sh_degree + 1) * (s->sh_degree + 1);
+        const int col_planes = 3 * K;
+        b_mean.ensure(std::max<int64_t>(n, 1) * 3 * 4);
+        b_cov.ensure(std::max<int64_t>(n, 1) * 6 * 4);
+        b_opac.ensure(std::max<int64_t>(n, 1) * 4);
+        b_col.ensure(std::max<int64_t>(n, 1) * col_planes * 4);
+        b_terms.ensure(std::max<int64_t>(n, 1) * 3 * 4);
+        const int max_cols = std::max(std::max(3, s->cov3d_stride), col_planes);
+        b_upload.ensure(std::max<int64_t>(n, 1) * max_cols * 4);
+        float* up = b_upload.as<float>();
+        auto transpose = [&](const float* host, int cols, const int* map, int planes, float* dst) {
+            if (n == 0) return;
+            HIPCHK(hipMemcpyAsync(up, host, (size_t)n * cols * 4, hipMemcpyHostToDevice, st));
+            HIPCHK(gs::launch_soa_transpose(up, n, cols, map, planes, dst, st));
+            sync();
+        };
+        const int id3[3] = {0, 1, 2};
+        transpose(s->means, 3, id3, 3, b_mean.as<float>());
+        const int u9[6] = {0, 1, 2, 4, 5, 8};
+        const int u6[6] = {0, 1, 2, 3, 4, 5};
+        transpose(s->cov3d, s->cov3d_stride, s->cov3d_stride == 9 ? u9 : u6, 6, b_cov.as<float>());
+        std::vector<int> cmap(col_planes);
+        for (int j = 0; j < col_planes; ++j) cmap[j] = j;
+        transpose(s->colors, col_planes, cmap.data(), col_planes, b_col.as<float>());
+        has_opac = s->opacities != nullptr;
+        h_opac.assign(has_opac ? (size_t)n : 0, 0.0f);
+        if (has_opac && n > 0) {
+            std::memcpy(h_opac.data(), s->opacities, (size_t)n * 4);
+            HIPCHK(hipMemcpyAsync(b_opac.p, s->opacities, (size_t)n * 4, hipMemcpyHostToDevice, st));
+        }
+        sync();
+        sd = gs::SceneDev{};
+        sd.n = n;
+        sd.sh_degree = s->sh_degree;
+        for (int c = 0; c < 3; ++c) sd.mean[c] = b_mean.as<float>() + (size_t)c * n;
+        for (int c = 0; c < 6; ++c) sd.cov[c] = b_cov.as<float>() + (size_t)c * n;
+        sd.opac = has_opac ? b_opac.as<float>() : nullptr;
+        if (s->sh_degree < 0) {
+            for (int c = 0; c < 3; ++c) sd.col[c] = b_col.as<float>() + (size_t)c * n;
+        } else {
+            sd.sh = b_col.as<float>();
+        }
+        sd.kfac = b_terms.as<float>();
+        sd.m2thr = b_terms.as<float>() + (size_t)n;
+        sd.lthr = b_terms.as<float>() + 2 * (size_t)n;
+        skey.means = s->means;
+        skey.cov = s->cov3d;
+        skey.opac = s->opacities;
+        skey.col = s->colors;
+        skey.n = n;
+        skey.stride = s->cov3d_stride;
+        skey.deg = s->sh_degree;
+        skey.ver = s->version;
+        skey.valid = true;
+        ++scene_gen;
+        tkey.valid = false;
+    }
+
+    void ensure_terms(const gs_view* v) {
+        REQUIRE(skey.valid, "no scene set");
+        if (tkey.valid && tkey.gen == scene_gen && tkey.cf == v->contrib_floor &&
+            tkey.mbf == v->mb_contrib_floor && tkey.kcap == v->k_cap && tkey.has_opac == has_opac)
+            return;
+        const int64_t n = sd.n;
+        std::vector<float> h(std::max<int64_t>(n, 1) * 3);
+        opacity_terms(has_opac ? h_opac.data() : nullptr, n, has_opac, v->contrib_floor,
+                      v->mb_contrib_floor, v->k_cap, h.data(), h.data() + n, h.data() + 2 * n);
+        sync();
+        if (n > 0)
+            HIPCHK(hipMemcpyAsync(b_terms.p, h.data(), (size_t)n * 3 * 4, hipMemcpyHostToDevice, st));
+        sync();
+        tkey = {v->contrib_floor, v->mb_contrib_floor, v->k_cap, has_opac, scene_gen, true};
+    }
+
+    // --------------------------------------------------------- helpers
+    void check_view(const gs_view* v) {
+        REQUIRE(v != nullptr, "view: null");
+        REQUIRE(v->image_height > 0 && v->image_width > 0, "view: image size must be positive");
+        REQUIRE((int64_t)v->image_height * v->image_width <= ((int64_t)1 << 28),
+                "view: image too large");
+        REQUIRE(v->tile_size == 16 || v->tile_size == 32, "view: tile_size must be 16 or 32");
+        REQUIRE(v->out_format >= GS_OUT_U8 && v->out_format <= GS_OUT_F32, "view: bad out_format");
+        REQUIRE(v->contrib_floor > 0.0f && v->mb_contrib_floor > 0.0f, "view: floors must be > 0");
+    }
+
+    gs::ProjParams proj_params(const gs_view* v) {
+        const float* e = v->extrinsics;
+        const float* K = v->intrinsics;
+        gs::ProjParams p{};
+        const int ri[9] = {0, 1, 2, 4, 5, 6, 8, 9, 10};
+        for (int j = 0; j < 9; ++j) p.r[j] = e[ri[j]];
+        p.t[0] = e[3];
+        p.t[1] = e[7];
+        p.t[2] = e[11];
+        p.fx = K[0];
+        p.fy = K[4];
+        p.cx = K[2];
+        p.cy = K[5];
+        p.ccx = -(e[0] * p.t[0] + e[4] * p.t[1] + e[8] * p.t[2]);
+        p.ccy = -(e[1] * p.t[0] + e[5] * p.t[1] + e[9] * p.t[2]);
+        p.ccz = -(e[2] * p.t[0] + e[6] * p.t[1] + e[10] * p.t[2]);
+        const int H = v->image_height, W = v->image_width;
+        const int mr = (v->max_radius < 0) ? INT_MAX
+                       : (v->max_radius > 0 ? v->max_radius : std::min(H, W) / 2);
+        p.max_radius = (float)mr;
+        p.min_opacity = v->min_opacity;
+        p.height = H;
+        p.width = W;
+        p.use_iso = v->use_isoellipse ? 1 : 0;
+        p.has_opac = has_opac ? 1 : 0;
+        p.sh_clamp_hi = v->sh_clamp_hi ? 1 : 0;
+        return p;
+    }
+
+    void ensure_counters() {
+        b_cnt.ensure(64 * 4);
+        if (!h_pin) HIPCHK(hipHostMalloc((void**)&h_pin, (gs::sort_hist_words() + 64) * 4));
+    }
+
+    void ensure_sort(int64_t n, int key_bytes) {
+        b_kalt.ensure(std::max<int64_t>(n, 1) * key_bytes);
+        b_valt.ensure(std::max<int64_t>(n, 1) * 4);
+        b_hist.ensure(gs::sort_hist_words() * 4);
+        const size_t sb = gs::sort_state_bytes(std::max<int64_t>(n, 1));
+        if (b_state.cap < sb) {
+            b_state.ensure(sb);
+            HIPCHK(hipMemsetAsync(b_state.p, 0, b_state.cap, st));
+            sort.epoch = 0;
+        }
+        sort.keys_alt = b_kalt.p;
+        sort.vals_alt = b_valt.as<uint32_t>();
+        sort.hist = b_hist.as<uint32_t>();
+        sort.state = b_state.as<uint64_t>();
+        if (timing) {
+            for (auto& e : sort_ev)
+                if (!e) HIPCHK(hipEventCreate(&e));
+            sort.pass_events = sort_ev;
+            sort.max_timed_passes = 8;
+        } else {
+            sort.pass_events = nullptr;
+            sort.max_timed_passes = 0;
+        }
+    }
+
+    void record(int i) {
+        if (timing) HIPCHK(hipEventRecord(ev[i], st));
+    }
+    float elapsed(int a, int b) {
+        if (!timing) return 0.0f;
+        float ms = 0.0f;
+        HIPCHK(hipEventElapsedTime(&ms, ev[a], ev[b]));
+        return ms;
+    }
+
+    // Project + compaction. Returns M; compact arrays in b_rect/b_covc/b_dkey/b_brec.
+    int64_t run_project(const gs_view* v, bool want_valid, bool want_src) {
+        const int64_t n = sd.n;
+        ensure_counters();
+        b_rect.ensure(std::max<int64_t>(n, 1) * 16);
+        b_covc.ensure(std::max<int64_t>(n, 1) * 16);
+        b_dkey.ensure(std::max<int64_t>(n, 1) * 4);
+        b_brec.ensure(std::max<int64_t>(n, 1) * 48);
+        if (want_src) b_src.ensure(std::max<int64_t>(n, 1) * 4);
+        if (want_valid) b_valid.ensure(std::max<int64_t>(n, 1));
+        const size_t parts = gs::project_partitions(std::max<int64_t>(n, 1));
+        b_lb.ensure(parts * 8);
+        HIPCHK(gs::launch_fill_u32(b_cnt.as<uint32_t>(), 0u, 64, st));
+        HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, parts * 2, st));
+        if (n == 0) return 0;
+        gs::ProjParams p = proj_params(v);
+        gs::Compact c{b_rect.as<float4>(), b_covc.as<float4>(), b_dkey.as<uint32_t>(),
+                      b_brec.as<float4>(), want_src ? b_src.as<uint32_t>() : nullptr};
+        HIPCHK(gs::launch_project(sd, p, c, want_valid ? b_valid.as<uint8_t>() : nullptr,
+                                  b_lb.as<uint64_t>(), b_cnt.as<uint32_t>() + 0,
+                                  b_cnt.as<uint32_t>() + 1, st));
+        HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
+        sync();
+        return h_pin[1];
+    }
+
+    // Candidate count scan + pair emission (+ per-pair cull) over `order`
+    // (nullptr = identity). Returns P; pairs in b_pair_tile / b_pair_id.
+    uint32_t run_tile_assign(const float4* rect, const float4* cov, const uint32_t* order,
+                             int64_t m, const gs::TileParams& tp, uint64_t* p_pre_out) {
+        ensure_counters();
+        b_offs.ensure(std::max<int64_t>(m, 1) * 4);
+        const size_t rparts = gs::rect_scan_partitions(std::max<int64_t>(m, 1));
+        b_lb.ensure(rparts * 8);
+        HIPCHK(gs::launch_fill_u32(b_cnt.as<uint32_t>() + 8, 0u, 8, st));
+        HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, rparts * 2, st));
+        HIPCHK(gs::launch_rect_count_scan(rect, order, m, tp, b_offs.as<uint32_t>(),
+                                          b_lb.as<uint64_t>(), b_cnt.as<uint32_t>() + 8,
+                                          b_cnt.as<uint32_t>() + 9, st));
+        HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
+        sync();
+        const uint32_t p_pre = h_pin[9];
+        if (p_pre == 0xFFFFFFFFu)
+            throw GsError(GS_E_CAPACITY, "tile_assign: more than 2^32-1 candidate pairs");
+        *p_pre_out = p_pre;
+        if (p_pre == 0) return 0;
+        b_pair_tile.ensure((size_t)p_pre * 4);
+        b_pair_id.ensure((size_t)p_pre * 4);
+        const size_t eparts = gs::emit_partitions(p_pre);
+        b_lb.ensure(eparts * 8);
+        HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, eparts * 2, st));
+        HIPCHK(gs::launch_pair_emit(rect, cov, order, b_offs.as<uint32_t>(), m, p_pre, tp,
+                                    b_pair_tile.as<uint32_t>(), b_pair_id.as<uint32_t>(), p_pre,
+                                    b_lb.as<uint64_t>(), b_cnt.as<uint32_t>() + 10,
+                                    b_cnt.as<uint32_t>() + 11, st));
+        HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
+        sync();
+        return h_pin[11];
+    }
+
+    // --------------------------------------------------------- render
+    void render(const gs_view* v, void* out, bool out_dev, gs_stats* stats) {
+        const auto t0 = std::chrono::steady_clock::now();
+        check_view(v);
+        REQUIRE(out != nullptr, "render: null output");
+        ensure_terms(v);
+        if (timing)
+            for (auto& e : ev)
+                if (!e) HIPCHK(hipEventCreate(&e));
+        const int H = v->image_height, W = v->image_width, ts = v->tile_size;
+        const int tiles_x = (W + ts - 1) / ts, tiles_y = (H + ts - 1) / ts;
+        const int64_t T = (int64_t)tiles_x * tiles_y;
+        const size_t px = (size_t)H * W * 3;
+        const size_t ebytes = v->out_format == GS_OUT_F32 ? 4 : (v->out_format == GS_OUT_BF16 ? 2 : 1);
+        void* dout = out;
+        if (!out_dev) {
+            b_out.ensure(px * ebytes);
+            dout = b_out.p;
+        }
+        gs_stats s{};
+        record(0);
+        const int64_t M = run_project(v, false, false);
+        record(1);
+        s.num_visible = M;
+        if (M == 0) {
+            HIPCHK(hipMemsetAsync(dout, 0, px * ebytes, st));
+            finish(out, dout, out_dev, px * ebytes, stats, s, t0);
+            return;
+        }
+        // depth order of the visible Gaussians (stable: ties keep index order)
+        ensure_sort(M, 4);
+        HIPCHK(hipStreamSynchronize(st));
+        int passes = 0;
+        void* kf = nullptr;
+        uint32_t* order = nullptr;
+        b_tmp_a.ensure((size_t)M * 4);
+        HIPCHK(gs::radix_sort_pairs(b_dkey.p, b_tmp_a.as<uint32_t>(), M, 4, 0, 32, sort,
+                                    h_pin + 64, st, &passes, true, &kf, &order));
+        record(2);
+        gs::TileParams tp{tiles_x, tiles_y, ts, v->cull_disabled ? 0 : 1};
+        uint64_t p_pre = 0;
+        const uint32_t P = run_tile_assign(b_rect.as<float4>(), b_covc.as<float4>(), order, M, tp,
+                                           &p_pre);
+        record(3);
+        s.pairs_pre = (int64_t)p_pre;
+        s.num_entries = P;
+        // stable tile sort of the depth-ordered pairs
+        ensure_sort(P, 4);
+        void* tiles_sorted = b_pair_tile.p;
+        uint32_t* ids_sorted = b_pair_id.as<uint32_t>();
+        if (P > 0)
+            HIPCHK(gs::radix_sort_pairs(b_pair_tile.p, b_pair_id.as<uint32_t>(), P, 4, 0,
+                                        tile_bits(T), sort, h_pin + 64, st, &passes, false,
+                                        &tiles_sorted, &ids_sorted));
+        b_ranges.ensure((size_t)T * 8);
+        HIPCHK(gs::launch_tile_ranges(static_cast<uint32_t*>(tiles_sorted), P,
+                                      b_ranges.as<uint32_t>(), T, st));
+        record(4);
+        gs::BlendParams bp{tiles_x, tiles_y, ts, H, W, v->cull_disabled ? 1 : 0,
+                           v->transmittance_threshold, v->out_format};
+        HIPCHK(gs::launch_blend(b_brec.as<float4>(), ids_sorted, b_ranges.as<uint32_t>(), bp,
+                                dout, st));
+        record(5);
+        finish(out, dout, out_dev, px * ebytes, stats, s, t0);
+        if (timing) {
+            s.ms_project = elapsed(0, 1);
+            s.ms_depth_sort = elapsed(1, 2);
+            s.ms_tile_assign = elapsed(2, 3);
+            s.ms_tile_sort = elapsed(3, 4);
+            s.ms_blend = elapsed(4, 5);
+            if (stats) {
+                stats->ms_project = s.ms_project;
+                stats->ms_depth_sort = s.ms_depth_sort;
+                stats->ms_tile_assign = s.ms_tile_assign;
+                stats->ms_tile_sort = s.ms_tile_sort;
+                stats->ms_blend = s.ms_blend;
+            }
+        }
+    }
+
+    void finish(void* out, void* dout, bool out_dev, size_t bytes, gs_stats* stats, gs_stats s,
+                std::chrono::steady_clock::time_point t0) {
+        if (!out_dev) HIPCHK(hipMemcpyAsync(out, dout, bytes, hipMemcpyDeviceToHost, st));
+        sync();
+        s.ms_total = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() - t0)
+                         .count();
+        if (stats) *stats = s;
+    }
+};
+
+extern "C" {
+
+const char* gs_last_error(void) { return g_err.c_str(); }
+
+int gs_create(int device, gs_ctx** out) {
+    return guard([&] {
+        REQUIRE(out != nullptr, "gs_create: null out");
+        int count = 0;
+        HIPCHK(hipGetDeviceCount(&count));
+        REQUIRE(device >= 0 && device < count, "gs_create: no such device");
+        HIPCHK(hipSetDevice(device));
+        auto* c = new gs_ctx();
+        c->device = device;
+        hipError_t e = hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            delete c;
+            throw GsError(GS_E_DEVICE, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+        }
+        (void)hipDeviceGetAttribute(&c->num_cus, hipDeviceAttributeMultiprocessorCount, device);
+        *out = c;
+    });
+}
+
+void gs_destroy(gs_ctx* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    delete ctx;
+}
+
+int gs_set_timing(gs_ctx* ctx, int on) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        ctx->timing = on != 0;
+    });
+}
+
+int gs_device_info(gs_ctx* ctx, int* num_cus, int* arch_minor) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        hipDeviceProp_t prop;
+        HIPCHK(hipGetDeviceProperties(&prop, ctx->device));
+        if (num_cus) *num_cus = prop.multiProcessorCount;
+        if (arch_minor) *arch_minor = prop.minor;
+    });
+}
+
+int gs_scene_set(gs_ctx* ctx, const gs_scene* scene) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->set_scene(scene);
+    });
+}
+
+int gs_render(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device, gs_stats* stats) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->render(view, out, out_on_device != 0, stats);
+    });
+}
+
+int gs_project(gs_ctx* ctx, const gs_scene* scene, const gs_view* view, uint8_t* valid_mask,
+               float* means2d, float* covs2d, float* depths, float* radii, float* colors_out,
+               float* opac_out, int64_t* m_out) {
+    return guard([&] {
+        REQUIRE(ctx && m_out, "null argument");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->set_scene(scene);
+        ctx->check_view(view);
+        ctx->ensure_terms(view);
+        const int64_t n = ctx->sd.n;
+        const int64_t M = ctx->run_project(view, valid_mask != nullptr, false);
+        *m_out = M;
+        if (valid_mask && n > 0)
+            HIPCHK(hipMemcpyAsync(valid_mask, ctx->b_valid.p, (size_t)n, hipMemcpyDeviceToHost, ctx->st));
+        std::vector<float> rect((size_t)M * 4), cov((size_t)M * 4), brec((size_t)M * 12);
+        std::vector<uint32_t> dk((size_t)M);
+        if (M > 0) {
+            HIPCHK(hipMemcpyAsync(rect.data(), ctx->b_rect.p, (size_t)M * 16, hipMemcpyDeviceToHost, ctx->st));
+            HIPCHK(hipMemcpyAsync(cov.data(), ctx->b_covc.p, (size_t)M * 16, hipMemcpyDeviceToHost, ctx->st));
+            HIPCHK(hipMemcpyAsync(brec.data(), ctx->b_brec.p, (size_t)M * 48, hipMemcpyDeviceToHost, ctx->st));
+            HIPCHK(hipMemcpyAsync(dk.data(), ctx->b_dkey.p, (size_t)M * 4, hipMemcpyDeviceToHost, ctx->st));
+        }
+        ctx->sync();
+        for (int64_t m = 0; m < M; ++m) {
+            if (means2d) {
+                means2d[m * 2 + 0] = rect[m * 4 + 0];
+                means2d[m * 2 + 1] = rect[m * 4 + 1];
+            }
+            if (radii) {
+                radii[m * 2 + 0] = rect[m * 4 + 2];
+                radii[m * 2 + 1] = rect[m * 4 + 3];
+            }
+            if (covs2d) {
+                covs2d[m * 4 + 0] = cov[m * 4 + 0];
+                covs2d[m * 4 + 1] = cov[m * 4 + 1];
+                covs2d[m * 4 + 2] = cov[m * 4 + 1];
+                covs2d[m * 4 + 3] = cov[m * 4 + 2];
+            }
+            if (depths) std::memcpy(&depths[m], &dk[m], 4);
+            if (opac_out) opac_out[m] = brec[m * 12 + 8];
+            if (colors_out) {
+                colors_out[m * 3 + 0] = brec[m * 12 + 9];
+                colors_out[m * 3 + 1] = brec[m * 12 + 10];
+                colors_out[m * 3 + 2] = brec[m * 12 + 11];
+            }
+        }
+    });
+}
+
+int gs_tile_assign(gs_ctx* ctx, const float* means2d, const float* radii, int64_t m,
+                   int image_height, int image_width, int tile_size, const float* covs2d,
+                   const float* opac, float contrib_floor, int64_t* gids, int64_t* tids,
+                   int64_t cap, int64_t* p_out, int64_t* p_pre_out) {
+    return guard([&] {
+        REQUIRE(ctx && p_out, "null argument");
+        REQUIRE(m >= 0 && m < ((int64_t)1 << 31), "m out of range");
+        REQUIRE(image_height > 0 && image_width > 0 && tile_size > 0, "bad image/tile size");
+        REQUIRE(m == 0 || (means2d && radii), "null means2d/radii");
+        HIPCHK(hipSetDevice(ctx->device));
+        const bool cull = covs2d != nullptr && opac != nullptr;
+        *p_out = 0;
+        if (p_pre_out) *p_pre_out = 0;
+        if (m == 0) return;
+        std::vector<float> rect((size_t)m * 4), cov((size_t)m * 4, 0.0f);
+        for (int64_t i = 0; i < m; ++i) {
+            rect[i * 4 + 0] = means2d[i * 2 + 0];
+            rect[i * 4 + 1] = means2d[i * 2 + 1];
+            rect[i * 4 + 2] = radii[i * 2 + 0];
+            rect[i * 4 + 3] = radii[i * 2 + 1];
+            if (cull) {
+                cov[i * 4 + 0] = covs2d[i * 4 + 0];
+                cov[i * 4 + 1] = covs2d[i * 4 + 1];
+                cov[i * 4 + 2] = covs2d[i * 4 + 3];
+                const float o = opac[i];
+                cov[i * 4 + 3] = (o > contrib_floor) ? -2.0f * std::log(contrib_floor / o) : -1.0f;
+            }
+        }
+        ctx->sync();
+        ctx->b_tmp_a.ensure((size_t)m * 16);
+        ctx->b_tmp_b.ensure((size_t)m * 16);
+        HIPCHK(hipMemcpyAsync(ctx->b_tmp_a.p, rect.data(), (size_t)m * 16, hipMemcpyHostToDevice, ctx->st));
+        HIPCHK(hipMemcpyAsync(ctx->b_tmp_b.p, cov.data(), (size_t)m * 16, hipMemcpyHostToDevice, ctx->st));
+        const int tx = (image_width + tile_size - 1) / tile_size;
+        const int ty = (image_height + tile_size - 1) / tile_size;
+        gs::TileParams tp{tx, ty, tile_size, cull ? 1 : 0};
+        uint64_t p_pre = 0;
+        const uint32_t P = ctx->run_tile_assign(ctx->b_tmp_a.as<float4>(), ctx->b_tmp_b.as<float4>(),
+                                                nullptr, m, tp, &p_pre);
+        if (p_pre_out) *p_pre_out = (int64_t)p_pre;
+        *p_out = P;
+        if ((int64_t)P > cap) throw GsError(GS_E_CAPACITY, "tile_assign: output capacity too small");
+        std::vector<uint32_t> t(P), g(P);
+        if (P > 0) {
+            HIPCHK(hipMemcpyAsync(t.data(), ctx->b_pair_tile.p, (size_t)P * 4, hipMemcpyDeviceToHost, ctx->st));
+            HIPCHK(hipMemcpyAsync(g.data(), ctx->b_pair_id.p, (size_t)P * 4, hipMemcpyDeviceToHost, ctx->st));
+        }
+        ctx->sync();
+        for (uint32_t i = 0; i < P; ++i) {
+            gids[i] = g[i];
+            tids[i] = t[i];
+        }
+    });
+}
+
+int gs_sort_and_bin(gs_ctx* ctx, const int64_t* gids, const int64_t* tids, const float* depths,
+                    int64_t p, int64_t m, int tiles_x, int tiles_y, int64_t* sorted_ids,
+                    int64_t* tile_ranges) {
+    return guard([&] {
+        REQUIRE(ctx && tile_ranges, "null argument");
+        REQUIRE(tiles_x > 0 && tiles_y > 0, "bad tile grid");
+        REQUIRE(p >= 0 && p < ((int64_t)1 << 32) - 1, "p out of range");
+        HIPCHK(hipSetDevice(ctx->device));
+        const int64_t T = (int64_t)tiles_x * tiles_y;
+        REQUIRE(T < ((int64_t)1 << 31), "too many tiles");
+        std::vector<uint32_t> g((size_t)p), t((size_t)p);
+        for (int64_t i = 0; i < p; ++i) {
+            REQUIRE(gids[i] >= 0 && gids[i] < m, "gaussian id out of range");
+            REQUIRE(tids[i] >= 0 && tids[i] < T, "tile id out of range");
+            g[i] = (uint32_t)gids[i];
+            t[i] = (uint32_t)tids[i];
+        }
+        if (p == 0) {
+            std::memset(tile_ranges, 0, (size_t)T * 16);
+            return;
+        }
+        ctx->sync();
+        ctx->ensure_counters();
+        ctx->b_tmp_a.ensure((size_t)p * 4);
+        ctx->b_tmp_b.ensure((size_t)p * 4);
+        ctx->b_tmp_c.ensure((size_t)std::max<int64_t>(m, 1) * 4);
+        ctx->b_pair_tile.ensure((size_t)p * 8);
+        ctx->b_ranges.ensure((size_t)T * 8);
+        HIPCHK(hipMemcpyAsync(ctx->b_tmp_a.p, g.data(), (size_t)p * 4, hipMemcpyHostToDevice, ctx->st));
+        HIPCHK(hipMemcpyAsync(ctx->b_tmp_b.p, t.data(), (size_t)p * 4, hipMemcpyHostToDevice, ctx->st));
+        if (m > 0)
+            HIPCHK(hipMemcpyAsync(ctx->b_tmp_c.p, depths, (size_t)m * 4, hipMemcpyHostToDevice, ctx->st));
+        uint64_t* keys = ctx->b_pair_tile.as<uint64_t>();
+        HIPCHK(gs::launch_make_keys64(ctx->b_tmp_a.as<uint32_t>(), ctx->b_tmp_b.as<uint32_t>(),
+                                      ctx->b_tmp_c.as<float>(), (uint32_t)p, keys, ctx->st));
+        ctx->ensure_sort(p, 8);
+        ctx->sync();
+        int passes = 0;
+        void* kf = nullptr;
+        uint32_t* vf = nullptr;
+        HIPCHK(gs::radix_sort_pairs(keys, ctx->b_tmp_a.as<uint32_t>(), p, 8, 0,
+                                    32 + tile_bits(T), ctx->sort, ctx->h_pin + 64, ctx->st,
+                                    &passes, false, &kf, &vf));
+        HIPCHK(gs::launch_tile_ranges64(static_cast<uint64_t*>(kf), (uint32_t)p,
+                                        ctx->b_ranges.as<uint32_t>(), T, ctx->st));
+        std::vector<uint32_t> sid((size_t)p), rg((size_t)T * 2);
+        HIPCHK(hipMemcpyAsync(sid.data(), vf, (size_t)p * 4, hipMemcpyDeviceToHost, ctx->st));
+        HIPCHK(hipMemcpyAsync(rg.data(), ctx->b_ranges.p, (size_t)T * 8, hipMemcpyDeviceToHost, ctx->st));
+        ctx->sync();
+        for (int64_t i = 0; i < p; ++i) sorted_ids[i] = sid[i];
+        for (int64_t i = 0; i < T * 2; ++i) tile_ranges[i] = rg[i];
+    });
+}
+
+int gs_cull_and_blend(gs_ctx* ctx, const float* means2d, const float* covs2d,
+                      const float* colors, const float* opac, const int64_t* sorted_ids,
+                      const int64_t* tile_ranges, int64_t m, int64_t p, const gs_view* view,
+                      void* image_out) {
+    return guard([&] {
+        REQUIRE(ctx && view && image_out && tile_ranges, "null argument");
+        REQUIRE(m >= 0 && m < ((int64_t)1 << 31) && p >= 0 && p < ((int64_t)1 << 32), "size out of range");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->check_view(view);
+        const int H = view->image_height, W = view->image_width, ts = view->tile_size;
+        const int tiles_x = (W + ts - 1) / ts, tiles_y = (H + ts - 1) / ts;
+        const int64_t T = (int64_t)tiles_x * tiles_y;
+        std::vector<uint32_t> sid((size_t)std::max<int64_t>(p, 1)), rg((size_t)T * 2);
+        for (int64_t i = 0; i < p; ++i) {
+            REQUIRE(sorted_ids[i] >= 0 && sorted_ids[i] < m, "sorted id out of range");
+            sid[i] = (uint32_t)sorted_ids[i];
+        }
+        for (int64_t t = 0; t < T; ++t) {
+            const int64_t a = tile_ranges[2 * t], b = tile_ranges[2 * t + 1];
+            REQUIRE(a >= 0 && a <= b && b <= p, "tile range out of bounds");
+            rg[2 * t] = (uint32_t)a;
+            rg[2 * t + 1] = (uint32_t)b;
+        }
+        std::vector<float> lthr((size_t)std::max<int64_t>(m, 1));
+        for (int64_t i = 0; i < m; ++i) {
+            const float o = opac[i];
+            lthr[i] = (o <= view->mb_contrib_floor) ? 0.0f : std::log(view->mb_contrib_floor / o);
+        }
+        ctx->sync();
+        const size_t mm = (size_t)std::max<int64_t>(m, 1);
+        ctx->b_tmp_a.ensure(mm * 4 * 11);
+        float* base = ctx->b_tmp_a.as<float>();
+        float *dm = base, *dc = base + mm * 2, *dcol = base + mm * 6, *dop = base + mm * 9,
+              *dl = base + mm * 10;
+        if (m > 0) {
+            HIPCHK(hipMemcpyAsync(dm, means2d, (size_t)m * 8, hipMemcpyHostToDevice, ctx->st));
+            HIPCHK(hipMemcpyAsync(dc, covs2d, (size_t)m * 16, hipMemcpyHostToDevice, ctx->st));
+            HIPCHK(hipMemcpyAsync(dcol, colors, (size_t)m * 12, hipMemcpyHostToDevice, ctx->st));
+            HIPCHK(hipMemcpyAsync(dop, opac, (size_t)m * 4, hipMemcpyHostToDevice, ctx->st));
+            HIPCHK(hipMemcpyAsync(dl, lthr.data(), (size_t)m * 4, hipMemcpyHostToDevice, ctx->st));
+        }
+        ctx->b_brec.ensure(mm * 48);
+        HIPCHK(gs::launch_brec_from_arrays(dm, dc, dcol, dop, dl, m, ctx->b_brec.as<float4>(), ctx->st));
+        ctx->b_pair_id.ensure(sid.size() * 4);
+        ctx->b_ranges.ensure((size_t)T * 8);
+        HIPCHK(hipMemcpyAsync(ctx->b_pair_id.p, sid.data(), sid.size() * 4, hipMemcpyHostToDevice, ctx->st));
+        HIPCHK(hipMemcpyAsync(ctx->b_ranges.p, rg.data(), (size_t)T * 8, hipMemcpyHostToDevice, ctx->st));
+        const size_t ebytes = view->out_format == GS_OUT_F32 ? 4 : (view->out_format == GS_OUT_BF16 ? 2 : 1);
+        const size_t bytes = (size_t)H * W * 3 * ebytes;
+        ctx->b_out.ensure(bytes);
+        gs::BlendParams bp{tiles_x, tiles_y, ts, H, W, view->cull_disabled ? 1 : 0,
+                           view->transmittance_threshold, view->out_format};
+        HIPCHK(gs::launch_blend(ctx->b_brec.as<float4>(), ctx->b_pair_id.as<uint32_t>(),
+                                ctx->b_ranges.as<uint32_t>(), bp, ctx->b_out.p, ctx->st));
+        HIPCHK(hipMemcpyAsync(image_out, ctx->b_out.p, bytes, hipMemcpyDeviceToHost, ctx->st));
+        ctx->sync();
+    });
+}
+
+int gs_sort_pairs_u64_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n, int begin_bit,
+                          int end_bit, int* passes_out) {
+    return guard([&] {
+        REQUIRE(ctx && keys && vals, "null argument");
+        REQUIRE(n >= 0 && n < ((int64_t)1 << 32) - 1, "n out of range");
+        REQUIRE(0 <= begin_bit && begin_bit < end_bit && end_bit <= 64, "bad bit range");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->ensure_counters();
+        ctx->ensure_sort(n, 8);
+        ctx->sync();
+        int passes = 0;
+        void* kf = nullptr;
+        uint32_t* vf = nullptr;
+        HIPCHK(gs::radix_sort_pairs(keys, vals, n, 8, begin_bit, end_bit, ctx->sort,
+                                    ctx->h_pin + 64, ctx->st, &passes, false, &kf, &vf));
+        if (kf != keys) {
+            HIPCHK(hipMemcpyAsync(keys, kf, (size_t)n * 8, hipMemcpyDeviceToDevice, ctx->st));
+            HIPCHK(hipMemcpyAsync(vals, vf, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->st));
+        }
+        ctx->sync();
+        ctx->last_sort_passes = passes;
+        if (passes_out) *passes_out = passes;
+    });
+}
+
+int gs_last_sort_pass_ms(gs_ctx* ctx, float* ms, int max_passes) {
+    if (!ctx || !ctx->timing) return 0;
+    const int np = std::min(std::min(ctx->last_sort_passes, max_passes), 8);
+    for (int i = 0; i < np; ++i) {
+        float v = 0.0f;
+        if (hipEventElapsedTime(&v, ctx->sort_ev[2 * i], ctx->sort_ev[2 * i + 1]) != hipSuccess)
+            v = -1.0f;
+        ms[i] = v;
+    }
+    return np;
+}
+
+int gs_dev_alloc(gs_ctx* ctx, int64_t bytes, void** ptr) {
+    return guard([&] {
+        REQUIRE(ctx && ptr && bytes >= 0, "bad argument");
+        HIPCHK(hipSetDevice(ctx->device));
+        HIPCHK(hipMalloc(ptr, (size_t)std::max<int64_t>(bytes, 1)));
+    });
+}
+
+int gs_dev_free(gs_ctx* ctx, void* ptr) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->sync();
+        if (ptr) HIPCHK(hipFree(ptr));
+    });
+}
+
+int gs_memcpy_h2d(gs_ctx* ctx, void* dst, const void* src, int64_t bytes) {
+    return guard([&] {
+        REQUIRE(ctx && bytes >= 0, "bad argument");
+        HIPCHK(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyHostToDevice, ctx->st));
+        ctx->sync();
+    });
+}
+
+int gs_memcpy_d2h(gs_ctx* ctx, void* dst, const void* src, int64_t bytes) {
+    return guard([&] {
+        REQUIRE(ctx && bytes >= 0, "bad argument");
+        HIPCHK(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToHost, ctx->st));
+        ctx->sync();
+    });
+}
+
+int gs_sync(gs_ctx* ctx) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        ctx->sync();
+    });
+}
+
+}  // extern "C"

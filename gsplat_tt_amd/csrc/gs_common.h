@@ -1,0 +1,116 @@
+// gs_common.h - device helpers shared by the gfx950 kernels: wave64 scans,
+// decoupled look-back, coherent (agent-scope) loads/stores, launch checks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define GS_WAVE 64
+
+namespace gs {
+
+// Agent-scope relaxed accesses: visible across the eight XCD L2s of one GPU.
+template <typename T>
+__device__ __forceinline__ T ld_agent(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void st_agent(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+    const int l = lane_id();
+    return (l == 0) ? 0ull : (~0ull >> (64 - l));
+}
+
+// Inclusive wave-wide prefix sum of a 32-bit value (Hillis-Steele over shfl_up).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+    const int l = lane_id();
+#pragma unroll
+    for (int o = 1; o < GS_WAVE; o <<= 1) {
+        const uint32_t u = __shfl_up(v, o, GS_WAVE);
+        if (l >= o) v += u;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint64_t wave_incl_scan64(uint64_t v) {
+    const int l = lane_id();
+#pragma unroll
+    for (int o = 1; o < GS_WAVE; o <<= 1) {
+        const uint64_t u = __shfl_up(v, o, GS_WAVE);
+        if (l >= o) v += u;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, GS_WAVE);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Decoupled look-back over a chain of 64-bit partition descriptors.
+// Descriptor = flag (2 bits, 62..63) | value (62 bits). flag 0 = not yet
+// published, 1 = aggregate of this partition only, 2 = inclusive prefix.
+// The caller is one full wave (all 64 lanes) of the partition with virtual id
+// `vid` (taken from an atomic ticket, so every predecessor is already
+// resident and never waits on us). Returns the exclusive prefix.
+// ---------------------------------------------------------------------------
+constexpr uint64_t kLbAgg = 1ull << 62;
+constexpr uint64_t kLbInc = 2ull << 62;
+constexpr uint64_t kLbVal = (1ull << 62) - 1;
+constexpr uint32_t kLbMaxSpins = 1u << 24;
+
+__device__ __forceinline__ uint64_t lookback_exclusive(uint64_t* state, uint32_t vid,
+                                                      uint64_t aggregate) {
+    const int l = lane_id();
+    if (vid == 0) {
+        if (l == 0) st_agent(&state[0], kLbInc | aggregate);
+        return 0;
+    }
+    if (l == 0) st_agent(&state[vid], kLbAgg | aggregate);
+    uint64_t excl = 0;
+    int64_t base = (int64_t)vid - 1;
+    uint32_t spins = 0;
+    while (true) {
+        const int64_t idx = base - l;
+        uint64_t s = (idx >= 0) ? ld_agent(&state[idx]) : (kLbInc | 0ull);
+        const uint64_t flag = s >> 62;
+        const uint64_t inc_mask = __ballot(flag == 2);
+        const uint64_t rdy_mask = __ballot(flag != 0);
+        // lanes [0, first_inc] are needed (all 64 when no inclusive seen)
+        uint64_t need;
+        if (inc_mask) {
+            const int first = __ffsll((unsigned long long)inc_mask) - 1;
+            need = (first == 63) ? ~0ull : ((2ull << first) - 1);
+        } else {
+            need = ~0ull;
+        }
+        if ((rdy_mask & need) != need) {
+            // Bounded wait: predecessors are resident (ticket order), so this
+            // only trips on a broken chain; better a wrong count than a hang.
+            if (++spins < kLbMaxSpins) {
+                __builtin_amdgcn_s_sleep(1);
+                continue;
+            }
+        }
+        uint64_t v = ((need >> l) & 1ull) ? (s & kLbVal) : 0ull;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, GS_WAVE);
+        excl += v;
+        if (inc_mask) break;
+        base -= GS_WAVE;
+    }
+    if (l == 0) st_agent(&state[vid], kLbInc | (excl + aggregate));
+    return excl;
+}
+
+}  // namespace gs
+
+// Host-side launch check: every launcher returns hipError_t.
+#define GS_LAUNCH_CHECK() hipGetLastError()

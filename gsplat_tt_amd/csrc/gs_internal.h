@@ -1,0 +1,120 @@
+// gs_internal.h - types shared by the host orchestration (gs_api.cpp) and the
+// kernel translation units, plus the kernel launchers each unit exports.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace gs {
+
+// Scene resident in HBM, structure-of-arrays (one coalesced dword stream per
+// attribute). `sh` holds (d+1)^2*3 planes of n floats, plane index k*3+c.
+struct SceneDev {
+    int64_t n = 0;
+    int sh_degree = -1;        // -1: plain RGB colours in col[0..2]
+    float* mean[3] = {nullptr, nullptr, nullptr};
+    float* cov[6] = {};        // c00 c01 c02 c11 c12 c22
+    float* opac = nullptr;
+    float* col[3] = {nullptr, nullptr, nullptr};
+    float* sh = nullptr;
+    // Per-Gaussian terms that depend only on opacity and the floors; they
+    // are computed on the host with the C library's logf so every log on the
+    // pair path is the reference's bit for bit.
+    float* kfac = nullptr;     // min(sqrt(2 ln max(op/floor,1)), k_cap)
+    float* m2thr = nullptr;    // -2 ln(floor/op) or -1 (drop) [tile cull]
+    float* lthr = nullptr;     // ln(mb_floor/op) or 0 (drop)  [microblock cull]
+};
+
+struct ProjParams {
+    float r[9];
+    float t[3];
+    float fx, fy, cx, cy;
+    float ccx, ccy, ccz;       // camera centre -R^T t (SH view direction)
+    float max_radius;          // already resolved (0 -> min(H,W)/2, <0 -> INT_MAX)
+    float min_opacity;
+    int height, width;
+    int use_iso;
+    int has_opac;
+    int sh_clamp_hi;
+    int write_src;             // also write compact->source index
+};
+
+// Compact (visible-only) Gaussian records, index m in [0, M).
+struct Compact {
+    float4* rect;      // px, py, rx, ry
+    float4* cov;       // a, b, c, m2thr
+    uint32_t* dkey;    // fp32 depth bits
+    float4* brec;      // 3 x float4 per Gaussian: (mx,my,xh,yh) (ci_a,ci_b,ci_c,lt) (op,r,g,b)
+    uint32_t* src;     // source index (optional)
+};
+
+// ---- project.hip
+hipError_t launch_project(const SceneDev& s, const ProjParams& p, Compact out,
+                          uint8_t* valid_mask, uint64_t* lb_state, uint32_t* ticket,
+                          uint32_t* count_out, hipStream_t st);
+hipError_t launch_soa_transpose(const float* aos, int64_t n, int cols, const int* col_map,
+                                int planes, float* soa, hipStream_t st);
+size_t project_partitions(int64_t n);
+hipError_t launch_brec_from_arrays(const float* means2d, const float* covs2d,
+                                   const float* colors, const float* opac, const float* lthr,
+                                   int64_t m, float4* brec, hipStream_t st);
+
+// ---- sort.hip: onesweep LSD radix sort (stable), 8-bit digits.
+struct SortTemp {
+    void* keys_alt = nullptr;      // ping-pong key buffer (n keys)
+    uint32_t* vals_alt = nullptr;  // ping-pong value buffer (n values)
+    uint32_t* hist = nullptr;      // sort_hist_words(): [8][256] histograms + 8 tickets
+    uint64_t* state = nullptr;     // sort_state_bytes(n): look-back descriptors
+    uint32_t epoch = 0;            // bumped per pass; tags descriptors (no clearing)
+    hipEvent_t* pass_events = nullptr;  // optional: 2 per pass (start, stop)
+    int max_timed_passes = 0;
+};
+size_t sort_partitions(int64_t n);
+size_t sort_state_bytes(int64_t n);
+size_t sort_hist_words();
+// Stable sort of (keys, vals) by key bits [begin_bit, end_bit). key_bytes = 4
+// or 8. With vals_iota the input values are taken as 0..n-1 (vals unread).
+// Passes whose digit is constant are skipped; the result is left in either
+// the caller's buffers or the SortTemp alternates: *keys_final / *vals_final.
+// Reads the histogram back to the host (one stream synchronisation).
+hipError_t radix_sort_pairs(void* keys, uint32_t* vals, int64_t n, int key_bytes,
+                            int begin_bit, int end_bit, SortTemp& tmp, uint32_t* host_hist,
+                            hipStream_t st, int* passes_run, bool vals_iota,
+                            void** keys_final, uint32_t** vals_final);
+
+// ---- tiles.hip
+struct TileParams {
+    int tiles_x, tiles_y, tile_size;
+    int cull;          // per-pair Mahalanobis cull on
+};
+hipError_t launch_rect_count_scan(const float4* rect, const uint32_t* order, int64_t m,
+                                  TileParams tp, uint32_t* offs, uint64_t* lb_state,
+                                  uint32_t* ticket, uint32_t* total_out, hipStream_t st);
+hipError_t launch_pair_emit(const float4* rect, const float4* cov, const uint32_t* order,
+                            const uint32_t* offs, int64_t m, uint32_t p_pre, TileParams tp,
+                            uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
+                            uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
+                            hipStream_t st);
+hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, uint32_t* ranges,
+                              int64_t num_tiles, hipStream_t st);
+hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t st);
+hipError_t launch_make_keys64(const uint32_t* gid, const uint32_t* tid, const float* depths,
+                              uint32_t p, uint64_t* keys, hipStream_t st);
+hipError_t launch_tile_ranges64(const uint64_t* keys, uint32_t p, uint32_t* ranges,
+                                int64_t num_tiles, hipStream_t st);
+size_t rect_scan_partitions(int64_t m);
+size_t emit_partitions(uint64_t p_pre);
+
+// ---- blend.hip
+struct BlendParams {
+    int tiles_x, tiles_y, tile_size;
+    int height, width;
+    int cull_disabled;
+    float thr;
+    int out_format;    // 0 u8, 1 bf16, 2 f32
+};
+hipError_t launch_blend(const float4* brec, const uint32_t* sorted_id, const uint32_t* ranges,
+                        BlendParams bp, void* out, hipStream_t st);
+
+}  // namespace gs

@@ -1,0 +1,320 @@
+// project.hip - fused per-Gaussian projection + SH colour + stable visibility
+// compaction, one pass over the scene.
+//
+// Per Gaussian (reference src/gsplat_cpu/project.cpp:558-685): camera-space
+// mean (R*m first, then +t), near-plane / opacity reject, pixel mean, EWA
+// Jacobian, cov_cam from the 6 unique cov3d entries, cov2d + 0.3 low-pass,
+// opacity-aware radius and the image-overlap validity test. Visible
+// Gaussians are written in source order (project.cpp:710-797) with a
+// decoupled look-back over 1024-Gaussian partitions, so compact index m equals
+// the reference's.
+//
+// All float expressions keep the reference's operation order and the unit is
+// compiled with -ffp-contract=off, so every output is bit-identical to the
+// reference's fp32 results.
+#include "gs_common.h"
+#include "gs_internal.h"
+
+namespace gs {
+namespace {
+
+constexpr int kProjThreads = 256;
+constexpr int kProjItems = 4;
+constexpr int kProjPart = kProjThreads * kProjItems;
+
+__device__ __forceinline__ float fmin_std(float a, float b) { return (b < a) ? b : a; }
+__device__ __forceinline__ float fmax_std(float a, float b) { return (a < b) ? b : a; }
+
+// 3DGS real SH basis (gsplat/train_oracle.py:46-52, 99-122), fp32,
+// left-to-right. `sh` planes: coefficient k, channel c at sh[(k*3+c)*n + i].
+template <int DEG>
+__device__ __forceinline__ void sh_eval(const float* __restrict__ sh, int64_t n, int64_t i,
+                                        float x, float y, float z, int clamp_hi, float* rgb) {
+    constexpr float C0 = 0.28209479177387814f;
+    constexpr float C1 = 0.4886025119029199f;
+    constexpr float C20 = 1.0925484305920792f, C21 = -1.0925484305920792f,
+                    C22 = 0.31539156525252005f, C23 = -1.0925484305920792f,
+                    C24 = 0.5462742152960396f;
+    constexpr float C30 = -0.5900435899266435f, C31 = 2.890611442640554f,
+                    C32 = -0.4570457994644658f, C33 = 0.3731763325901154f,
+                    C34 = -0.4570457994644658f, C35 = 1.445305721320277f,
+                    C36 = -0.5900435899266435f;
+    const float xx = x * x, yy = y * y, zz = z * z;
+    const float xy = x * y, yz = y * z, xz = x * z;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        auto S = [&](int k) { return sh[(int64_t)(k * 3 + c) * n + i]; };
+        float o = C0 * S(0);
+        if (DEG >= 1) {
+            o = o - C1 * y * S(1) + C1 * z * S(2) - C1 * x * S(3);
+        }
+        if (DEG >= 2) {
+            o = o + C20 * xy * S(4) + C21 * yz * S(5) + C22 * (2.0f * zz - xx - yy) * S(6) +
+                C23 * xz * S(7) + C24 * (xx - yy) * S(8);
+        }
+        if (DEG >= 3) {
+            o = o + C30 * y * (3.0f * xx - yy) * S(9) + C31 * xy * z * S(10) +
+                C32 * y * (4.0f * zz - xx - yy) * S(11) +
+                C33 * z * (2.0f * zz - 3.0f * xx - 3.0f * yy) * S(12) +
+                C34 * x * (4.0f * zz - xx - yy) * S(13) + C35 * z * (xx - yy) * S(14) +
+                C36 * x * (xx - 3.0f * yy) * S(15);
+        }
+        o = o + 0.5f;
+        o = (o < 0.0f) ? 0.0f : o;
+        if (clamp_hi) o = (o > 1.0f) ? 1.0f : o;
+        rgb[c] = o;
+    }
+}
+
+template <int DEG>
+__global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams p, Compact out,
+                                                          uint8_t* __restrict__ valid_mask,
+                                                          uint64_t* lb_state, uint32_t* ticket,
+                                                          uint32_t* count_out) {
+    __shared__ uint32_t s_vid;
+    __shared__ uint32_t s_cnt[kProjItems][kProjThreads / GS_WAVE];
+    __shared__ uint64_t s_excl;
+    const int tid = threadIdx.x;
+    const int w = tid / GS_WAVE;
+    const int lane = lane_id();
+    if (tid == 0) s_vid = atomicAdd(ticket, 1u);
+    __syncthreads();
+    const uint32_t vid = s_vid;
+    const int64_t base = (int64_t)vid * kProjPart;
+    const int64_t n = s.n;
+
+    float vmx[kProjItems], vmy[kProjItems], vtz[kProjItems];
+    float va[kProjItems], vb[kProjItems], vc[kProjItems], vrx[kProjItems], vry[kProjItems];
+    bool valid[kProjItems];
+    uint64_t bal[kProjItems];
+
+#pragma unroll
+    for (int it = 0; it < kProjItems; ++it) {
+        const int64_t i = base + it * kProjThreads + tid;
+        valid[it] = false;
+        vmx[it] = vmy[it] = vtz[it] = va[it] = vb[it] = vc[it] = vrx[it] = vry[it] = 0.0f;
+        if (i < n) {
+            const float mx = s.mean[0][i], my = s.mean[1][i], mz = s.mean[2][i];
+            const float rmx = mx * p.r[0] + my * p.r[1] + mz * p.r[2];
+            const float rmy = mx * p.r[3] + my * p.r[4] + mz * p.r[5];
+            const float rmz = mx * p.r[6] + my * p.r[7] + mz * p.r[8];
+            const float tx = rmx + p.t[0];
+            const float ty = rmy + p.t[1];
+            const float tz = rmz + p.t[2];
+            bool ok = !(tz <= 0.2f);
+            if (ok && p.has_opac) ok = !(s.opac[i] < p.min_opacity);
+            if (ok) {
+                const float inv_tz = 1.0f / tz;
+                const float mean_x = p.fx * tx * inv_tz + p.cx;
+                const float mean_y = p.fy * ty * inv_tz + p.cy;
+                const float tz2 = tz * tz;
+                const float j00 = p.fx / tz, j02 = -p.fx * tx / tz2;
+                const float j11 = p.fy / tz, j12 = -p.fy * ty / tz2;
+                const float c00 = s.cov[0][i], c01 = s.cov[1][i], c02 = s.cov[2][i];
+                const float c11 = s.cov[3][i], c12 = s.cov[4][i], c22 = s.cov[5][i];
+                const float r00 = p.r[0], r01 = p.r[1], r02 = p.r[2];
+                const float r10 = p.r[3], r11 = p.r[4], r12 = p.r[5];
+                const float r20 = p.r[6], r21 = p.r[7], r22 = p.r[8];
+                const float v0_0 = c00 * r00 + c01 * r01 + c02 * r02;
+                const float v0_1 = c01 * r00 + c11 * r01 + c12 * r02;
+                const float v0_2 = c02 * r00 + c12 * r01 + c22 * r02;
+                const float v1_0 = c00 * r10 + c01 * r11 + c02 * r12;
+                const float v1_1 = c01 * r10 + c11 * r11 + c12 * r12;
+                const float v1_2 = c02 * r10 + c12 * r11 + c22 * r12;
+                const float v2_0 = c00 * r20 + c01 * r21 + c02 * r22;
+                const float v2_1 = c01 * r20 + c11 * r21 + c12 * r22;
+                const float v2_2 = c02 * r20 + c12 * r21 + c22 * r22;
+                const float cc00 = r00 * v0_0 + r01 * v0_1 + r02 * v0_2;
+                const float cc01 = r00 * v1_0 + r01 * v1_1 + r02 * v1_2;
+                const float cc02 = r00 * v2_0 + r01 * v2_1 + r02 * v2_2;
+                const float cc11 = r10 * v1_0 + r11 * v1_1 + r12 * v1_2;
+                const float cc12 = r10 * v2_0 + r11 * v2_1 + r12 * v2_2;
+                const float cc22 = r20 * v2_0 + r21 * v2_1 + r22 * v2_2;
+                const float m00 = j00 * cc00 + j02 * cc02;
+                const float m01 = j00 * cc01 + j02 * cc12;
+                const float m02 = j00 * cc02 + j02 * cc22;
+                const float m11 = j11 * cc11 + j12 * cc12;
+                const float m12 = j11 * cc12 + j12 * cc22;
+                const float a = m00 * j00 + m02 * j02 + 0.3f;
+                const float b = m01 * j11 + m02 * j12;
+                const float c = m11 * j11 + m12 * j12 + 0.3f;
+                const float k = s.kfac[i];
+                float rx, ry;
+                if (p.use_iso) {
+                    const float trace = a + c;
+                    const float disc =
+                        sqrtf(fmax_std(trace * trace - 4.0f * (a * c - b * b), 0.0f));
+                    const float l1 = 0.5f * (trace + disc);
+                    const float l2 = 0.5f * (trace - disc);
+                    const float theta = 0.5f * atan2f(2.0f * b, a - c);
+                    const float ct = cosf(theta), st = sinf(theta);
+                    const float cos2 = ct * ct, sin2 = st * st;
+                    rx = ceilf(k * sqrtf(fmax_std(l1 * cos2 + l2 * sin2, 0.0f)));
+                    ry = ceilf(k * sqrtf(fmax_std(l1 * sin2 + l2 * cos2, 0.0f)));
+                } else {
+                    rx = ceilf(k * sqrtf(fmax_std(a, 0.0f)));
+                    ry = ceilf(k * sqrtf(fmax_std(c, 0.0f)));
+                }
+                const bool v = (mean_x + rx > 0.0f) && (mean_x - rx < (float)p.width) &&
+                               (mean_y + ry > 0.0f) && (mean_y - ry < (float)p.height) &&
+                               (rx > 0.0f) && (ry > 0.0f) && (rx <= p.max_radius) &&
+                               (ry <= p.max_radius);
+                valid[it] = v;
+                vmx[it] = mean_x;
+                vmy[it] = mean_y;
+                vtz[it] = tz;
+                va[it] = a;
+                vb[it] = b;
+                vc[it] = c;
+                vrx[it] = rx;
+                vry[it] = ry;
+            }
+            if (valid_mask != nullptr) valid_mask[i] = valid[it] ? 1 : 0;
+        }
+        bal[it] = __ballot(valid[it]);
+        if (lane == 0) s_cnt[it][w] = (uint32_t)__popcll(bal[it]);
+    }
+    __syncthreads();
+
+    uint32_t total = 0;
+    uint32_t my_off[kProjItems];
+#pragma unroll
+    for (int it = 0; it < kProjItems; ++it) {
+#pragma unroll
+        for (int ww = 0; ww < kProjThreads / GS_WAVE; ++ww) {
+            if (ww == w) my_off[it] = total;
+            total += s_cnt[it][ww];
+        }
+    }
+    if (w == 0) {
+        const uint64_t excl = lookback_exclusive(lb_state, vid, total);
+        if (lane == 0) {
+            s_excl = excl;
+            if (vid == gridDim.x - 1) *count_out = (uint32_t)(excl + total);
+        }
+    }
+    __syncthreads();
+    const uint64_t excl = s_excl;
+    const uint64_t lt_mask = lanemask_lt();
+
+#pragma unroll
+    for (int it = 0; it < kProjItems; ++it) {
+        if (!valid[it]) continue;
+        const int64_t i = base + it * kProjThreads + tid;
+        const uint64_t m = excl + my_off[it] + (uint64_t)__popcll(bal[it] & lt_mask);
+        const float a = va[it], b = vb[it], c = vc[it];
+        out.rect[m] = make_float4(vmx[it], vmy[it], vrx[it], vry[it]);
+        out.cov[m] = make_float4(a, b, c, s.m2thr[i]);
+        out.dkey[m] = __float_as_uint(vtz[it]);
+        // Microblock cull / blend record (cull_and_blend.cpp:723-777).
+        const float det = fmax_std(a * c - b * b, 1e-6f);
+        const float ci_a = c / det;
+        const float ci_b = -b / det;
+        const float ci_c = a / det;
+        const float lt = s.lthr[i];
+        float xh = 0.0f, yh = 0.0f;
+        if (lt < 0.0f) {
+            const float rd = sqrtf(-2.0f * lt);
+            xh = rd * sqrtf(fmax_std(a, 0.0f));
+            yh = rd * sqrtf(fmax_std(c, 0.0f));
+        }
+        float rgb[3];
+        if (DEG < 0) {
+            rgb[0] = s.col[0][i];
+            rgb[1] = s.col[1][i];
+            rgb[2] = s.col[2][i];
+        } else {
+            const float dx = s.mean[0][i] - p.ccx;
+            const float dy = s.mean[1][i] - p.ccy;
+            const float dz = s.mean[2][i] - p.ccz;
+            const float nrm = sqrtf(dx * dx + dy * dy + dz * dz);
+            sh_eval<(DEG < 0 ? 0 : DEG)>(s.sh, n, i, dx / nrm, dy / nrm, dz / nrm,
+                                         p.sh_clamp_hi, rgb);
+        }
+        const float op = p.has_opac ? s.opac[i] : 1.0f;
+        out.brec[m * 3 + 0] = make_float4(vmx[it], vmy[it], xh, yh);
+        out.brec[m * 3 + 1] = make_float4(ci_a, ci_b, ci_c, lt);
+        out.brec[m * 3 + 2] = make_float4(op, rgb[0], rgb[1], rgb[2]);
+        if (out.src != nullptr) out.src[m] = (uint32_t)i;
+    }
+}
+
+struct ColMap {
+    int c[64];
+};
+
+// AoS (n x cols) -> SoA planes; plane j takes column map.c[j].
+__global__ void k_soa_transpose(const float* __restrict__ aos, int64_t n, int cols, ColMap map,
+                                int planes, float* __restrict__ soa) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    for (int j = 0; j < planes; ++j) soa[(int64_t)j * n + i] = aos[i * cols + map.c[j]];
+}
+
+__global__ void k_brec_from_arrays(const float* __restrict__ means2d,
+                                   const float* __restrict__ covs2d,
+                                   const float* __restrict__ colors,
+                                   const float* __restrict__ opac,
+                                   const float* __restrict__ lthr, int64_t m,
+                                   float4* __restrict__ brec) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m) return;
+    const float a = covs2d[i * 4 + 0], b = covs2d[i * 4 + 1], c = covs2d[i * 4 + 3];
+    const float det = fmax_std(a * c - b * b, 1e-6f);
+    const float lt = lthr[i];
+    float xh = 0.0f, yh = 0.0f;
+    if (lt < 0.0f) {
+        const float rd = sqrtf(-2.0f * lt);
+        xh = rd * sqrtf(fmax_std(a, 0.0f));
+        yh = rd * sqrtf(fmax_std(c, 0.0f));
+    }
+    brec[i * 3 + 0] = make_float4(means2d[i * 2 + 0], means2d[i * 2 + 1], xh, yh);
+    brec[i * 3 + 1] = make_float4(c / det, -b / det, a / det, lt);
+    brec[i * 3 + 2] = make_float4(opac[i], colors[i * 3 + 0], colors[i * 3 + 1],
+                                  colors[i * 3 + 2]);
+}
+
+}  // namespace
+
+hipError_t launch_project(const SceneDev& s, const ProjParams& p, Compact out,
+                          uint8_t* valid_mask, uint64_t* lb_state, uint32_t* ticket,
+                          uint32_t* count_out, hipStream_t st) {
+    if (s.n <= 0) return hipSuccess;
+    const unsigned grid = (unsigned)((s.n + kProjPart - 1) / kProjPart);
+    switch (s.sh_degree) {
+        case -1: k_project<-1><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out); break;
+        case 0: k_project<0><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out); break;
+        case 1: k_project<1><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out); break;
+        case 2: k_project<2><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out); break;
+        case 3: k_project<3><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+size_t project_partitions(int64_t n) { return (size_t)((n + kProjPart - 1) / kProjPart); }
+
+hipError_t launch_soa_transpose(const float* aos, int64_t n, int cols, const int* col_map,
+                                int planes, float* soa, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    if (planes > 64 || planes <= 0) return hipErrorInvalidValue;
+    ColMap map{};
+    for (int j = 0; j < planes; ++j) {
+        if (col_map[j] < 0 || col_map[j] >= cols) return hipErrorInvalidValue;
+        map.c[j] = col_map[j];
+    }
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    k_soa_transpose<<<grid, 256, 0, st>>>(aos, n, cols, map, planes, soa);
+    return hipGetLastError();
+}
+
+hipError_t launch_brec_from_arrays(const float* means2d, const float* covs2d,
+                                   const float* colors, const float* opac, const float* lthr,
+                                   int64_t m, float4* brec, hipStream_t st) {
+    if (m <= 0) return hipSuccess;
+    const unsigned grid = (unsigned)((m + 255) / 256);
+    k_brec_from_arrays<<<grid, 256, 0, st>>>(means2d, covs2d, colors, opac, lthr, m, brec);
+    return hipGetLastError();
+}
+
+}  // namespace gs

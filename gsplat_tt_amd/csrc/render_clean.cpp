@@ -1,0 +1,192 @@
+// render_clean.cpp - the drop-in `render_clean` Python module over the C ABI.
+//
+// Same surface as the reference's module (render/host/render.cpp:617-721):
+// render_view(...) -> (uint8 (H,W,3), {"num_visible", "num_entries"}) plus
+// pfwc_num_cores, bump_scene_version, scene_version, device_shutdown,
+// stage_timings, reset_stage_timings. Device work runs with the GIL released
+// under one module mutex (render.cpp:73-75, 351-354). No CPU fallback: a
+// device failure raises RuntimeError (render.cpp:252-259).
+//
+// Extensions, all keyword-only with defaults that keep the reference's
+// behaviour: `output` ("u8" default, "bf16" as uint16 bits, "f32") and SH
+// colours (colors of shape (N, K, 3), K = (d+1)^2, evaluated on the GPU).
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+
+#include <chrono>
+#include <cstring>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+
+#include "gsplat_hip.h"
+
+namespace py = pybind11;
+
+namespace {
+
+std::mutex g_mutex;
+gs_ctx* g_ctx = nullptr;
+uint64_t g_scene_version = 0;
+
+struct Timings {
+    int64_t views = 0;
+    double project = 0, depth_sort = 0, tile_assign = 0, tile_sort = 0, blend = 0, view_total = 0;
+} g_t;
+
+void check(int rc) {
+    if (rc == GS_OK) return;
+    const std::string msg = std::string("render_clean: ") + gs_last_error();
+    if (rc == GS_E_INVALID) throw std::invalid_argument(msg);
+    throw std::runtime_error(msg);
+}
+
+gs_ctx* ctx_locked() {
+    if (g_ctx == nullptr) {
+        check(gs_create(0, &g_ctx));
+        check(gs_set_timing(g_ctx, 1));
+    }
+    return g_ctx;
+}
+
+using farr = py::array_t<float, py::array::c_style | py::array::forcecast>;
+
+py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr extrinsics,
+                      farr intrinsics, int image_height, int image_width, int tile_size,
+                      float min_opacity, float contrib_floor, float mb_contrib_floor,
+                      bool cull_disabled, float transmittance_threshold, int max_radius,
+                      float k_cap, bool use_isoellipse, int blend_mode, py::object next_extrinsics,
+                      const std::string& output, bool sh_clamp) {
+    (void)blend_mode;
+    const auto mi = means.request();
+    if (mi.ndim != 2 || mi.shape[1] != 3) throw std::invalid_argument("means must have shape (N, 3)");
+    const int64_t N = mi.shape[0];
+    const auto ci = cov3d.request();
+    int stride = 0;
+    if (ci.size == N * 9) stride = 9;
+    else if (ci.size == N * 6) stride = 6;
+    else throw std::invalid_argument("cov3d must have shape (N, 3, 3), (N, 9) or (N, 6)");
+    const auto oi = opacities.request();
+    if (oi.size != N) throw std::invalid_argument("opacities must have shape (N,)");
+    const auto coli = colors.request();
+    int deg = -1;
+    if (coli.ndim == 2 && coli.shape[1] == 3 && coli.shape[0] == N) {
+        deg = -1;
+    } else if (coli.ndim == 3 && coli.shape[0] == N && coli.shape[2] == 3) {
+        const int64_t K = coli.shape[1];
+        deg = K == 1 ? 0 : K == 4 ? 1 : K == 9 ? 2 : K == 16 ? 3 : -2;
+        if (deg == -2) throw std::invalid_argument("colors: SH coefficient count must be 1, 4, 9 or 16");
+    } else {
+        throw std::invalid_argument("colors must have shape (N, 3) or (N, K, 3)");
+    }
+    if (extrinsics.size() != 16) throw std::invalid_argument("extrinsics must be 4x4");
+    if (intrinsics.size() != 9) throw std::invalid_argument("intrinsics must be 3x3");
+    if (!next_extrinsics.is_none()) {
+        auto ne = farr::ensure(next_extrinsics);
+        if (!ne || ne.size() != 16)
+            throw std::invalid_argument("render_view: next_extrinsics must be 16 floats (4x4)");
+    }
+    int fmt;
+    if (output == "u8") fmt = GS_OUT_U8;
+    else if (output == "bf16") fmt = GS_OUT_BF16;
+    else if (output == "f32") fmt = GS_OUT_F32;
+    else throw std::invalid_argument("output must be 'u8', 'bf16' or 'f32'");
+
+    gs_scene sc{};
+    sc.means = static_cast<const float*>(mi.ptr);
+    sc.cov3d = static_cast<const float*>(ci.ptr);
+    sc.cov3d_stride = stride;
+    sc.opacities = static_cast<const float*>(oi.ptr);
+    sc.colors = static_cast<const float*>(coli.ptr);
+    sc.sh_degree = deg;
+    sc.n = N;
+    gs_view v{};
+    std::memcpy(v.extrinsics, extrinsics.data(), sizeof(v.extrinsics));
+    std::memcpy(v.intrinsics, intrinsics.data(), sizeof(v.intrinsics));
+    v.image_height = image_height;
+    v.image_width = image_width;
+    v.tile_size = tile_size;
+    v.min_opacity = min_opacity;
+    v.contrib_floor = contrib_floor;
+    v.mb_contrib_floor = mb_contrib_floor;
+    v.cull_disabled = cull_disabled ? 1 : 0;
+    v.transmittance_threshold = transmittance_threshold;
+    v.max_radius = max_radius;
+    v.k_cap = k_cap;
+    v.use_isoellipse = use_isoellipse ? 1 : 0;
+    v.out_format = fmt;
+    v.sh_clamp_hi = sh_clamp ? 1 : 0;
+    if (image_height <= 0 || image_width <= 0) throw std::invalid_argument("image size must be positive");
+
+    py::array image;
+    if (fmt == GS_OUT_U8) image = py::array_t<uint8_t>({image_height, image_width, 3});
+    else if (fmt == GS_OUT_BF16) image = py::array_t<uint16_t>({image_height, image_width, 3});
+    else image = py::array_t<float>({image_height, image_width, 3});
+    void* out = image.mutable_data();
+    gs_stats st{};
+    {
+        py::gil_scoped_release nogil;
+        std::lock_guard<std::mutex> lock(g_mutex);
+        gs_ctx* c = ctx_locked();
+        sc.version = g_scene_version;
+        check(gs_scene_set(c, &sc));
+        check(gs_render(c, &v, out, 0, &st));
+        g_t.views++;
+        g_t.project += st.ms_project;
+        g_t.depth_sort += st.ms_depth_sort;
+        g_t.tile_assign += st.ms_tile_assign;
+        g_t.tile_sort += st.ms_tile_sort;
+        g_t.blend += st.ms_blend;
+        g_t.view_total += st.ms_total;
+    }
+    py::dict stats;
+    stats["num_visible"] = st.num_visible;
+    stats["num_entries"] = st.num_entries;
+    return py::make_tuple(image, stats);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(render_clean, m) {
+    m.doc() = "MI355X (gfx950) Gaussian-splat renderer with the render_clean surface";
+    m.def("render_view", &render_view, "Render one view on the GPU", py::arg("means"),
+          py::arg("cov3d"), py::arg("opacities"), py::arg("colors"), py::arg("extrinsics"),
+          py::arg("intrinsics"), py::arg("image_height"), py::arg("image_width"),
+          py::arg("tile_size"), py::arg("min_opacity"), py::arg("contrib_floor"),
+          py::arg("mb_contrib_floor"), py::arg("cull_disabled"),
+          py::arg("transmittance_threshold"), py::arg("max_radius"), py::arg("k_cap"),
+          py::arg("use_isoellipse"), py::arg("blend_mode") = 2,
+          py::arg("next_extrinsics") = py::none(), py::kw_only(), py::arg("output") = "u8",
+          py::arg("sh_clamp") = true);
+    m.def("pfwc_num_cores", []() {
+        py::gil_scoped_release nogil;
+        std::lock_guard<std::mutex> lock(g_mutex);
+        int cus = 0;
+        check(gs_device_info(ctx_locked(), &cus, nullptr));
+        return static_cast<int64_t>(cus);
+    });
+    m.def("bump_scene_version", []() {
+        py::gil_scoped_release nogil;
+        std::lock_guard<std::mutex> lock(g_mutex);
+        return ++g_scene_version;
+    });
+    m.def("scene_version", []() { return g_scene_version; });
+    m.def("device_shutdown", []() {
+        py::gil_scoped_release nogil;
+        std::lock_guard<std::mutex> lock(g_mutex);
+        if (g_ctx) gs_destroy(g_ctx);
+        g_ctx = nullptr;
+    });
+    m.def("stage_timings", []() {
+        py::dict d;
+        d["views"] = g_t.views;
+        d["project"] = g_t.project;
+        d["depth_sort"] = g_t.depth_sort;
+        d["tile_assign"] = g_t.tile_assign;
+        d["sort"] = g_t.tile_sort;
+        d["blend"] = g_t.blend;
+        d["view_total"] = g_t.view_total;
+        return d;
+    });
+    m.def("reset_stage_timings", []() { g_t = Timings{}; });
+}

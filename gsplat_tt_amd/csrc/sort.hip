@@ -1,0 +1,330 @@
+// sort.hip - stable onesweep LSD radix sort of (key, u32 value) pairs on gfx950.
+//
+// One upsweep pass builds the digit histograms of every pass at once; each
+// digit pass is then a single kernel (Adinets & Merrill, "Onesweep", 2022):
+//   * a 4096-key partition per 256-thread workgroup, partitions taken in
+//     order from an atomic ticket so look-back only waits on resident
+//     predecessors;
+//   * wave64 stable ranking with 8 ballots per key (peer mask of equal digits)
+//     plus per-wave digit counters in LDS;
+//   * per-digit decoupled look-back over epoch-tagged 64-bit descriptors (no
+//     clearing between passes or sorts);
+//   * keys re-ordered by digit in LDS and written out in digit runs, so global
+//     stores are contiguous per digit.
+// Stability across passes makes the whole sort stable, which is what the
+// reference's per-tile depth sort requires (src/gsplat_cpu/sort.cpp:24-85,
+// ties keep input order).
+#include <algorithm>
+#include <utility>
+
+#include "gs_common.h"
+#include "gs_internal.h"
+
+namespace gs {
+namespace {
+
+constexpr int kSortThreads = 256;
+constexpr int kSortItems = 16;
+constexpr int kSortPart = kSortThreads * kSortItems;   // 4096 keys
+constexpr int kWaves = kSortThreads / GS_WAVE;
+constexpr int kHistThreads = 256;
+constexpr int kMaxPasses = 8;
+
+// descriptor: [63:34] epoch, [33:32] flag (1 aggregate, 2 inclusive), [31:0] value
+__device__ __forceinline__ uint64_t make_desc(uint32_t epoch, uint32_t flag, uint32_t v) {
+    return ((uint64_t)epoch << 34) | ((uint64_t)flag << 32) | v;
+}
+
+template <typename K>
+__device__ __forceinline__ uint32_t digit_of(K k, int shift, uint32_t mask) {
+    return (uint32_t)(k >> shift) & mask;
+}
+
+// Exclusive scan of one value per thread over a 256-thread block.
+__device__ __forceinline__ uint32_t block_excl_scan256(uint32_t v, uint32_t* s_tmp) {
+    const int w = threadIdx.x / GS_WAVE;
+    const int lane = lane_id();
+    const uint32_t incl = wave_incl_scan(v);
+    if (lane == GS_WAVE - 1) s_tmp[w] = incl;
+    __syncthreads();
+    uint32_t pre = 0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i)
+        if (i < w) pre += s_tmp[i];
+    __syncthreads();
+    return pre + incl - v;
+}
+
+template <typename K>
+__global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ keys, int64_t n,
+                                                       int begin_bit, int end_bit, int npass,
+                                                       uint32_t* __restrict__ g_hist) {
+    __shared__ uint32_t h[kWaves][kMaxPasses][256];
+    const int w = threadIdx.x / GS_WAVE;
+    for (int i = threadIdx.x; i < kWaves * kMaxPasses * 256; i += kHistThreads)
+        (&h[0][0][0])[i] = 0;
+    __syncthreads();
+    const int64_t stride = (int64_t)gridDim.x * kHistThreads;
+    for (int64_t i = (int64_t)blockIdx.x * kHistThreads + threadIdx.x; i < n; i += stride) {
+        const K k = keys[i];
+        for (int p = 0; p < npass; ++p) {
+            const int shift = begin_bit + 8 * p;
+            const int bits = min(8, end_bit - shift);
+            const uint32_t d = digit_of(k, shift, (1u << bits) - 1u);
+            atomicAdd(&h[w][p][d], 1u);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < npass * 256; i += kHistThreads) {
+        const int p = i / 256, d = i % 256;
+        uint32_t s = 0;
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) s += h[ww][p][d];
+        if (s) atomicAdd(&g_hist[p * 256 + d], s);
+    }
+}
+
+template <typename K, bool IOTA>
+__global__ __launch_bounds__(kSortThreads) void k_onesweep(
+    const K* __restrict__ kin, const uint32_t* __restrict__ vin, K* __restrict__ kout,
+    uint32_t* __restrict__ vout, int64_t n, int shift, int bits,
+    const uint32_t* __restrict__ g_hist_pass, uint64_t* __restrict__ state,
+    uint32_t* __restrict__ ticket, uint32_t epoch) {
+    __shared__ uint32_t s_vid;
+    __shared__ uint32_t s_wcnt[kWaves][256];
+    __shared__ uint32_t s_loff[256];
+    __shared__ uint32_t s_gpos[256];
+    __shared__ uint32_t s_tmp[kWaves];
+    __shared__ K s_keys[kSortPart];
+    __shared__ uint32_t s_vals[kSortPart];
+
+    const int tid = threadIdx.x;
+    const int w = tid / GS_WAVE;
+    const int lane = lane_id();
+    const uint32_t mask = (1u << bits) - 1u;
+
+    if (tid == 0) s_vid = atomicAdd(ticket, 1u);
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) s_wcnt[ww][tid] = 0;
+    __syncthreads();
+    const uint32_t vid = s_vid;
+    const int64_t part_base = (int64_t)vid * kSortPart;
+    const int64_t wave_base = part_base + (int64_t)w * (kSortItems * GS_WAVE);
+
+    K key[kSortItems];
+    uint32_t val[kSortItems];
+    uint32_t rank[kSortItems];
+#pragma unroll
+    for (int it = 0; it < kSortItems; ++it) {
+        const int64_t idx = wave_base + it * GS_WAVE + lane;
+        if (idx < n) {
+            key[it] = kin[idx];
+            val[it] = IOTA ? (uint32_t)idx : vin[idx];
+        } else {
+            key[it] = 0;
+            val[it] = 0;
+        }
+    }
+    const uint64_t lt = lanemask_lt();
+#pragma unroll
+    for (int it = 0; it < kSortItems; ++it) {
+        const int64_t idx = wave_base + it * GS_WAVE + lane;
+        rank[it] = 0;
+        if (idx < n) {
+            const uint32_t d = digit_of(key[it], shift, mask);
+            uint64_t peers = __ballot(1);
+            for (int b = 0; b < bits; ++b) {
+                const bool bit = (d >> b) & 1u;
+                const uint64_t bb = __ballot(bit);
+                peers &= bit ? bb : ~bb;
+            }
+            const uint32_t before = s_wcnt[w][d];
+            rank[it] = before + (uint32_t)__popcll(peers & lt);
+            const int leader = __ffsll((unsigned long long)peers) - 1;
+            if (lane == leader) s_wcnt[w][d] = before + (uint32_t)__popcll(peers);
+        }
+    }
+    __syncthreads();
+
+    // Digit totals and per-wave exclusive offsets (thread = digit).
+    uint32_t tot = 0;
+    {
+        uint32_t c[kWaves];
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) c[ww] = s_wcnt[ww][tid];
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) {
+            s_wcnt[ww][tid] = tot;
+            tot += c[ww];
+        }
+    }
+    // Decoupled look-back for digit `tid` over earlier partitions.
+    uint32_t excl = 0;
+    if (vid == 0) {
+        st_agent(&state[tid], make_desc(epoch, 2u, tot));
+    } else {
+        st_agent(&state[(size_t)vid * 256 + tid], make_desc(epoch, 1u, tot));
+        int64_t j = (int64_t)vid - 1;
+        uint32_t spins = 0;
+        while (true) {
+            const uint64_t s = ld_agent(&state[(size_t)j * 256 + tid]);
+            const uint32_t flag = (uint32_t)(s >> 32) & 3u;
+            if ((uint32_t)(s >> 34) != epoch || flag == 0u) {
+                // bounded wait (see lookback_exclusive): never hang the GPU
+                if (++spins < kLbMaxSpins) {
+                    __builtin_amdgcn_s_sleep(1);
+                    continue;
+                }
+                break;
+            }
+            excl += (uint32_t)s;
+            if (flag == 2u) break;
+            --j;
+        }
+        st_agent(&state[(size_t)vid * 256 + tid], make_desc(epoch, 2u, excl + tot));
+    }
+    const uint32_t loff = block_excl_scan256(tot, s_tmp);
+    const uint32_t gbase = block_excl_scan256(g_hist_pass[tid], s_tmp);
+    s_loff[tid] = loff;
+    s_gpos[tid] = gbase + excl - loff;
+    __syncthreads();
+
+#pragma unroll
+    for (int it = 0; it < kSortItems; ++it) {
+        const int64_t idx = wave_base + it * GS_WAVE + lane;
+        if (idx < n) {
+            const uint32_t d = digit_of(key[it], shift, mask);
+            const uint32_t lp = s_loff[d] + s_wcnt[w][d] + rank[it];
+            if (lp < (uint32_t)kSortPart) {
+                s_keys[lp] = key[it];
+                s_vals[lp] = val[it];
+            }
+        }
+    }
+    __syncthreads();
+    const int64_t cnt64 = n - part_base;
+    const int count = cnt64 < kSortPart ? (int)cnt64 : kSortPart;
+    for (int j = tid; j < count; j += kSortThreads) {
+        const K k = s_keys[j];
+        const uint32_t d = digit_of(k, shift, mask);
+        const uint32_t g = s_gpos[d] + (uint32_t)j;
+        if ((int64_t)g < n) {
+            kout[g] = k;
+            vout[g] = s_vals[j];
+        }
+    }
+}
+
+__global__ void k_fill_u32(uint32_t* p, uint32_t v, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+__global__ void k_iota_u32(uint32_t* p, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = (uint32_t)i;
+}
+
+template <typename K>
+hipError_t sort_impl(K* keys, uint32_t* vals, int64_t n, int begin_bit, int end_bit,
+                     SortTemp& tmp, uint32_t* host_hist, hipStream_t st, int* passes_run,
+                     bool vals_iota, K** keys_final, uint32_t** vals_final) {
+    *passes_run = 0;
+    *keys_final = keys;
+    *vals_final = vals;
+    if (n <= 0) return hipSuccess;
+    if (n >= (int64_t)1 << 32) return hipErrorInvalidValue;
+    const int npass = (end_bit - begin_bit + 7) / 8;
+    if (npass <= 0 || npass > kMaxPasses) return hipErrorInvalidValue;
+    hipError_t e;
+    // clear histograms and tickets in one small launch
+    {
+        const size_t words = (size_t)kMaxPasses * 256 + kMaxPasses;
+        k_fill_u32<<<(unsigned)((words + 255) / 256), 256, 0, st>>>(tmp.hist, 0u, words);
+    }
+    const unsigned hgrid = (unsigned)std::min<int64_t>((n + 4095) / 4096, 1024);
+    k_hist<K><<<hgrid, kHistThreads, 0, st>>>(keys, n, begin_bit, end_bit, npass, tmp.hist);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = hipMemcpyAsync(host_hist, tmp.hist, (size_t)npass * 256 * 4,
+                            hipMemcpyDeviceToHost, st)) != hipSuccess)
+        return e;
+    if ((e = hipStreamSynchronize(st)) != hipSuccess) return e;
+
+    K* kin = keys;
+    uint32_t* vin = vals;
+    K* kalt = static_cast<K*>(tmp.keys_alt);
+    uint32_t* valt = tmp.vals_alt;
+    bool iota_pending = vals_iota;
+    const unsigned grid = (unsigned)((n + kSortPart - 1) / kSortPart);
+    uint32_t* tickets = tmp.hist + (size_t)kMaxPasses * 256;
+    for (int p = 0; p < npass; ++p) {
+        bool trivial = false;
+        for (int d = 0; d < 256; ++d)
+            if (host_hist[p * 256 + d] == (uint32_t)n) trivial = true;
+        if (trivial) continue;
+        const int shift = begin_bit + 8 * p;
+        const int bits = std::min(8, end_bit - shift);
+        const uint32_t epoch = ++tmp.epoch;
+        const bool timed = tmp.pass_events != nullptr && *passes_run < tmp.max_timed_passes;
+        if (timed) (void)hipEventRecord(tmp.pass_events[2 * *passes_run], st);
+        if (iota_pending) {
+            k_onesweep<K, true><<<grid, kSortThreads, 0, st>>>(
+                kin, vin, kalt, valt, n, shift, bits, tmp.hist + p * 256,
+                tmp.state, tickets + p, epoch);
+            iota_pending = false;
+        } else {
+            k_onesweep<K, false><<<grid, kSortThreads, 0, st>>>(
+                kin, vin, kalt, valt, n, shift, bits, tmp.hist + p * 256,
+                tmp.state, tickets + p, epoch);
+        }
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (timed) (void)hipEventRecord(tmp.pass_events[2 * *passes_run + 1], st);
+        std::swap(kin, kalt);
+        std::swap(vin, valt);
+        ++*passes_run;
+    }
+    if (iota_pending) {
+        k_iota_u32<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(vin, (size_t)n);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    *keys_final = kin;
+    *vals_final = vin;
+    return hipSuccess;
+}
+
+}  // namespace
+
+size_t sort_partitions(int64_t n) { return (size_t)((n + kSortPart - 1) / kSortPart); }
+size_t sort_state_bytes(int64_t n) { return sort_partitions(n) * 256 * sizeof(uint64_t); }
+size_t sort_hist_words() { return (size_t)kMaxPasses * 256 + kMaxPasses; }
+
+hipError_t radix_sort_pairs(void* keys, uint32_t* vals, int64_t n, int key_bytes, int begin_bit,
+                            int end_bit, SortTemp& tmp, uint32_t* host_hist, hipStream_t st,
+                            int* passes_run, bool vals_iota, void** keys_final,
+                            uint32_t** vals_final) {
+    if (key_bytes == 4) {
+        uint32_t* kf = nullptr;
+        hipError_t e = sort_impl<uint32_t>(static_cast<uint32_t*>(keys), vals, n, begin_bit,
+                                           end_bit, tmp, host_hist, st, passes_run, vals_iota,
+                                           &kf, vals_final);
+        *keys_final = kf;
+        return e;
+    }
+    if (key_bytes == 8) {
+        uint64_t* kf = nullptr;
+        hipError_t e = sort_impl<uint64_t>(static_cast<uint64_t*>(keys), vals, n, begin_bit,
+                                           end_bit, tmp, host_hist, st, passes_run, vals_iota,
+                                           &kf, vals_final);
+        *keys_final = kf;
+        return e;
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    k_fill_u32<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(p, v, n);
+    return hipGetLastError();
+}
+
+}  // namespace gs

@@ -1,0 +1,333 @@
+// tiles.hip - tile assignment: per-Gaussian tile rectangle, exclusive scan of
+// rectangle areas (decoupled look-back), pair-centric emission with the
+// per-pair Mahalanobis cull and a stable compaction of the kept pairs, and
+// tile-range extraction from the tile-sorted pair list.
+//
+// Reference: src/gsplat_cpu/tile_assign.cpp:60-102 (rectangle: float divide,
+// truncate toward zero, clamp), :121-149 (row-major pairs per Gaussian),
+// :151-290 (constrained minimum of the Mahalanobis distance over the tile
+// rectangle, keep iff num <= det * m2thr), :298-349 (stable compaction);
+// src/gsplat_cpu/sort.cpp:146-165 (tile_ranges, (0,0) for empty tiles).
+// Compiled with -ffp-contract=off: every comparison sees the reference's
+// fp32 values.
+#include "gs_common.h"
+#include "gs_internal.h"
+
+namespace gs {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / GS_WAVE;
+constexpr int kCountItems = 4;
+constexpr int kCountPart = kThreads * kCountItems;   // ranks per scan partition
+constexpr int kEmitItems = 8;
+constexpr int kEmitPart = kThreads * kEmitItems;     // candidates per emit partition
+
+__device__ __forceinline__ float fmin_std(float a, float b) { return (b < a) ? b : a; }
+__device__ __forceinline__ float fmax_std(float a, float b) { return (a < b) ? b : a; }
+
+struct Rect {
+    int x0, x1, y0, y1;
+};
+
+__device__ __forceinline__ Rect tile_rect(float4 r, const TileParams& tp) {
+    const float ts = (float)tp.tile_size;
+    Rect o;
+    o.x0 = max(0, min((int)((r.x - r.z) / ts), tp.tiles_x - 1));
+    o.x1 = max(0, min((int)((r.x + r.z) / ts), tp.tiles_x - 1));
+    o.y0 = max(0, min((int)((r.y - r.w) / ts), tp.tiles_y - 1));
+    o.y1 = max(0, min((int)((r.y + r.w) / ts), tp.tiles_y - 1));
+    return o;
+}
+
+// tile_assign.cpp:151-290, one (Gaussian, tile) pair.
+__device__ __forceinline__ bool pair_keep(float px, float py, float4 cv, int tile_id,
+                                          const TileParams& tp) {
+    const float m2thr = cv.w;
+    if (!(m2thr >= 0.0f)) return false;  // opacity <= floor
+    const float a = cv.x, b = cv.y, c = cv.z;
+    const float det = fmax_std(a * c - b * b, 1e-6f);
+    const float ts = (float)tp.tile_size;
+    const float tx_tile = (float)(tile_id % tp.tiles_x) * ts;
+    const float ty_tile = (float)(tile_id / tp.tiles_x) * ts;
+    const float u_lo = tx_tile - px;
+    const float u_hi = u_lo + ts;
+    const float v_lo = ty_tile - py;
+    const float v_hi = v_lo + ts;
+    const bool x_in = (u_lo <= 0.0f) && (0.0f <= u_hi);
+    const bool y_in = (v_lo <= 0.0f) && (0.0f <= v_hi);
+    const float scaled = det * m2thr;
+    if (x_in && y_in) return true;
+    float m2_v = __builtin_inff(), m2_h = __builtin_inff();
+    if (!x_in) {
+        const float uf = (u_lo > 0.0f) ? u_lo : u_hi;
+        const float a_safe = fmax_std(a, 1e-12f);
+        float vs = (b * uf) / a_safe;
+        vs = fmax_std(v_lo, fmin_std(vs, v_hi));
+        m2_v = c * uf * uf - 2.0f * b * uf * vs + a * vs * vs;
+    }
+    if (!y_in) {
+        const float vf = (v_lo > 0.0f) ? v_lo : v_hi;
+        const float c_safe = fmax_std(c, 1e-12f);
+        float us = (b * vf) / c_safe;
+        us = fmax_std(u_lo, fmin_std(us, u_hi));
+        m2_h = c * us * us - 2.0f * b * us * vf + a * vf * vf;
+    }
+    return fmin_std(m2_v, m2_h) <= scaled;
+}
+
+// Rectangle area per rank, exclusive scan -> offs[r]; last partition writes
+// the total candidate count (saturated to 0xFFFFFFFF on overflow).
+__global__ __launch_bounds__(kThreads) void k_rect_count_scan(const float4* __restrict__ rect,
+                                                              const uint32_t* __restrict__ order,
+                                                              int64_t m, TileParams tp,
+                                                              uint32_t* __restrict__ offs,
+                                                              uint64_t* lb_state,
+                                                              uint32_t* ticket,
+                                                              uint32_t* total_out) {
+    __shared__ uint32_t s_vid;
+    __shared__ uint32_t s_wsum[kCountItems][kWaves];
+    __shared__ uint64_t s_excl;
+    const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
+    if (tid == 0) s_vid = atomicAdd(ticket, 1u);
+    __syncthreads();
+    const uint32_t vid = s_vid;
+    const int64_t base = (int64_t)vid * kCountPart;
+    uint32_t incl[kCountItems], cnt[kCountItems];
+#pragma unroll
+    for (int it = 0; it < kCountItems; ++it) {
+        const int64_t r = base + it * kThreads + tid;
+        uint32_t c = 0;
+        if (r < m) {
+            const uint32_t g = order ? order[r] : (uint32_t)r;
+            const Rect q = tile_rect(rect[g], tp);
+            c = (uint32_t)((q.x1 - q.x0 + 1) * (q.y1 - q.y0 + 1));
+        }
+        cnt[it] = c;
+        incl[it] = wave_incl_scan(c);
+        if (lane == GS_WAVE - 1) s_wsum[it][w] = incl[it];
+    }
+    __syncthreads();
+    uint64_t total = 0;
+    uint64_t my_off[kCountItems];
+#pragma unroll
+    for (int it = 0; it < kCountItems; ++it)
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) {
+            if (ww == w) my_off[it] = total;
+            total += s_wsum[it][ww];
+        }
+    if (w == 0) {
+        const uint64_t ex = lookback_exclusive(lb_state, vid, total);
+        if (lane == 0) {
+            s_excl = ex;
+            if (vid == gridDim.x - 1) {
+                const uint64_t t = ex + total;
+                *total_out = t > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)t;
+            }
+        }
+    }
+    __syncthreads();
+    const uint64_t ex = s_excl;
+#pragma unroll
+    for (int it = 0; it < kCountItems; ++it) {
+        const int64_t r = base + it * kThreads + tid;
+        if (r < m) offs[r] = (uint32_t)(ex + my_off[it] + incl[it] - cnt[it]);
+    }
+}
+
+// Largest r in [lo, hi) with offs[r] <= c (offs ascending, offs[lo] <= c).
+__device__ __forceinline__ int64_t upper_rank(const uint32_t* offs, int64_t lo, int64_t hi,
+                                              uint32_t c) {
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (offs[mid] <= c) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+// Pair-centric emission: candidate c -> (rank r, j-th tile of r's rectangle),
+// cull, stable compaction of kept pairs in candidate order.
+__global__ __launch_bounds__(kThreads) void k_pair_emit(
+    const float4* __restrict__ rect, const float4* __restrict__ cov,
+    const uint32_t* __restrict__ order, const uint32_t* __restrict__ offs, int64_t m,
+    uint32_t p_pre, TileParams tp, uint32_t* __restrict__ pair_tile,
+    uint32_t* __restrict__ pair_id, uint32_t cap, uint64_t* lb_state, uint32_t* ticket,
+    uint32_t* total_out) {
+    __shared__ uint32_t s_vid;
+    __shared__ int64_t s_rlo, s_rhi;
+    __shared__ uint32_t s_off[kEmitPart + 1];
+    __shared__ uint32_t s_g[kEmitPart + 1];
+    __shared__ int32_t s_x0[kEmitPart + 1];
+    __shared__ int32_t s_y0[kEmitPart + 1];
+    __shared__ int32_t s_w[kEmitPart + 1];
+    __shared__ uint32_t s_cnt[kEmitItems][kWaves];
+    __shared__ uint64_t s_excl;
+    const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
+    if (tid == 0) s_vid = atomicAdd(ticket, 1u);
+    __syncthreads();
+    const uint32_t vid = s_vid;
+    const uint64_t c0 = (uint64_t)vid * kEmitPart;
+    const uint64_t c1 = min((uint64_t)p_pre, c0 + kEmitPart);
+    if (tid == 0) {
+        s_rlo = upper_rank(offs, 0, m, (uint32_t)c0);
+        s_rhi = upper_rank(offs, 0, m, (uint32_t)(c1 - 1));
+    }
+    __syncthreads();
+    const int64_t rlo = s_rlo;
+    // every rank owns >= 1 candidate, so nr <= kEmitPart; clamp defensively
+    const int64_t nr = min(s_rhi - s_rlo + 1, (int64_t)kEmitPart + 1);
+    for (int64_t k = tid; k < nr; k += kThreads) {
+        const int64_t r = rlo + k;
+        const uint32_t g = order ? order[r] : (uint32_t)r;
+        const Rect q = tile_rect(rect[g], tp);
+        s_off[k] = offs[r];
+        s_g[k] = g;
+        s_x0[k] = q.x0;
+        s_y0[k] = q.y0;
+        s_w[k] = q.x1 - q.x0 + 1;
+    }
+    __syncthreads();
+
+    bool keep[kEmitItems];
+    uint32_t tile[kEmitItems], gid[kEmitItems];
+    uint64_t bal[kEmitItems];
+#pragma unroll
+    for (int it = 0; it < kEmitItems; ++it) {
+        const uint64_t c = c0 + it * kThreads + tid;
+        keep[it] = false;
+        tile[it] = 0;
+        gid[it] = 0;
+        if (c < c1) {
+            int lo = 0, hi = (int)nr;
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (s_off[mid] <= (uint32_t)c) lo = mid; else hi = mid;
+            }
+            const uint32_t j = (uint32_t)c - s_off[lo];
+            const uint32_t wdt = (uint32_t)s_w[lo];
+            const int t = (s_y0[lo] + (int)(j / wdt)) * tp.tiles_x + s_x0[lo] + (int)(j % wdt);
+            const uint32_t g = s_g[lo];
+            bool k = true;
+            if (tp.cull) {
+                const float4 rr = rect[g];
+                k = pair_keep(rr.x, rr.y, cov[g], t, tp);
+            }
+            keep[it] = k;
+            tile[it] = (uint32_t)t;
+            gid[it] = g;
+        }
+        bal[it] = __ballot(keep[it]);
+        if (lane == 0) s_cnt[it][w] = (uint32_t)__popcll(bal[it]);
+    }
+    __syncthreads();
+    uint32_t total = 0, my_off[kEmitItems];
+#pragma unroll
+    for (int it = 0; it < kEmitItems; ++it)
+#pragma unroll
+        for (int ww = 0; ww < kWaves; ++ww) {
+            if (ww == w) my_off[it] = total;
+            total += s_cnt[it][ww];
+        }
+    if (w == 0) {
+        const uint64_t ex = lookback_exclusive(lb_state, vid, total);
+        if (lane == 0) {
+            s_excl = ex;
+            if (vid == gridDim.x - 1) {
+                const uint64_t t = ex + total;
+                *total_out = t > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)t;
+            }
+        }
+    }
+    __syncthreads();
+    const uint64_t ex = s_excl;
+    const uint64_t ltm = lanemask_lt();
+#pragma unroll
+    for (int it = 0; it < kEmitItems; ++it) {
+        if (!keep[it]) continue;
+        const uint64_t pos = ex + my_off[it] + (uint64_t)__popcll(bal[it] & ltm);
+        if (pos < cap) {
+            pair_tile[pos] = tile[it];
+            pair_id[pos] = gid[it];
+        }
+    }
+}
+
+__global__ void k_tile_ranges(const uint32_t* __restrict__ st, uint32_t p,
+                              uint32_t* __restrict__ ranges) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= p) return;
+    const uint32_t t = st[i];
+    if (i == 0 || st[i - 1] != t) ranges[2 * (size_t)t] = i;
+    if (i == p - 1 || st[i + 1] != t) ranges[2 * (size_t)t + 1] = i + 1;
+}
+
+// key = (tile << 32) | fp32 depth bits of the pair's Gaussian (sort.cpp:180-205).
+__global__ void k_make_keys64(const uint32_t* __restrict__ gid, const uint32_t* __restrict__ tid,
+                              const float* __restrict__ depths, uint32_t p,
+                              uint64_t* __restrict__ keys) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= p) return;
+    keys[i] = ((uint64_t)tid[i] << 32) | (uint64_t)__float_as_uint(depths[gid[i]]);
+}
+
+__global__ void k_tile_ranges64(const uint64_t* __restrict__ keys, uint32_t p,
+                                uint32_t* __restrict__ ranges) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= p) return;
+    const uint32_t t = (uint32_t)(keys[i] >> 32);
+    if (i == 0 || (uint32_t)(keys[i - 1] >> 32) != t) ranges[2 * (size_t)t] = i;
+    if (i == p - 1 || (uint32_t)(keys[i + 1] >> 32) != t) ranges[2 * (size_t)t + 1] = i + 1;
+}
+
+}  // namespace
+
+hipError_t launch_make_keys64(const uint32_t* gid, const uint32_t* tid, const float* depths,
+                              uint32_t p, uint64_t* keys, hipStream_t st) {
+    if (p == 0) return hipSuccess;
+    k_make_keys64<<<(p + 255) / 256, 256, 0, st>>>(gid, tid, depths, p, keys);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_ranges64(const uint64_t* keys, uint32_t p, uint32_t* ranges,
+                                int64_t num_tiles, hipStream_t st) {
+    hipError_t e = launch_fill_u32(ranges, 0u, (size_t)num_tiles * 2, st);
+    if (e != hipSuccess || p == 0) return e;
+    k_tile_ranges64<<<(p + 255) / 256, 256, 0, st>>>(keys, p, ranges);
+    return hipGetLastError();
+}
+
+size_t rect_scan_partitions(int64_t m) { return (size_t)((m + kCountPart - 1) / kCountPart); }
+size_t emit_partitions(uint64_t p_pre) { return (size_t)((p_pre + kEmitPart - 1) / kEmitPart); }
+
+hipError_t launch_rect_count_scan(const float4* rect, const uint32_t* order, int64_t m,
+                                  TileParams tp, uint32_t* offs, uint64_t* lb_state,
+                                  uint32_t* ticket, uint32_t* total_out, hipStream_t st) {
+    if (m <= 0) return hipSuccess;
+    const unsigned grid = (unsigned)rect_scan_partitions(m);
+    k_rect_count_scan<<<grid, kThreads, 0, st>>>(rect, order, m, tp, offs, lb_state, ticket,
+                                                 total_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_pair_emit(const float4* rect, const float4* cov, const uint32_t* order,
+                            const uint32_t* offs, int64_t m, uint32_t p_pre, TileParams tp,
+                            uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
+                            uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
+                            hipStream_t st) {
+    if (p_pre == 0 || m <= 0) return hipSuccess;
+    const unsigned grid = (unsigned)emit_partitions(p_pre);
+    k_pair_emit<<<grid, kThreads, 0, st>>>(rect, cov, order, offs, m, p_pre, tp, pair_tile,
+                                           pair_id, cap, lb_state, ticket, total_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, uint32_t* ranges,
+                              int64_t num_tiles, hipStream_t st) {
+    hipError_t e = launch_fill_u32(ranges, 0u, (size_t)num_tiles * 2, st);
+    if (e != hipSuccess || p == 0) return e;
+    k_tile_ranges<<<(p + 255) / 256, 256, 0, st>>>(sorted_tile, p, ranges);
+    return hipGetLastError();
+}
+
+}  // namespace gs

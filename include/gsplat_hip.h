@@ -1,0 +1,149 @@
+/*
+ * gsplat_hip.h - C ABI of the MI355X (gfx950) Gaussian-splat rasterizer.
+ *
+ * Plain pointers and sizes only; no exceptions cross this boundary. Every
+ * entry point returns GS_OK (0) or a negative GS_E* status, with a message in
+ * gs_last_error() (thread-local). One context = one GPU + one HIP stream;
+ * calls on one context must not overlap (the Python module serialises them
+ * with a mutex, like the reference's render_view_mutex,
+ * render/host/render.cpp:73-75).
+ *
+ * Host-pointer entry points copy their inputs to HBM and their outputs back;
+ * the *_dev variants take device pointers and never touch host memory.
+ */
+#ifndef GSPLAT_HIP_H
+#define GSPLAT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GS_OK 0
+#define GS_E_INVALID -1   /* bad argument (-> std::invalid_argument / ValueError) */
+#define GS_E_DEVICE -2    /* HIP runtime / kernel failure (-> RuntimeError) */
+#define GS_E_CAPACITY -3  /* a size limit of this build was exceeded */
+
+#define GS_OUT_U8 0       /* uint8(clip(rgb,0,1)*255), truncation */
+#define GS_OUT_BF16 1     /* bf16, round to nearest even */
+#define GS_OUT_F32 2
+
+typedef struct gs_ctx gs_ctx;
+
+/* Scene description. Host pointers, read during gs_scene_set only.
+ * Replaces the per-scene caches of render/host/render.cpp:96-118
+ * (cov3d_unique, keyed by pointer, N and scene version). */
+typedef struct gs_scene {
+    const float* means;     /* (n,3) world positions */
+    const float* cov3d;     /* (n,9) row-major 3x3, or (n,6) c00 c01 c02 c11 c12 c22 */
+    int cov3d_stride;       /* 9 or 6 */
+    const float* opacities; /* (n) activated opacity, or NULL (k = 3, no opacity tests) */
+    const float* colors;    /* sh_degree < 0: (n,3) RGB; else (n,(d+1)^2,3) SH coefficients */
+    int sh_degree;          /* -1 (RGB) or 0..3 */
+    int64_t n;
+    uint64_t version;       /* caller's scene version; any change forces a re-upload */
+} gs_scene;
+
+/* One view. Mirrors the argument list of render_clean.render_view
+ * (render/host/render.cpp:263-273) and _gsplat_cpu.render_full
+ * (backends/cpu_cpp/pybind_module.cpp:2071-2091). */
+typedef struct gs_view {
+    float extrinsics[16];   /* world-to-camera 4x4, row-major, R | t in column 3 */
+    float intrinsics[9];    /* 3x3, fx = [0], cx = [2], fy = [4], cy = [5] */
+    int image_height, image_width;
+    int tile_size;          /* 16 or 32 */
+    float min_opacity;
+    float contrib_floor;    /* radius k and per-pair tile cull floor */
+    float mb_contrib_floor; /* microblock cull floor */
+    int cull_disabled;
+    float transmittance_threshold;
+    int max_radius;         /* 0: min(H,W)/2, > 0: explicit, < 0: unlimited */
+    float k_cap;            /* <= 0: uncapped */
+    int use_isoellipse;
+    int out_format;         /* GS_OUT_* */
+    int sh_clamp_hi;        /* SH colour clamp to [0,1] (display) when 1, >= 0 only when 0 */
+} gs_view;
+
+typedef struct gs_stats {
+    int64_t num_visible;    /* M */
+    int64_t num_entries;    /* P, tile-Gaussian pairs after the per-pair cull */
+    int64_t pairs_pre;      /* rectangle pairs before the cull */
+    float ms_project;       /* device time per stage (events), when timing is on */
+    float ms_depth_sort;
+    float ms_tile_assign;
+    float ms_tile_sort;
+    float ms_blend;
+    float ms_total;         /* host wall clock of the whole call */
+} gs_stats;
+
+/* ---- context -------------------------------------------------------- */
+int gs_create(int device, gs_ctx** out);
+void gs_destroy(gs_ctx* ctx);
+const char* gs_last_error(void);
+int gs_set_timing(gs_ctx* ctx, int on);      /* per-stage hipEvent timing */
+int gs_device_info(gs_ctx* ctx, int* num_cus, int* arch_minor);
+
+/* ---- frame ----------------------------------------------------------
+ * gs_scene_set: makes `scene` resident (no-op when pointers, n and version
+ * are unchanged). gs_render: the five stages of render_view
+ * (render/host/render.cpp:263-615): project+SH -> visibility compaction ->
+ * tile assign + pair cull -> tile/depth sort -> microblock cull + blend.
+ * `out` is (H,W,3) of the requested format, host memory unless
+ * out_on_device. M == 0 gives a black image. */
+int gs_scene_set(gs_ctx* ctx, const gs_scene* scene);
+int gs_render(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device, gs_stats* stats);
+
+/* ---- stages on host arrays (parity entry points) ----------------------
+ * gs_project: project_full_fused, src/gsplat_cpu/project.cpp:484-798.
+ * Outputs sized for n; *m_out = M. colors_out is (M,3) RGB (SH evaluated). */
+int gs_project(gs_ctx* ctx, const gs_scene* scene, const gs_view* view,
+               uint8_t* valid_mask, float* means2d, float* covs2d, float* depths,
+               float* radii, float* colors_out, float* opac_out, int64_t* m_out);
+
+/* gs_tile_assign: tile_assign, src/gsplat_cpu/tile_assign.cpp:26-368.
+ * covs2d (m,4) and opac (m) may be NULL (no per-pair cull). Pairs are
+ * Gaussian-major. Writes at most `cap` pairs; *p_out = P, *p_pre_out =
+ * pairs before the cull (cap < P -> GS_E_CAPACITY, nothing written). */
+int gs_tile_assign(gs_ctx* ctx, const float* means2d, const float* radii, int64_t m,
+                   int image_height, int image_width, int tile_size, const float* covs2d,
+                   const float* opac, float contrib_floor, int64_t* gids, int64_t* tids,
+                   int64_t cap, int64_t* p_out, int64_t* p_pre_out);
+
+/* gs_sort_and_bin: sort_and_bin, src/gsplat_cpu/sort.cpp:89-263. Stable by
+ * (tile, fp32 depth bits); tile_ranges (T,2) with (0,0) for empty tiles. */
+int gs_sort_and_bin(gs_ctx* ctx, const int64_t* gids, const int64_t* tids,
+                    const float* depths, int64_t p, int64_t m, int tiles_x, int tiles_y,
+                    int64_t* sorted_ids, int64_t* tile_ranges);
+
+/* gs_cull_and_blend: cull_and_blend, src/gsplat_cpu/cull_and_blend.cpp:678-838.
+ * Writes (H,W,3) in view->out_format; only tile_size, image size, floors,
+ * cull_disabled, transmittance_threshold and out_format of `view` are read. */
+int gs_cull_and_blend(gs_ctx* ctx, const float* means2d, const float* covs2d,
+                      const float* colors, const float* opac, const int64_t* sorted_ids,
+                      const int64_t* tile_ranges, int64_t m, int64_t p, const gs_view* view,
+                      void* image_out);
+
+/* ---- standalone tile/depth key sort (device pointers) -----------------
+ * Stable LSD radix sort of (u64 key, u32 value) pairs by key bits
+ * [begin_bit, end_bit), in place. Replaces the per-tile stable radix of
+ * src/gsplat_cpu/sort.cpp:24-85 / render/kernels/dataflow/sort_radix_tile.cpp
+ * for a whole (tile<<32 | depth_bits) key array. *passes_out = digit passes
+ * executed (passes whose digit is constant are skipped). */
+int gs_sort_pairs_u64_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n,
+                          int begin_bit, int end_bit, int* passes_out);
+/* Average device time (ms) of each onesweep pass kernel of the last
+ * gs_sort_pairs_u64_dev call when timing is on; returns the pass count. */
+int gs_last_sort_pass_ms(gs_ctx* ctx, float* ms, int max_passes);
+
+/* ---- device memory helpers (for callers without a GPU framework) ------ */
+int gs_dev_alloc(gs_ctx* ctx, int64_t bytes, void** ptr);
+int gs_dev_free(gs_ctx* ctx, void* ptr);
+int gs_memcpy_h2d(gs_ctx* ctx, void* dst, const void* src, int64_t bytes);
+int gs_memcpy_d2h(gs_ctx* ctx, void* dst, const void* src, int64_t bytes);
+int gs_sync(gs_ctx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
