@@ -1,0 +1,219 @@
+"""Benchmark: forward render of the 6M-Gaussian scene (SH degree 3, 1237x822,
+16x16 tiles, 64-view orbit) on one MI355X, plus the standalone 50M-key
+tile/depth radix sort, with roofline figures and the CPU baseline.
+
+Contract: `python bench.py --gpus N --steps K --warmup W` prints ONE JSON line.
+A step is one frame: the whole five-stage pipeline of one orbit view, from the
+HBM-resident scene to a bf16 image in HBM (inputs resident before timing).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+FP32_PEAK_TFLOPS = 157.3     # MI355X FP32 vector peak
+BLEND_FLOPS_PER_EVAL = 20    # per pixel x Gaussian evaluation
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--views", type=int, default=64)
+    ap.add_argument("--n", type=int, default=6_000_000)
+    ap.add_argument("--sort-keys", type=int, default=50_000_000)
+    ap.add_argument("--no-sort", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-frames", type=int, default=4)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    return ap.parse_args()
+
+
+def bench_frames(args):
+    from gsplat_tt_amd import _lib as L
+    from gsplat_tt_amd import scenes
+
+    t = time.time()
+    scene, cams = scenes.config3(n=args.n, views=args.views)
+    cov = scenes.cov3d(scene.scales, scene.quats)
+    log(f"scene generated in {time.time() - t:.1f}s (N={scene.n})")
+    ctx = L.Context(0, timing=True)
+    cus, _ = ctx.device_info()
+    t = time.time()
+    ctx.set_scene(scene.means, cov, scene.opacities, scene.sh, sh_degree=3)
+    log(f"scene resident in HBM in {time.time() - t:.1f}s ({cus} CUs)")
+    H, W = cams[0].height, cams[0].width
+    out = ctx.dev_alloc(H * W * 3 * 2)
+    views = [L.make_view(c.w2c, c.K, H, W, tile_size=16, output="bf16") for c in cams]
+
+    for i in range(args.warmup):
+        ctx.render_dev(views[i % len(views)], out)
+    ctx._L.gs_sync(ctx.handle)
+    log(f"warmup {args.warmup} frames done")
+    stats = []
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        stats.append(ctx.render_dev(views[i % len(views)], out))
+    ctx._L.gs_sync(ctx.handle)
+    dt = time.perf_counter() - t0
+    ctx.dev_free(out)
+    log(f"timed {args.steps} frames in {dt:.3f}s")
+    return ctx, scene, cov, cams, stats, dt
+
+
+def stage_summary(scene, stats):
+    keys = ("ms_project", "ms_depth_sort", "ms_tile_assign", "ms_tile_sort", "ms_blend",
+            "ms_total")
+    avg = {k: float(np.mean([s[k] for s in stats])) for k in keys}
+    M = float(np.mean([s["num_visible"] for s in stats]))
+    P = float(np.mean([s["num_entries"] for s in stats]))
+    Ppre = float(np.mean([s["pairs_pre"] for s in stats]))
+    evals = float(np.mean([s["blend_evals"] for s in stats]))
+    N = scene.n
+    # algorithmic bytes: projection reads mean 12 + cov 24 + opacity 4 +
+    # SH 192 (+ k 4) per Gaussian, writes 84 B per visible Gaussian.
+    proj_bytes = N * (12 + 24 + 4 + 4) + M * (192 + 8 + 84)
+    blend_flops = evals * BLEND_FLOPS_PER_EVAL
+    st = {
+        "N": N, "M_avg": M, "pairs_avg": P, "pairs_pre_avg": Ppre, "blend_evals_avg": evals,
+        "ms": {k[3:]: round(v, 4) for k, v in avg.items()},
+        "project_gbs": proj_bytes / (avg["ms_project"] * 1e-3) / 1e9,
+        "blend_tflops": blend_flops / (avg["ms_blend"] * 1e-3) / 1e12,
+    }
+    return st, avg, blend_flops
+
+
+def bench_sort(ctx, n):
+    from gsplat_tt_amd import scenes
+
+    t = time.time()
+    keys, vals = scenes.config4_keys(n=n)
+    log(f"sort keys generated in {time.time() - t:.1f}s")
+    dk, dv = ctx.dev_alloc(n * 8), ctx.dev_alloc(n * 4)
+    L = ctx._L
+    times, passes, pass_ms = [], 0, []
+    for rep in range(4):
+        ctx.h2d(dk, keys)   # restore the unsorted input, outside the timed region
+        ctx.h2d(dv, vals)
+        L.gs_sync(ctx.handle)
+        t0 = time.perf_counter()
+        passes = ctx.sort_pairs_u64_dev(dk, dv, n, 0, 45)
+        times.append(time.perf_counter() - t0)
+        pass_ms.append(ctx.last_sort_pass_ms())
+    # spot-check: sortedness, tile ranges contiguity and permutation checksum
+    ko = np.empty(n, np.uint64)
+    vo = np.empty(n, np.uint32)
+    ctx.d2h(ko, dk)
+    ctx.d2h(vo, dv)
+    ok = bool(np.all(ko[1:] >= ko[:-1])) and int(vo.astype(np.uint64).sum()) == n * (n - 1) // 2
+    ok = ok and bool(np.array_equal(keys[vo[: 1 << 20]], ko[: 1 << 20]))
+    for p in (dk, dv):
+        ctx.dev_free(p)
+    best = min(times[1:]) if len(times) > 1 else times[0]
+    kernel_ms = float(np.mean([sum(p) for p in pass_ms[1:]])) if len(pass_ms) > 1 else float(sum(pass_ms[0]))
+    per_pass_ms = float(np.mean([np.mean(p) for p in pass_ms[1:] if p])) if len(pass_ms) > 1 else 0.0
+    bytes_total = n * (24 * passes + 8)
+    return {
+        "keys": n, "tiles": 5000, "zipf_s": 1.1, "passes": passes, "ok": ok,
+        "wall_ms": round(best * 1e3, 3), "kernel_ms": round(kernel_ms, 3),
+        "gkeys_per_s": round(n / best / 1e9, 3),
+        "gkeys_per_s_kernels": round(n / (kernel_ms * 1e-3) / 1e9, 3) if kernel_ms > 0 else None,
+        "roofline": {"bound": "hbm", "achieved": round(n * 24 / (per_pass_ms * 1e-3) / 1e9, 1)
+                     if per_pass_ms > 0 else None, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(n * 24 / (per_pass_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+                     if per_pass_ms > 0 else None, "traffic": None,
+                     "bytes_model": f"keys*(24*passes+8) = {bytes_total}"},
+    }
+
+
+def cpu_baseline(scene, cov, cams, frames, threads):
+    """The reference's own CPU renderer (_gsplat_cpu.render_full, compiled from its
+    sources into oracle/_ref) on a bounded sample of the same workload; SH colour
+    evaluated on the CPU first (oracle, single thread) and included."""
+    os.environ["GSPLAT_TT_NUM_THREADS"] = str(threads)
+    from oracle import oracle as O
+
+    R = O.ref_module()
+    kind = "reference"
+    times = []
+    for i in range(frames + 1):
+        cam = cams[(i * 7) % len(cams)]
+        t0 = time.perf_counter()
+        rgb = O.sh_rgb(scene.means, scene.sh, 3, cam.w2c)
+        if R is not None:
+            R.render_full(scene.means, cov, scene.opacities, rgb, cam.w2c, cam.K, cam.height,
+                          cam.width, tile_size=16)
+        else:
+            kind = "port"
+            O.render_full(scene.means, cov, scene.opacities, rgb, cam.w2c, cam.K, cam.height,
+                          cam.width, tile_size=16)
+        dt = time.perf_counter() - t0
+        if i > 0:
+            times.append(dt)
+        log(f"cpu frame {i}: {dt:.2f}s")
+    med = float(np.median(times))
+    return {"value": round(1.0 / med, 4), "unit": "frames/s", "cores": threads if kind == "reference" else 1,
+            "kind": kind,
+            "sample": f"{frames} orbit views of the 6M-Gaussian scene after 1 warm-up, median "
+                      f"{med * 1e3:.0f} ms/frame (SH eval + render_full, 16x16 tiles)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); multi-GPU "
+              "sharding is not part of this build", file=sys.stderr)
+        sys.exit(2)
+    ctx, scene, cov, cams, stats, dt = bench_frames(args)
+    st, avg, blend_flops = stage_summary(scene, stats)
+    fps = args.steps / dt
+    log(f"{fps:.1f} frames/s; stages {st['ms']}")
+    blend_ms = avg["ms_blend"]
+    stage_ms = {k: v for k, v in st["ms"].items() if k != "total"}
+    dominant = max(stage_ms, key=stage_ms.get)
+    roof = {"kernel": "k_blend (cull + blend)", "bound": "valu",
+            "achieved": round(blend_flops / (blend_ms * 1e-3) / 1e12, 3),
+            "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(blend_flops / (blend_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4),
+            "traffic": None, "dominant_stage": dominant}
+    res = {
+        "metric": "frames/sec @6M Gaussians 1237x822; sort Gkeys/s; blend frac of FP32 peak",
+        "value": round(fps, 3), "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "forward render, 6M Gaussians (slab+shell), SH degree 3, "
+                               "1237x822, 16x16 tiles, 64-view orbit r=4m h=1m fx=fy=1100, "
+                               "bf16 out", "global_batch": 1, "seq_len": 0,
+                   "parallelism": "single GPU", "n_gaussians": scene.n, "views": len(cams)},
+        "stages": st,
+        "roofline": roof,
+    }
+    if not args.no_sort:
+        res["sort"] = bench_sort(ctx, args.sort_keys)
+        log(f"sort: {res['sort']}")
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(scene, cov, cams, args.cpu_frames, args.cpu_threads)
+    else:
+        res["cpu_baseline"] = None
+    ctx.close()
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

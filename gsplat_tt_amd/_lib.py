@@ -49,7 +49,7 @@ class GsStats(ctypes.Structure):
                 ("pairs_pre", ctypes.c_int64), ("ms_project", ctypes.c_float),
                 ("ms_depth_sort", ctypes.c_float), ("ms_tile_assign", ctypes.c_float),
                 ("ms_tile_sort", ctypes.c_float), ("ms_blend", ctypes.c_float),
-                ("ms_total", ctypes.c_float)]
+                ("ms_total", ctypes.c_float), ("blend_evals", ctypes.c_int64)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}

@@ -99,6 +99,9 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
 
     float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
     bool doneA = emptyA, doneB = emptyB;
+    const uint32_t npixA = emptyA ? 0u : (uint32_t)((pxEA - pxA) * (pyE - py0));
+    const uint32_t npixB = emptyB ? 0u : (uint32_t)((pxEB - pxB) * (pyE - py0));
+    uint64_t evals = 0;
     uint32_t cntA = 0, cntB = 0;
 
     const uint32_t start = ranges[2 * tile], end = ranges[2 * tile + 1];
@@ -206,6 +209,7 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
                     T = T * (1.0f - al);
                 }
             }
+            evals += (jA >= 0 ? npixA : 0u) + (jB >= 0 ? npixB : 0u);
             bool chkA = false, chkB = false;
             if (jA >= 0) {
                 mA &= mA - 1;
@@ -233,6 +237,8 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
         __syncthreads();
     }
 
+    if (bp.evals != nullptr && lane == 0 && evals != 0)
+        atomicAdd(bp.evals, (unsigned long long)evals);
     if (!pix_valid) return;
     const size_t o = ((size_t)(py0 + pi) * bp.width + (size_t)(px_start + pj)) * 3;
     if (OUT == 2) {

@@ -474,9 +474,13 @@ struct gs_ctx {
         b_ranges.ensure((size_t)T * 8);
         HIPCHK(gs::launch_tile_ranges(static_cast<uint32_t*>(tiles_sorted), P,
                                       b_ranges.as<uint32_t>(), T, st));
-        record(4);
         gs::BlendParams bp{tiles_x, tiles_y, ts, H, W, v->cull_disabled ? 1 : 0,
-                           v->transmittance_threshold, v->out_format};
+                           v->transmittance_threshold, v->out_format, nullptr};
+        if (timing) {
+            HIPCHK(gs::launch_fill_u32(b_cnt.as<uint32_t>() + 16, 0u, 2, st));
+            bp.evals = reinterpret_cast<unsigned long long*>(b_cnt.as<uint32_t>() + 16);
+        }
+        record(4);
         HIPCHK(gs::launch_blend(b_brec.as<float4>(), ids_sorted, b_ranges.as<uint32_t>(), bp,
                                 dout, st));
         record(5);
@@ -500,7 +504,13 @@ struct gs_ctx {
     void finish(void* out, void* dout, bool out_dev, size_t bytes, gs_stats* stats, gs_stats s,
                 std::chrono::steady_clock::time_point t0) {
         if (!out_dev) HIPCHK(hipMemcpyAsync(out, dout, bytes, hipMemcpyDeviceToHost, st));
+        if (timing) HIPCHK(hipMemcpyAsync(h_pin + 32, b_cnt.as<uint32_t>() + 16, 8, hipMemcpyDeviceToHost, st));
         sync();
+        if (timing && s.num_entries > 0) {
+            uint64_t e;
+            std::memcpy(&e, h_pin + 32, 8);
+            s.blend_evals = (int64_t)e;
+        }
         s.ms_total = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() - t0)
                          .count();
         if (stats) *stats = s;
@@ -778,7 +788,7 @@ int gs_cull_and_blend(gs_ctx* ctx, const float* means2d, const float* covs2d,
         const size_t bytes = (size_t)H * W * 3 * ebytes;
         ctx->b_out.ensure(bytes);
         gs::BlendParams bp{tiles_x, tiles_y, ts, H, W, view->cull_disabled ? 1 : 0,
-                           view->transmittance_threshold, view->out_format};
+                           view->transmittance_threshold, view->out_format, nullptr};
         HIPCHK(gs::launch_blend(ctx->b_brec.as<float4>(), ctx->b_pair_id.as<uint32_t>(),
                                 ctx->b_ranges.as<uint32_t>(), bp, ctx->b_out.p, ctx->st));
         HIPCHK(hipMemcpyAsync(image_out, ctx->b_out.p, bytes, hipMemcpyDeviceToHost, ctx->st));

@@ -113,6 +113,7 @@ struct BlendParams {
     int cull_disabled;
     float thr;
     int out_format;    // 0 u8, 1 bf16, 2 f32
+    unsigned long long* evals;  // optional: += pixel-Gaussian evaluations blended
 };
 hipError_t launch_blend(const float4* brec, const uint32_t* sorted_id, const uint32_t* ranges,
                         BlendParams bp, void* out, hipStream_t st);

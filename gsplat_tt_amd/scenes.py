@@ -71,6 +71,34 @@ def look_at_w2c(eye, target, up=(0.0, -1.0, 0.0)) -> np.ndarray:
     return w2c.astype(np.float32)
 
 
+def cov3d(scales: np.ndarray, quats: np.ndarray) -> np.ndarray:
+    """Sigma = (R(q) diag(s)) (R(q) diag(s))^T, (N, 9) row-major float32, with the
+    reference's operation order (types.h:68-97; quaternion wxyz used as given).
+    numpy float32 ufuncs round every operation, so this equals the reference's
+    -ffp-contract=off result bit for bit."""
+    s = np.ascontiguousarray(scales, np.float32)
+    q = np.ascontiguousarray(quats, np.float32)
+    q0, q1, q2, q3 = q[:, 0], q[:, 1], q[:, 2], q[:, 3]
+    two, one = np.float32(2.0), np.float32(1.0)
+    r = np.empty((s.shape[0], 3, 3), np.float32)
+    r[:, 0, 0] = one - two * (q2 * q2 + q3 * q3)
+    r[:, 0, 1] = two * (q1 * q2 - q0 * q3)
+    r[:, 0, 2] = two * (q1 * q3 + q0 * q2)
+    r[:, 1, 0] = two * (q1 * q2 + q0 * q3)
+    r[:, 1, 1] = one - two * (q1 * q1 + q3 * q3)
+    r[:, 1, 2] = two * (q2 * q3 - q0 * q1)
+    r[:, 2, 0] = two * (q1 * q3 - q0 * q2)
+    r[:, 2, 1] = two * (q2 * q3 + q0 * q1)
+    r[:, 2, 2] = one - two * (q1 * q1 + q2 * q2)
+    r *= s[:, None, :]
+    out = np.empty((s.shape[0], 3, 3), np.float32)
+    for a in range(3):
+        for b in range(3):
+            out[:, a, b] = (r[:, a, 0] * r[:, b, 0] + r[:, a, 1] * r[:, b, 1]) + \
+                r[:, a, 2] * r[:, b, 2]
+    return out.reshape(-1, 9)
+
+
 def config1(seed: int = 1, n: int = 100_000):
     """100K Gaussians, 640x480, pinhole fx=fy=500 at the image centre, camera at
     the origin looking +z, RGB colours."""
@@ -89,11 +117,11 @@ def config1(seed: int = 1, n: int = 100_000):
 
 def _sh_coeffs(rng, n, degree):
     K = (degree + 1) ** 2
-    sh = np.empty((n, K, 3), np.float32)
-    sh[:, 0, :] = rng.uniform(0, 1, (n, 3))
-    if K > 1:
-        sh[:, 1:, :] = rng.normal(0, 0.1, (n, K - 1, 3))
-    return sh
+    dc = rng.random((n, 3), dtype=np.float32)
+    sh = rng.standard_normal((n, K * 3), dtype=np.float32)  # one contiguous draw
+    sh *= np.float32(0.1)
+    sh[:, :3] = dc
+    return sh.reshape(n, K, 3)
 
 
 def config2(seed: int = 2, n: int = 1_000_000, degree: int = 3):
@@ -117,30 +145,34 @@ def config2(seed: int = 2, n: int = 1_000_000, degree: int = 3):
 
 
 def config3(seed: int = 3, n: int = 6_000_000, degree: int = 3, views: int = 64,
-            slab_frac: float = 0.6):
+            slab_frac: float = 0.8, slab_half: float = 3.5, shell_r=(4.5, 6.5)):
     """Scene-scale cloud: a dense ground-plane slab plus a surrounding shell,
     heavy-tailed log-scales (98% N(-5,1), 2% N(-2,0.5)), SH degree 3, rendered
     at 1237x822 over a 64-view orbit (radius 4 m, 1 m above the centroid,
-    fx=fy=1100). World up is -y (OpenCV-style world)."""
+    fx=fy=1100). World up is -y (OpenCV-style world). The slab is
+    x,z ~ U[-slab_half, slab_half], y ~ N(0, 0.05); the shell is the upper
+    hemisphere at radius ~ U[shell_r]."""
     rng = np.random.default_rng(seed)
+    f32 = np.float32
     n_slab = int(n * slab_frac)
     n_shell = n - n_slab
-    slab = np.stack([rng.uniform(-6, 6, n_slab), rng.normal(0.0, 0.05, n_slab),
-                     rng.uniform(-6, 6, n_slab)], 1)
-    d = rng.standard_normal((n_shell, 3))
+    means = np.empty((n, 3), f32)
+    means[:n_slab, 0] = rng.uniform(-slab_half, slab_half, n_slab)
+    means[:n_slab, 1] = rng.standard_normal(n_slab, dtype=f32) * f32(0.05)
+    means[:n_slab, 2] = rng.uniform(-slab_half, slab_half, n_slab)
+    d = rng.standard_normal((n_shell, 3), dtype=f32)
     d /= np.linalg.norm(d, axis=1, keepdims=True)
     d[:, 1] = -np.abs(d[:, 1])  # upper hemisphere (world up is -y)
-    rad = rng.uniform(7.0, 9.0, n_shell)
-    shell = d * rad[:, None]
-    means = np.concatenate([slab, shell], 0).astype(np.float32)
-    perm = rng.permutation(n)
-    means = means[perm]
-    ls = rng.normal(-5.0, 1.0, (n, 3))
-    big = rng.uniform(0, 1, n) < 0.02
-    ls[big] = rng.normal(-2.0, 0.5, (int(big.sum()), 3))
-    scales = np.exp(ls).astype(np.float32)
-    quats = _unit_quats(rng, n)
-    opac = _sigmoid(rng.normal(0, 2.0, n)).astype(np.float32)
+    d *= rng.uniform(shell_r[0], shell_r[1], n_shell).astype(f32)[:, None]
+    means[n_slab:] = d
+    means = means[rng.permutation(n)]
+    ls = rng.standard_normal((n, 3), dtype=f32) + f32(-5.0)
+    big = rng.random(n, dtype=f32) < f32(0.02)
+    ls[big] = rng.standard_normal((int(big.sum()), 3), dtype=f32) * f32(0.5) + f32(-2.0)
+    scales = np.exp(ls)
+    q = rng.standard_normal((n, 4), dtype=f32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    opac = (1.0 / (1.0 + np.exp(-2.0 * rng.standard_normal(n, dtype=f32)))).astype(f32)
     sh = _sh_coeffs(rng, n, degree)
     centroid = np.zeros(3)
     cams = []
@@ -149,9 +181,10 @@ def config3(seed: int = 3, n: int = 6_000_000, degree: int = 3, views: int = 64,
         eye = centroid + np.array([4.0 * math.cos(a), -1.0, 4.0 * math.sin(a)])
         cams.append(Camera(look_at_w2c(eye, centroid), intrinsics(1100, 1100, 618.5, 411.0),
                            822, 1237))
-    scene = Scene(means, scales, quats, opac, None, sh, degree,
+    scene = Scene(means, scales, q, opac, None, sh, degree,
                   dict(config=3, seed=seed, n=n, slab_frac=slab_frac,
-                       slab="x,z~U[-6,6], y~N(0,0.05)", shell="r~U[7,9], upper hemisphere"))
+                       slab=f"x,z~U[-{slab_half},{slab_half}], y~N(0,0.05)",
+                       shell=f"r~U[{shell_r[0]},{shell_r[1]}], upper hemisphere"))
     return scene, cams
 
 

@@ -75,6 +75,7 @@ typedef struct gs_stats {
     float ms_tile_sort;
     float ms_blend;
     float ms_total;         /* host wall clock of the whole call */
+    int64_t blend_evals;    /* pixel x Gaussian evaluations blended (timing on) */
 } gs_stats;
 
 /* ---- context -------------------------------------------------------- */
