@@ -84,6 +84,8 @@ def stage_summary(scene, stats):
     P = float(np.mean([s["num_entries"] for s in stats]))
     Ppre = float(np.mean([s["pairs_pre"] for s in stats]))
     evals = float(np.mean([s["blend_evals"] for s in stats]))
+    diag = {k: float(np.mean([s[k] for s in stats])) for k in ("blend_batches", "blend_iters",
+                                                                 "blend_kept", "blend_max_iters")}
     N = scene.n
     # algorithmic bytes: projection reads mean 12 + cov 24 + opacity 4 +
     # SH 192 (+ k 4) per Gaussian, writes 84 B per visible Gaussian.
@@ -91,6 +93,7 @@ def stage_summary(scene, stats):
     blend_flops = evals * BLEND_FLOPS_PER_EVAL
     st = {
         "N": N, "M_avg": M, "pairs_avg": P, "pairs_pre_avg": Ppre, "blend_evals_avg": evals,
+        "blend_diag": diag,
         "ms": {k[3:]: round(v, 4) for k, v in avg.items()},
         "project_gbs": proj_bytes / (avg["ms_project"] * 1e-3) / 1e9,
         "blend_tflops": blend_flops / (avg["ms_blend"] * 1e-3) / 1e12,

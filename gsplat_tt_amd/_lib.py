@@ -22,7 +22,7 @@ EXPORTED = (
     "gs_create", "gs_destroy", "gs_last_error", "gs_set_timing", "gs_device_info",
     "gs_scene_set", "gs_render", "gs_project", "gs_tile_assign", "gs_sort_and_bin",
     "gs_cull_and_blend", "gs_sort_pairs_u64_dev", "gs_last_sort_pass_ms", "gs_dev_alloc",
-    "gs_dev_free", "gs_memcpy_h2d", "gs_memcpy_d2h", "gs_sync",
+    "gs_dev_free", "gs_memcpy_h2d", "gs_memcpy_d2h", "gs_memcpy_d2d", "gs_sync",
 )
 
 
@@ -49,7 +49,9 @@ class GsStats(ctypes.Structure):
                 ("pairs_pre", ctypes.c_int64), ("ms_project", ctypes.c_float),
                 ("ms_depth_sort", ctypes.c_float), ("ms_tile_assign", ctypes.c_float),
                 ("ms_tile_sort", ctypes.c_float), ("ms_blend", ctypes.c_float),
-                ("ms_total", ctypes.c_float), ("blend_evals", ctypes.c_int64)]
+                ("ms_total", ctypes.c_float), ("blend_evals", ctypes.c_int64),
+                ("blend_batches", ctypes.c_int64), ("blend_iters", ctypes.c_int64),
+                ("blend_kept", ctypes.c_int64), ("blend_max_iters", ctypes.c_int64)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
@@ -272,6 +274,10 @@ class Context:
         _check(self._L.gs_memcpy_d2h(self._c, _ptr(arr), ctypes.c_void_p(src),
                                      ctypes.c_int64(arr.nbytes)))
         return arr
+
+    def d2d(self, dst: int, src: int, nbytes: int):
+        _check(self._L.gs_memcpy_d2d(self._c, ctypes.c_void_p(dst), ctypes.c_void_p(src),
+                                     ctypes.c_int64(nbytes)))
 
     def sort_pairs_u64_dev(self, keys_ptr: int, vals_ptr: int, n: int, begin_bit=0, end_bit=64):
         passes = ctypes.c_int()

@@ -7,12 +7,12 @@
 // lanes 32-63 microblock B, lane = row*8 + column inside the microblock.
 //
 // Per batch of 32 depth-ordered tile entries the wave
-//   1. loads the 48-byte records (each half loads the same 32),
+//   1. loads the 48-byte records (lane q and lane q+32 hold entry q),
 //   2. evaluates the constrained-minimum microblock cull for (entry, own
 //      microblock) -> a 64-bit ballot = both halves' kept masks,
-//   3. stages the blend parameters of the 32 entries in LDS,
-//   4. walks each half's kept mask in order, both halves in lockstep, with
-//      transmittance and colour held in VGPRs.
+//   3. walks the union of the two kept masks in depth order: the entry's
+//      parameters are read into SGPRs (v_readlane), the halves that keep it
+//      blend it, transmittance and colour stay in VGPRs.
 // Full microblocks follow the reference's AVX2 arithmetic exactly (degree-4
 // exp, power clamp [-30,0], T -= alpha*T, early-out test every 4 kept entries);
 // image-edge microblocks follow its scalar rule (exp, T *= 1-alpha, test after
@@ -60,7 +60,6 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
                                                    BlendParams bp, void* __restrict__ out) {
     constexpr int BX = TS / 16;  // 16-pixel band columns per tile
     constexpr int BY = TS / 4;   // 4-row bands per tile
-    __shared__ float4 s_p[32][3];
 
     const int band = blockIdx.x % (BX * BY);
     const int tile = blockIdx.x / (BX * BY);
@@ -101,7 +100,7 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
     bool doneA = emptyA, doneB = emptyB;
     const uint32_t npixA = emptyA ? 0u : (uint32_t)((pxEA - pxA) * (pyE - py0));
     const uint32_t npixB = emptyB ? 0u : (uint32_t)((pxEB - pxB) * (pyE - py0));
-    uint64_t evals = 0;
+    uint64_t evals = 0, n_batch = 0, n_iter = 0, n_kept = 0;
     uint32_t cntA = 0, cntB = 0;
 
     const uint32_t start = ranges[2 * tile], end = ranges[2 * tile + 1];
@@ -158,23 +157,40 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
             }
         }
         const uint64_t mask = __ballot(keep);
-        if (h == 0 && has) {
-            s_p[q][0] = make_float4(r0.x, r0.y, -0.5f * r1.x, -r1.y);
-            s_p[q][1] = make_float4(-0.5f * r1.z, r2.x, r2.y, r2.z);
-            s_p[q][2] = make_float4(r2.w, r1.x, r1.y, r1.z);
-        }
-        __syncthreads();
-        uint32_t mA = (uint32_t)mask, mB = (uint32_t)(mask >> 32);
-        while (mA | mB) {
-            const int jA = mA ? (__ffs(mA) - 1) : -1;
-            const int jB = mB ? (__ffs(mB) - 1) : -1;
-            const int j = h ? jB : jA;
-            if (j >= 0) {
-                const float4 p0 = s_p[j][0];
-                const float4 p1 = s_p[j][1];
-                const float4 p2 = s_p[j][2];
-                const float mx = p0.x, my = p0.y, A = p0.z, B = p0.w;
-                const float C = p1.x, op = p1.y, col_r = p1.z, col_g = p1.w, col_b = p2.x;
+        ++n_batch;
+        n_kept += (uint64_t)__popcll(mask);
+        // Power coefficients of the AVX2 path (cull_and_blend.cpp:198-200),
+        // computed once per entry in its own lane.
+        const float qA = -0.5f * r1.x, qB = -r1.y, qC = -0.5f * r1.z;
+        // Walk the union of both halves' kept entries in depth order; the
+        // entry's parameters are wave-uniform (SGPRs), a half that does not
+        // keep the entry (or is done) is masked off.
+        uint32_t mA = __builtin_amdgcn_readfirstlane((uint32_t)mask);
+        uint32_t mB = __builtin_amdgcn_readfirstlane((uint32_t)(mask >> 32));
+        uint32_t uni = mA | mB;
+        while (uni) {
+            const int j = __builtin_ctz(uni);
+            uni &= uni - 1;
+            const bool inA = (mA >> j) & 1u, inB = (mB >> j) & 1u;
+            const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r0.x), j));
+            const float my = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r0.y), j));
+            const float op = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r2.x), j));
+            const float col_r = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r2.y), j));
+            const float col_g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r2.z), j));
+            const float col_b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r2.w), j));
+            // v_readlane reads lane j whatever EXEC is, so every read happens
+            // here, in wave-uniform control flow, before the per-half branch.
+            const float A = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qA), j));
+            const float B = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qB), j));
+            const float C = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qC), j));
+            float ci_a = 0.0f, ci_b = 0.0f, ci_c = 0.0f;
+            if (!(fullA && fullB)) {  // image-edge band: scalar-rule parameters
+                ci_a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r1.x), j));
+                ci_b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r1.y), j));
+                ci_c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r1.z), j));
+            }
+            const bool runA = inA && !doneA, runB = inB && !doneB;
+            if (h ? runB : runA) {
                 if (full) {
                     const float px_base = pxs - mx;
                     const float dx = px_base + offx;
@@ -195,12 +211,11 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
                     cb = __builtin_fmaf(at, col_b, cb);
                     T = T - at;
                 } else if (pix_valid) {
-                    const float ci_a = p2.y, ci_b = p2.z, ci_c = p2.w;
                     const float dx = pxc - mx;
                     const float dy = pyc - my;
                     const float power =
                         -0.5f * (ci_a * dx * dx + 2.0f * ci_b * dx * dy + ci_c * dy * dy);
-                    const float gw = (float)exp((double)fmin_std(power, 0.0f));
+                    const float gw = expf(fmin_std(power, 0.0f));
                     const float al = fmin_std(op * gw, 0.99f);
                     const float at = al * T;
                     cr += at * col_r;
@@ -209,36 +224,37 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
                     T = T * (1.0f - al);
                 }
             }
-            evals += (jA >= 0 ? npixA : 0u) + (jB >= 0 ? npixB : 0u);
+            evals += (runA ? npixA : 0u) + (runB ? npixB : 0u);
+            ++n_iter;
             bool chkA = false, chkB = false;
-            if (jA >= 0) {
-                mA &= mA - 1;
+            if (runA) {
                 ++cntA;
                 chkA = fullA ? ((cntA & 3u) == 0u) : true;
             }
-            if (jB >= 0) {
-                mB &= mB - 1;
+            if (runB) {
                 ++cntB;
                 chkB = fullB ? ((cntB & 3u) == 0u) : true;
             }
             if (chkA || chkB) {
-                float t = pix_valid ? T : 0.0f;
-                t = fmax_std(t, __shfl_xor(t, 16, GS_WAVE));
-                t = fmax_std(t, __shfl_xor(t, 8, GS_WAVE));
-                t = fmax_std(t, __shfl_xor(t, 4, GS_WAVE));
-                t = fmax_std(t, __shfl_xor(t, 2, GS_WAVE));
-                t = fmax_std(t, __shfl_xor(t, 1, GS_WAVE));
-                const float tA = __shfl(t, 0, GS_WAVE);
-                const float tB = __shfl(t, 32, GS_WAVE);
-                if (chkA && tA < bp.thr) { doneA = true; mA = 0; }
-                if (chkB && tB < bp.thr) { doneB = true; mB = 0; }
+                // max over the microblock's pixels < thr  <=>  no pixel has T >= thr
+                // (T is never NaN; edge pixels outside the image do not vote).
+                const uint64_t live = __ballot(pix_valid && !(T < bp.thr));
+                if (chkA && (uint32_t)live == 0u) doneA = true;
+                if (chkB && (uint32_t)(live >> 32) == 0u) doneB = true;
+                if (doneA && doneB) break;
             }
         }
-        __syncthreads();
     }
 
-    if (bp.evals != nullptr && lane == 0 && evals != 0)
-        atomicAdd(bp.evals, (unsigned long long)evals);
+    if (bp.evals != nullptr && lane == 0) {
+        // 64 slot groups of 8 counters: spreads the per-wave atomics
+        unsigned long long* slot = bp.evals + (size_t)(blockIdx.x & 63u) * 8;
+        atomicAdd(slot + 0, (unsigned long long)evals);
+        atomicAdd(slot + 1, (unsigned long long)n_batch);
+        atomicAdd(slot + 2, (unsigned long long)n_iter);
+        atomicAdd(slot + 3, (unsigned long long)n_kept);
+        atomicMax(slot + 4, (unsigned long long)n_iter);
+    }
     if (!pix_valid) return;
     const size_t o = ((size_t)(py0 + pi) * bp.width + (size_t)(px_start + pj)) * 3;
     if (OUT == 2) {

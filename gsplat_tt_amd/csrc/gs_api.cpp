@@ -167,18 +167,19 @@ struct gs_ctx {
 
     // frame
     DevBuf b_rect, b_covc, b_dkey, b_brec, b_src, b_valid;
-    DevBuf b_offs, b_pair_tile, b_pair_id, b_ranges, b_out;
+    DevBuf b_offs, b_bstart, b_pair_tile, b_pair_id, b_ranges, b_out;
     DevBuf b_kalt, b_valt, b_hist, b_state, b_lb, b_cnt;
-    DevBuf b_tmp_a, b_tmp_b, b_tmp_c;
+    DevBuf b_tmp_a, b_tmp_b, b_tmp_c, b_evals;
+    std::vector<uint64_t> h_evals = std::vector<uint64_t>(64 * 8);
     uint32_t* h_pin = nullptr;  // pinned: counters + histograms
     gs::SortTemp sort;
 
     ~gs_ctx() {
         if (st) (void)hipStreamSynchronize(st);
         for (DevBuf* b : {&b_mean, &b_cov, &b_opac, &b_col, &b_terms, &b_upload, &b_rect, &b_covc,
-                          &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_pair_tile, &b_pair_id,
+                          &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_bstart, &b_pair_tile, &b_pair_id,
                           &b_ranges, &b_out, &b_kalt, &b_valt, &b_hist, &b_state, &b_lb, &b_cnt,
-                          &b_tmp_a, &b_tmp_b, &b_tmp_c})
+                          &b_tmp_a, &b_tmp_b, &b_tmp_c, &b_evals})
             b->release();
         if (h_pin) (void)hipHostFree(h_pin);
         for (auto& e : ev)
@@ -377,7 +378,7 @@ struct gs_ctx {
                       b_brec.as<float4>(), want_src ? b_src.as<uint32_t>() : nullptr};
         HIPCHK(gs::launch_project(sd, p, c, want_valid ? b_valid.as<uint8_t>() : nullptr,
                                   b_lb.as<uint64_t>(), b_cnt.as<uint32_t>() + 0,
-                                  b_cnt.as<uint32_t>() + 1, st));
+                                  b_cnt.as<uint32_t>() + 1, nullptr, st));
         HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
         sync();
         return h_pin[1];
@@ -391,16 +392,25 @@ struct gs_ctx {
         b_offs.ensure(std::max<int64_t>(m, 1) * 4);
         const size_t rparts = gs::rect_scan_partitions(std::max<int64_t>(m, 1));
         b_lb.ensure(rparts * 8);
-        HIPCHK(gs::launch_fill_u32(b_cnt.as<uint32_t>() + 8, 0u, 8, st));
-        HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, rparts * 2, st));
-        HIPCHK(gs::launch_rect_count_scan(rect, order, m, tp, b_offs.as<uint32_t>(),
-                                          b_lb.as<uint64_t>(), b_cnt.as<uint32_t>() + 8,
-                                          b_cnt.as<uint32_t>() + 9, st));
-        HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
-        sync();
-        const uint32_t p_pre = h_pin[9];
-        if (p_pre == 0xFFFFFFFFu)
-            throw GsError(GS_E_CAPACITY, "tile_assign: more than 2^32-1 candidate pairs");
+        if (b_bstart.cap < 4096 * 4) b_bstart.ensure(4096 * 4);
+        uint32_t p_pre = 0;
+        for (int attempt = 0; attempt < 2; ++attempt) {
+            HIPCHK(gs::launch_fill_u32(b_cnt.as<uint32_t>() + 8, 0u, 8, st));
+            HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, rparts * 2, st));
+            HIPCHK(gs::launch_rect_count_scan(rect, order, m, nullptr, tp, b_offs.as<uint32_t>(),
+                                              b_bstart.as<uint32_t>(),
+                                              (uint32_t)(b_bstart.cap / 4), b_lb.as<uint64_t>(),
+                                              b_cnt.as<uint32_t>() + 8, b_cnt.as<uint32_t>() + 9,
+                                              st));
+            HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
+            sync();
+            p_pre = h_pin[9];
+            if (p_pre == 0xFFFFFFFFu)
+                throw GsError(GS_E_CAPACITY, "tile_assign: more than 2^32-1 candidate pairs");
+            const size_t need = gs::emit_partitions(p_pre) + 1;
+            if (need * 4 <= b_bstart.cap) break;
+            b_bstart.ensure(need * 4);  // partition table too small: grow, count again
+        }
         *p_pre_out = p_pre;
         if (p_pre == 0) return 0;
         b_pair_tile.ensure((size_t)p_pre * 4);
@@ -408,10 +418,11 @@ struct gs_ctx {
         const size_t eparts = gs::emit_partitions(p_pre);
         b_lb.ensure(eparts * 8);
         HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, eparts * 2, st));
-        HIPCHK(gs::launch_pair_emit(rect, cov, order, b_offs.as<uint32_t>(), m, p_pre, tp,
+        HIPCHK(gs::launch_pair_emit(rect, cov, order, b_offs.as<uint32_t>(),
+                                    b_bstart.as<uint32_t>(), m, nullptr, p_pre, nullptr, tp,
                                     b_pair_tile.as<uint32_t>(), b_pair_id.as<uint32_t>(), p_pre,
                                     b_lb.as<uint64_t>(), b_cnt.as<uint32_t>() + 10,
-                                    b_cnt.as<uint32_t>() + 11, st));
+                                    b_cnt.as<uint32_t>() + 11, nullptr, st));
         HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
         sync();
         return h_pin[11];
@@ -472,13 +483,14 @@ struct gs_ctx {
                                         tile_bits(T), sort, h_pin + 64, st, &passes, false,
                                         &tiles_sorted, &ids_sorted));
         b_ranges.ensure((size_t)T * 8);
-        HIPCHK(gs::launch_tile_ranges(static_cast<uint32_t*>(tiles_sorted), P,
+        HIPCHK(gs::launch_tile_ranges(static_cast<uint32_t*>(tiles_sorted), P, nullptr,
                                       b_ranges.as<uint32_t>(), T, st));
         gs::BlendParams bp{tiles_x, tiles_y, ts, H, W, v->cull_disabled ? 1 : 0,
                            v->transmittance_threshold, v->out_format, nullptr};
         if (timing) {
-            HIPCHK(gs::launch_fill_u32(b_cnt.as<uint32_t>() + 16, 0u, 2, st));
-            bp.evals = reinterpret_cast<unsigned long long*>(b_cnt.as<uint32_t>() + 16);
+            b_evals.ensure(64 * 8 * 8);
+            HIPCHK(gs::launch_fill_u32(b_evals.as<uint32_t>(), 0u, 64 * 8 * 2, st));
+            bp.evals = b_evals.as<unsigned long long>();
         }
         record(4);
         HIPCHK(gs::launch_blend(b_brec.as<float4>(), ids_sorted, b_ranges.as<uint32_t>(), bp,
@@ -504,12 +516,20 @@ struct gs_ctx {
     void finish(void* out, void* dout, bool out_dev, size_t bytes, gs_stats* stats, gs_stats s,
                 std::chrono::steady_clock::time_point t0) {
         if (!out_dev) HIPCHK(hipMemcpyAsync(out, dout, bytes, hipMemcpyDeviceToHost, st));
-        if (timing) HIPCHK(hipMemcpyAsync(h_pin + 32, b_cnt.as<uint32_t>() + 16, 8, hipMemcpyDeviceToHost, st));
+        if (timing && s.num_entries > 0)
+            HIPCHK(hipMemcpyAsync(h_evals.data(), b_evals.p, 64 * 8 * 8, hipMemcpyDeviceToHost, st));
         sync();
         if (timing && s.num_entries > 0) {
-            uint64_t e;
-            std::memcpy(&e, h_pin + 32, 8);
-            s.blend_evals = (int64_t)e;
+            uint64_t e[5] = {0, 0, 0, 0, 0};
+            for (int k = 0; k < 64; ++k) {
+                for (int c = 0; c < 4; ++c) e[c] += h_evals[k * 8 + c];
+                e[4] = std::max<uint64_t>(e[4], h_evals[k * 8 + 4]);
+            }
+            s.blend_evals = (int64_t)e[0];
+            s.blend_batches = (int64_t)e[1];
+            s.blend_iters = (int64_t)e[2];
+            s.blend_kept = (int64_t)e[3];
+            s.blend_max_iters = (int64_t)e[4];
         }
         s.ms_total = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() - t0)
                          .count();
@@ -862,6 +882,14 @@ int gs_memcpy_d2h(gs_ctx* ctx, void* dst, const void* src, int64_t bytes) {
     return guard([&] {
         REQUIRE(ctx && bytes >= 0, "bad argument");
         HIPCHK(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToHost, ctx->st));
+        ctx->sync();
+    });
+}
+
+int gs_memcpy_d2d(gs_ctx* ctx, void* dst, const void* src, int64_t bytes) {
+    return guard([&] {
+        REQUIRE(ctx && bytes >= 0, "bad argument");
+        HIPCHK(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToDevice, ctx->st));
         ctx->sync();
     });
 }

@@ -50,9 +50,11 @@ struct Compact {
 };
 
 // ---- project.hip
+// part_hist (optional): per-partition digit histograms of the visible depth
+// keys, [project_partitions(n)][4][256], summed by launch_reduce_rows.
 hipError_t launch_project(const SceneDev& s, const ProjParams& p, Compact out,
                           uint8_t* valid_mask, uint64_t* lb_state, uint32_t* ticket,
-                          uint32_t* count_out, hipStream_t st);
+                          uint32_t* count_out, uint32_t* part_hist, hipStream_t st);
 hipError_t launch_soa_transpose(const float* aos, int64_t n, int cols, const int* col_map,
                                 int planes, float* soa, hipStream_t st);
 size_t project_partitions(int64_t n);
@@ -82,22 +84,45 @@ hipError_t radix_sort_pairs(void* keys, uint32_t* vals, int64_t n, int key_bytes
                             int begin_bit, int end_bit, SortTemp& tmp, uint32_t* host_hist,
                             hipStream_t st, int* passes_run, bool vals_iota,
                             void** keys_final, uint32_t** vals_final);
+// Same sort with no host synchronisation: the key count is min(n_cap, *n_dev)
+// (n_dev may be null), `hist` holds the [pass][256] digit histograms of the
+// keys (built by their producer), `tickets` one zeroed word per pass. Every
+// pass runs; the result buffer follows from the pass count alone.
+hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const uint32_t* n_dev,
+                                int key_bytes, int begin_bit, int end_bit, const uint32_t* hist,
+                                uint32_t* tickets, SortTemp& tmp, hipStream_t st, bool vals_iota,
+                                void** keys_final, uint32_t** vals_final);
 
 // ---- tiles.hip
 struct TileParams {
     int tiles_x, tiles_y, tile_size;
     int cull;          // per-pair Mahalanobis cull on
 };
+// offs: exclusive scan of rectangle areas in `order`; bstart[b]: rank owning
+// candidate b*emit_part (b < bstart_cap).
+// Sizes: m / p_pre / p are host capacities sizing the grids; when the *_dev
+// pointer is given the real count is read on the device (min with the
+// capacity) and partitions beyond it exit at once.
 hipError_t launch_rect_count_scan(const float4* rect, const uint32_t* order, int64_t m,
-                                  TileParams tp, uint32_t* offs, uint64_t* lb_state,
+                                  const uint32_t* m_dev, TileParams tp, uint32_t* offs,
+                                  uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
                                   uint32_t* ticket, uint32_t* total_out, hipStream_t st);
+// part_hist (optional): per-partition digit histograms [emit_partitions][2][256]
+// of the kept pairs' tile ids (bits 0-7, 8-15).
 hipError_t launch_pair_emit(const float4* rect, const float4* cov, const uint32_t* order,
-                            const uint32_t* offs, int64_t m, uint32_t p_pre, TileParams tp,
-                            uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
+                            const uint32_t* offs, const uint32_t* bstart, int64_t m,
+                            const uint32_t* m_dev, uint32_t p_pre, const uint32_t* p_pre_dev,
+                            TileParams tp, uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
                             uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
-                            hipStream_t st);
-hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, uint32_t* ranges,
-                              int64_t num_tiles, hipStream_t st);
+                            uint32_t* part_hist, hipStream_t st);
+hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, const uint32_t* p_dev,
+                              uint32_t* ranges, int64_t num_tiles, hipStream_t st);
+// out[c] += sum over rows of part[r][c] (out must be cleared by the caller).
+hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,
+                              const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
+                              uint32_t* out, hipStream_t st);
+constexpr uint32_t kEmitPartition = 2048;   // candidates per emit partition
+constexpr uint32_t kProjPartition = 1024;   // Gaussians per project partition
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t st);
 hipError_t launch_make_keys64(const uint32_t* gid, const uint32_t* tid, const float* depths,
                               uint32_t p, uint64_t* keys, hipStream_t st);
@@ -113,7 +138,10 @@ struct BlendParams {
     int cull_disabled;
     float thr;
     int out_format;    // 0 u8, 1 bf16, 2 f32
-    unsigned long long* evals;  // optional: += pixel-Gaussian evaluations blended
+    // optional counters, 64 slot groups of 8 (summed by the host): pixel-Gaussian
+    // evaluations, entry batches, apply iterations, kept (entry, microblock)
+    // pairs, max apply iterations of one wave
+    unsigned long long* evals;
 };
 hipError_t launch_blend(const float4* brec, const uint32_t* sorted_id, const uint32_t* ranges,
                         BlendParams bp, void* out, hipStream_t st);

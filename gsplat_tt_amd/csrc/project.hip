@@ -70,14 +70,18 @@ template <int DEG>
 __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams p, Compact out,
                                                           uint8_t* __restrict__ valid_mask,
                                                           uint64_t* lb_state, uint32_t* ticket,
-                                                          uint32_t* count_out) {
+                                                          uint32_t* count_out,
+                                                          uint32_t* __restrict__ part_hist) {
     __shared__ uint32_t s_vid;
     __shared__ uint32_t s_cnt[kProjItems][kProjThreads / GS_WAVE];
+    __shared__ uint32_t s_hist[4][256];
     __shared__ uint64_t s_excl;
     const int tid = threadIdx.x;
     const int w = tid / GS_WAVE;
     const int lane = lane_id();
     if (tid == 0) s_vid = atomicAdd(ticket, 1u);
+    if (part_hist != nullptr)
+        for (int i = tid; i < 4 * 256; i += kProjThreads) (&s_hist[0][0])[i] = 0;
     __syncthreads();
     const uint32_t vid = s_vid;
     const int64_t base = (int64_t)vid * kProjPart;
@@ -173,8 +177,19 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
         }
         bal[it] = __ballot(valid[it]);
         if (lane == 0) s_cnt[it][w] = (uint32_t)__popcll(bal[it]);
+        if (part_hist != nullptr && valid[it]) {
+            // digit histograms of the depth keys, for the depth sort's passes
+            const uint32_t k = __float_as_uint(vtz[it]);
+            atomicAdd(&s_hist[0][k & 255u], 1u);
+            atomicAdd(&s_hist[1][(k >> 8) & 255u], 1u);
+            atomicAdd(&s_hist[2][(k >> 16) & 255u], 1u);
+            atomicAdd(&s_hist[3][k >> 24], 1u);
+        }
     }
     __syncthreads();
+    if (part_hist != nullptr)
+        for (int i = tid; i < 4 * 256; i += kProjThreads)
+            part_hist[(size_t)vid * 1024 + i] = (&s_hist[0][0])[i];
 
     uint32_t total = 0;
     uint32_t my_off[kProjItems];
@@ -278,15 +293,15 @@ __global__ void k_brec_from_arrays(const float* __restrict__ means2d,
 
 hipError_t launch_project(const SceneDev& s, const ProjParams& p, Compact out,
                           uint8_t* valid_mask, uint64_t* lb_state, uint32_t* ticket,
-                          uint32_t* count_out, hipStream_t st) {
+                          uint32_t* count_out, uint32_t* part_hist, hipStream_t st) {
     if (s.n <= 0) return hipSuccess;
     const unsigned grid = (unsigned)((s.n + kProjPart - 1) / kProjPart);
     switch (s.sh_degree) {
-        case -1: k_project<-1><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out); break;
-        case 0: k_project<0><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out); break;
-        case 1: k_project<1><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out); break;
-        case 2: k_project<2><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out); break;
-        case 3: k_project<3><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out); break;
+        case -1: k_project<-1><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out, part_hist); break;
+        case 0: k_project<0><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out, part_hist); break;
+        case 1: k_project<1><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out, part_hist); break;
+        case 2: k_project<2><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out, part_hist); break;
+        case 3: k_project<3><<<grid, kProjThreads, 0, st>>>(s, p, out, valid_mask, lb_state, ticket, count_out, part_hist); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

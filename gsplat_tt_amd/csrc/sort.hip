@@ -2,9 +2,9 @@
 //
 // One upsweep pass builds the digit histograms of every pass at once; each
 // digit pass is then a single kernel (Adinets & Merrill, "Onesweep", 2022):
-//   * a 4096-key partition per 256-thread workgroup, partitions taken in
-//     order from an atomic ticket so look-back only waits on resident
-//     predecessors;
+//   * a 5120 (u64 keys) or 7168 (u32 keys) key partition per 1024-thread
+//     workgroup, partitions taken in order from an atomic ticket so look-back
+//     only waits on resident predecessors;
 //   * wave64 stable ranking with 8 ballots per key (peer mask of equal digits)
 //     plus per-wave digit counters in LDS;
 //   * per-digit decoupled look-back over epoch-tagged 64-bit descriptors (no
@@ -23,12 +23,13 @@
 namespace gs {
 namespace {
 
-constexpr int kSortThreads = 256;
-constexpr int kSortItems = 16;
-constexpr int kSortPart = kSortThreads * kSortItems;   // 4096 keys
-constexpr int kWaves = kSortThreads / GS_WAVE;
+constexpr int kWaves = 4;  // waves of the 256-thread histogram / scan blocks
 constexpr int kHistThreads = 256;
 constexpr int kMaxPasses = 8;
+#ifndef GS_LB_BATCH
+#define GS_LB_BATCH 4
+#endif
+constexpr int kLbBatch = GS_LB_BATCH;  // predecessors read per look-back round trip
 
 // descriptor: [63:34] epoch, [33:32] flag (1 aggregate, 2 inclusive), [31:0] value
 __device__ __forceinline__ uint64_t make_desc(uint32_t epoch, uint32_t flag, uint32_t v) {
@@ -84,19 +85,22 @@ __global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ key
     }
 }
 
-template <typename K, bool IOTA>
-__global__ __launch_bounds__(kSortThreads) void k_onesweep(
+template <typename K, bool IOTA, int THREADS, int ITEMS>
+__global__ __launch_bounds__(THREADS) void k_onesweep(
     const K* __restrict__ kin, const uint32_t* __restrict__ vin, K* __restrict__ kout,
-    uint32_t* __restrict__ vout, int64_t n, int shift, int bits,
-    const uint32_t* __restrict__ g_hist_pass, uint64_t* __restrict__ state,
+    uint32_t* __restrict__ vout, int64_t n_cap, const uint32_t* __restrict__ n_dev, int shift,
+    int bits, const uint32_t* __restrict__ g_hist_pass, uint64_t* __restrict__ state,
     uint32_t* __restrict__ ticket, uint32_t epoch) {
+    constexpr int WAVES = THREADS / GS_WAVE;
+    constexpr int PART = THREADS * ITEMS;
+    static_assert(THREADS >= 256, "one thread per digit");
     __shared__ uint32_t s_vid;
-    __shared__ uint32_t s_wcnt[kWaves][256];
+    __shared__ uint32_t s_wcnt[WAVES][256];
     __shared__ uint32_t s_loff[256];
     __shared__ uint32_t s_gpos[256];
-    __shared__ uint32_t s_tmp[kWaves];
-    __shared__ K s_keys[kSortPart];
-    __shared__ uint32_t s_vals[kSortPart];
+    __shared__ uint32_t s_tmp[2][4];
+    __shared__ K s_keys[PART];
+    __shared__ uint32_t s_vals[PART];
 
     const int tid = threadIdx.x;
     const int w = tid / GS_WAVE;
@@ -104,18 +108,20 @@ __global__ __launch_bounds__(kSortThreads) void k_onesweep(
     const uint32_t mask = (1u << bits) - 1u;
 
     if (tid == 0) s_vid = atomicAdd(ticket, 1u);
-#pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) s_wcnt[ww][tid] = 0;
+    for (int i = tid; i < WAVES * 256; i += THREADS) (&s_wcnt[0][0])[i] = 0;
     __syncthreads();
     const uint32_t vid = s_vid;
-    const int64_t part_base = (int64_t)vid * kSortPart;
-    const int64_t wave_base = part_base + (int64_t)w * (kSortItems * GS_WAVE);
+    const int64_t part_base = (int64_t)vid * PART;
+    // grid sized for a capacity; the key count may be known only on the device
+    const int64_t n = n_dev ? min(n_cap, (int64_t)*n_dev) : n_cap;
+    if (part_base >= n) return;  // tickets are in order: no later partition has keys
+    const int64_t wave_base = part_base + (int64_t)w * (ITEMS * GS_WAVE);
 
-    K key[kSortItems];
-    uint32_t val[kSortItems];
-    uint32_t rank[kSortItems];
+    K key[ITEMS];
+    uint32_t val[ITEMS];
+    uint32_t rank[ITEMS];
 #pragma unroll
-    for (int it = 0; it < kSortItems; ++it) {
+    for (int it = 0; it < ITEMS; ++it) {
         const int64_t idx = wave_base + it * GS_WAVE + lane;
         if (idx < n) {
             key[it] = kin[idx];
@@ -125,9 +131,11 @@ __global__ __launch_bounds__(kSortThreads) void k_onesweep(
             val[it] = 0;
         }
     }
+    // Stable wave ranking: peers = lanes with the same digit (8 ballots);
+    // rank = earlier items of this wave with that digit + lower peer lanes.
     const uint64_t lt = lanemask_lt();
 #pragma unroll
-    for (int it = 0; it < kSortItems; ++it) {
+    for (int it = 0; it < ITEMS; ++it) {
         const int64_t idx = wave_base + it * GS_WAVE + lane;
         rank[it] = 0;
         if (idx < n) {
@@ -146,56 +154,85 @@ __global__ __launch_bounds__(kSortThreads) void k_onesweep(
     }
     __syncthreads();
 
-    // Digit totals and per-wave exclusive offsets (thread = digit).
-    uint32_t tot = 0;
-    {
-        uint32_t c[kWaves];
+    // Threads 0..255 own one digit each: per-wave exclusive offsets, digit
+    // total of this partition, decoupled look-back over earlier partitions.
+    uint32_t tot = 0, excl = 0;
+    if (tid < 256) {
 #pragma unroll
-        for (int ww = 0; ww < kWaves; ++ww) c[ww] = s_wcnt[ww][tid];
-#pragma unroll
-        for (int ww = 0; ww < kWaves; ++ww) {
+        for (int ww = 0; ww < WAVES; ++ww) {
+            const uint32_t c = s_wcnt[ww][tid];
             s_wcnt[ww][tid] = tot;
-            tot += c[ww];
+            tot += c;
         }
-    }
-    // Decoupled look-back for digit `tid` over earlier partitions.
-    uint32_t excl = 0;
-    if (vid == 0) {
-        st_agent(&state[tid], make_desc(epoch, 2u, tot));
-    } else {
-        st_agent(&state[(size_t)vid * 256 + tid], make_desc(epoch, 1u, tot));
-        int64_t j = (int64_t)vid - 1;
-        uint32_t spins = 0;
-        while (true) {
-            const uint64_t s = ld_agent(&state[(size_t)j * 256 + tid]);
-            const uint32_t flag = (uint32_t)(s >> 32) & 3u;
-            if ((uint32_t)(s >> 34) != epoch || flag == 0u) {
-                // bounded wait (see lookback_exclusive): never hang the GPU
-                if (++spins < kLbMaxSpins) {
-                    __builtin_amdgcn_s_sleep(1);
-                    continue;
+        if (vid == 0) {
+            st_agent(&state[tid], make_desc(epoch, 2u, tot));
+        } else {
+            st_agent(&state[(size_t)vid * 256 + tid], make_desc(epoch, 1u, tot));
+            // Look back kLbBatch predecessors per round trip: the loads are
+            // independent, so one memory latency covers the whole batch.
+            int64_t j = (int64_t)vid - 1;
+            uint32_t spins = 0;
+            bool done = false;
+            while (!done) {
+                uint64_t sv[kLbBatch];
+#pragma unroll
+                for (int q = 0; q < kLbBatch; ++q)
+                    sv[q] = (j - q >= 0) ? ld_agent(&state[(size_t)(j - q) * 256 + tid])
+                                         : make_desc(epoch, 2u, 0u);
+                int used = 0;
+#pragma unroll
+                for (int q = 0; q < kLbBatch; ++q) {
+                    if (done || used < q) continue;  // stop at the first gap
+                    const uint64_t s = sv[q];
+                    const uint32_t flag = (uint32_t)(s >> 32) & 3u;
+                    if ((uint32_t)(s >> 34) != epoch || flag == 0u) continue;
+                    excl += (uint32_t)s;
+                    ++used;
+                    if (flag == 2u) done = true;
                 }
-                break;
+                j -= used;
+                if (!done && used < kLbBatch) {
+                    // bounded wait (see lookback_exclusive): never hang the GPU
+                    if (++spins < kLbMaxSpins) {
+                        __builtin_amdgcn_s_sleep(1);
+                    } else {
+                        done = true;
+                    }
+                }
             }
-            excl += (uint32_t)s;
-            if (flag == 2u) break;
-            --j;
+            st_agent(&state[(size_t)vid * 256 + tid], make_desc(epoch, 2u, excl + tot));
         }
-        st_agent(&state[(size_t)vid * 256 + tid], make_desc(epoch, 2u, excl + tot));
     }
-    const uint32_t loff = block_excl_scan256(tot, s_tmp);
-    const uint32_t gbase = block_excl_scan256(g_hist_pass[tid], s_tmp);
-    s_loff[tid] = loff;
-    s_gpos[tid] = gbase + excl - loff;
+    // Exclusive scans over the 256 digits: partition-local offsets (tot) and
+    // global digit bases (histogram of this pass).
+    const uint32_t v1 = (tid < 256) ? tot : 0u;
+    const uint32_t v2 = (tid < 256) ? g_hist_pass[tid] : 0u;
+    const uint32_t i1 = wave_incl_scan(v1);
+    const uint32_t i2 = wave_incl_scan(v2);
+    if (lane == GS_WAVE - 1 && w < 4) {
+        s_tmp[0][w] = i1;
+        s_tmp[1][w] = i2;
+    }
+    __syncthreads();
+    if (tid < 256) {
+        uint32_t p1 = 0, p2 = 0;
+        for (int ww = 0; ww < w; ++ww) {
+            p1 += s_tmp[0][ww];
+            p2 += s_tmp[1][ww];
+        }
+        const uint32_t loff = p1 + i1 - v1;
+        s_loff[tid] = loff;
+        s_gpos[tid] = (p2 + i2 - v2) + excl - loff;
+    }
     __syncthreads();
 
 #pragma unroll
-    for (int it = 0; it < kSortItems; ++it) {
+    for (int it = 0; it < ITEMS; ++it) {
         const int64_t idx = wave_base + it * GS_WAVE + lane;
         if (idx < n) {
             const uint32_t d = digit_of(key[it], shift, mask);
             const uint32_t lp = s_loff[d] + s_wcnt[w][d] + rank[it];
-            if (lp < (uint32_t)kSortPart) {
+            if (lp < (uint32_t)PART) {
                 s_keys[lp] = key[it];
                 s_vals[lp] = val[it];
             }
@@ -203,8 +240,8 @@ __global__ __launch_bounds__(kSortThreads) void k_onesweep(
     }
     __syncthreads();
     const int64_t cnt64 = n - part_base;
-    const int count = cnt64 < kSortPart ? (int)cnt64 : kSortPart;
-    for (int j = tid; j < count; j += kSortThreads) {
+    const int count = cnt64 < PART ? (int)cnt64 : PART;
+    for (int j = tid; j < count; j += THREADS) {
         const K k = s_keys[j];
         const uint32_t d = digit_of(k, shift, mask);
         const uint32_t g = s_gpos[d] + (uint32_t)j;
@@ -214,6 +251,22 @@ __global__ __launch_bounds__(kSortThreads) void k_onesweep(
         }
     }
 }
+
+// Partition shapes per key width (LDS: keys + values + 16 per-wave digit
+// counters must leave room for two workgroups per CU).
+#ifndef GS_SWEEP_T32
+#define GS_SWEEP_T32 1024
+#define GS_SWEEP_I32 7
+#endif
+#ifndef GS_SWEEP_T64
+#define GS_SWEEP_T64 1024
+#define GS_SWEEP_I64 5
+#endif
+template <typename K> struct SweepCfg;
+template <> struct SweepCfg<uint32_t> { static constexpr int T = GS_SWEEP_T32, I = GS_SWEEP_I32; };
+template <> struct SweepCfg<uint64_t> { static constexpr int T = GS_SWEEP_T64, I = GS_SWEEP_I64; };
+constexpr int kMinPart = (GS_SWEEP_T64 * GS_SWEEP_I64 < GS_SWEEP_T32 * GS_SWEEP_I32)
+                             ? GS_SWEEP_T64 * GS_SWEEP_I64 : GS_SWEEP_T32 * GS_SWEEP_I32;
 
 __global__ void k_fill_u32(uint32_t* p, uint32_t v, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -255,7 +308,8 @@ hipError_t sort_impl(K* keys, uint32_t* vals, int64_t n, int begin_bit, int end_
     K* kalt = static_cast<K*>(tmp.keys_alt);
     uint32_t* valt = tmp.vals_alt;
     bool iota_pending = vals_iota;
-    const unsigned grid = (unsigned)((n + kSortPart - 1) / kSortPart);
+    constexpr int T = SweepCfg<K>::T, I = SweepCfg<K>::I;
+    const unsigned grid = (unsigned)((n + T * I - 1) / (T * I));
     uint32_t* tickets = tmp.hist + (size_t)kMaxPasses * 256;
     for (int p = 0; p < npass; ++p) {
         bool trivial = false;
@@ -268,13 +322,13 @@ hipError_t sort_impl(K* keys, uint32_t* vals, int64_t n, int begin_bit, int end_
         const bool timed = tmp.pass_events != nullptr && *passes_run < tmp.max_timed_passes;
         if (timed) (void)hipEventRecord(tmp.pass_events[2 * *passes_run], st);
         if (iota_pending) {
-            k_onesweep<K, true><<<grid, kSortThreads, 0, st>>>(
-                kin, vin, kalt, valt, n, shift, bits, tmp.hist + p * 256,
+            k_onesweep<K, true, T, I><<<grid, T, 0, st>>>(
+                kin, vin, kalt, valt, n, nullptr, shift, bits, tmp.hist + p * 256,
                 tmp.state, tickets + p, epoch);
             iota_pending = false;
         } else {
-            k_onesweep<K, false><<<grid, kSortThreads, 0, st>>>(
-                kin, vin, kalt, valt, n, shift, bits, tmp.hist + p * 256,
+            k_onesweep<K, false, T, I><<<grid, T, 0, st>>>(
+                kin, vin, kalt, valt, n, nullptr, shift, bits, tmp.hist + p * 256,
                 tmp.state, tickets + p, epoch);
         }
         if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -292,9 +346,73 @@ hipError_t sort_impl(K* keys, uint32_t* vals, int64_t n, int begin_bit, int end_
     return hipSuccess;
 }
 
+// Every pass runs (no trivial-pass skipping: the host does not see the
+// histogram); n is min(n_cap, *n_dev), read on the device.
+template <typename K>
+hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t* n_dev,
+                         int begin_bit, int end_bit, const uint32_t* hist, uint32_t* tickets,
+                         SortTemp& tmp, hipStream_t st, bool vals_iota, K** keys_final,
+                         uint32_t** vals_final) {
+    *keys_final = keys;
+    *vals_final = vals;
+    if (n_cap <= 0) return hipSuccess;
+    if (n_cap >= (int64_t)1 << 32) return hipErrorInvalidValue;
+    const int npass = (end_bit - begin_bit + 7) / 8;
+    if (npass <= 0 || npass > kMaxPasses) return hipErrorInvalidValue;
+    K* kin = keys;
+    uint32_t* vin = vals;
+    K* kalt = static_cast<K*>(tmp.keys_alt);
+    uint32_t* valt = tmp.vals_alt;
+    constexpr int T = SweepCfg<K>::T, I = SweepCfg<K>::I;
+    const unsigned grid = (unsigned)((n_cap + T * I - 1) / (T * I));
+    for (int p = 0; p < npass; ++p) {
+        const int shift = begin_bit + 8 * p;
+        const int bits = std::min(8, end_bit - shift);
+        const uint32_t epoch = ++tmp.epoch;
+        if (p == 0 && vals_iota)
+            k_onesweep<K, true, T, I><<<grid, T, 0, st>>>(kin, vin, kalt, valt, n_cap, n_dev,
+                                                          shift, bits, hist + p * 256, tmp.state,
+                                                          tickets + p, epoch);
+        else
+            k_onesweep<K, false, T, I><<<grid, T, 0, st>>>(kin, vin, kalt, valt, n_cap, n_dev,
+                                                           shift, bits, hist + p * 256, tmp.state,
+                                                           tickets + p, epoch);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        std::swap(kin, kalt);
+        std::swap(vin, valt);
+    }
+    *keys_final = kin;
+    *vals_final = vin;
+    return hipSuccess;
+}
+
 }  // namespace
 
-size_t sort_partitions(int64_t n) { return (size_t)((n + kSortPart - 1) / kSortPart); }
+hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const uint32_t* n_dev,
+                                int key_bytes, int begin_bit, int end_bit, const uint32_t* hist,
+                                uint32_t* tickets, SortTemp& tmp, hipStream_t st, bool vals_iota,
+                                void** keys_final, uint32_t** vals_final) {
+    if (key_bytes == 4) {
+        uint32_t* kf = nullptr;
+        hipError_t e = sort_dev_impl<uint32_t>(static_cast<uint32_t*>(keys), vals, n_cap, n_dev,
+                                               begin_bit, end_bit, hist, tickets, tmp, st,
+                                               vals_iota, &kf, vals_final);
+        *keys_final = kf;
+        return e;
+    }
+    if (key_bytes == 8) {
+        uint64_t* kf = nullptr;
+        hipError_t e = sort_dev_impl<uint64_t>(static_cast<uint64_t*>(keys), vals, n_cap, n_dev,
+                                               begin_bit, end_bit, hist, tickets, tmp, st,
+                                               vals_iota, &kf, vals_final);
+        *keys_final = kf;
+        return e;
+    }
+    return hipErrorInvalidValue;
+}
+
+size_t sort_partitions(int64_t n) { return (size_t)((n + kMinPart - 1) / kMinPart); }
 size_t sort_state_bytes(int64_t n) { return sort_partitions(n) * 256 * sizeof(uint64_t); }
 size_t sort_hist_words() { return (size_t)kMaxPasses * 256 + kMaxPasses; }
 

@@ -10,6 +10,8 @@
 // src/gsplat_cpu/sort.cpp:146-165 (tile_ranges, (0,0) for empty tiles).
 // Compiled with -ffp-contract=off: every comparison sees the reference's
 // fp32 values.
+#include <algorithm>
+
 #include "gs_common.h"
 #include "gs_internal.h"
 
@@ -29,6 +31,22 @@ __device__ __forceinline__ float fmax_std(float a, float b) { return (a < b) ? b
 struct Rect {
     int x0, x1, y0, y1;
 };
+
+// q = j / w, r = j % w for j < 2^24 and a quotient below 2^16 (a tile row of a
+// Gaussian's rectangle): float reciprocal estimate, then one exact correction.
+__device__ __forceinline__ void divmod_small(uint32_t j, uint32_t w, uint32_t& q, uint32_t& r) {
+    int qi = (int)((float)j * __builtin_amdgcn_rcpf((float)w));
+    int ri = (int)j - qi * (int)w;
+    if (ri < 0) {
+        --qi;
+        ri += (int)w;
+    } else if (ri >= (int)w) {
+        ++qi;
+        ri -= (int)w;
+    }
+    q = (uint32_t)qi;
+    r = (uint32_t)ri;
+}
 
 __device__ __forceinline__ Rect tile_rect(float4 r, const TileParams& tp) {
     const float ts = (float)tp.tile_size;
@@ -78,10 +96,16 @@ __device__ __forceinline__ bool pair_keep(float px, float py, float4 cv, int til
 
 // Rectangle area per rank, exclusive scan -> offs[r]; last partition writes
 // the total candidate count (saturated to 0xFFFFFFFF on overflow).
+// Also records, for every emit partition b (candidates [b*kEmitPart, ...)),
+// the rank that owns its first candidate: bstart[b].
 __global__ __launch_bounds__(kThreads) void k_rect_count_scan(const float4* __restrict__ rect,
                                                               const uint32_t* __restrict__ order,
-                                                              int64_t m, TileParams tp,
+                                                              int64_t m_cap,
+                                                              const uint32_t* __restrict__ m_dev,
+                                                              TileParams tp,
                                                               uint32_t* __restrict__ offs,
+                                                              uint32_t* __restrict__ bstart,
+                                                              uint32_t bstart_cap,
                                                               uint64_t* lb_state,
                                                               uint32_t* ticket,
                                                               uint32_t* total_out) {
@@ -92,6 +116,10 @@ __global__ __launch_bounds__(kThreads) void k_rect_count_scan(const float4* __re
     if (tid == 0) s_vid = atomicAdd(ticket, 1u);
     __syncthreads();
     const uint32_t vid = s_vid;
+    // the grid may be sized for a capacity; the real count can live on the device
+    const int64_t m = m_dev ? min(m_cap, (int64_t)*m_dev) : m_cap;
+    const uint32_t nparts = (uint32_t)((m + kCountPart - 1) / kCountPart);
+    if (vid >= nparts) return;  // no later partition has work either
     const int64_t base = (int64_t)vid * kCountPart;
     uint32_t incl[kCountItems], cnt[kCountItems];
 #pragma unroll
@@ -121,7 +149,7 @@ __global__ __launch_bounds__(kThreads) void k_rect_count_scan(const float4* __re
         const uint64_t ex = lookback_exclusive(lb_state, vid, total);
         if (lane == 0) {
             s_excl = ex;
-            if (vid == gridDim.x - 1) {
+            if (vid == nparts - 1) {
                 const uint64_t t = ex + total;
                 *total_out = t > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)t;
             }
@@ -132,60 +160,91 @@ __global__ __launch_bounds__(kThreads) void k_rect_count_scan(const float4* __re
 #pragma unroll
     for (int it = 0; it < kCountItems; ++it) {
         const int64_t r = base + it * kThreads + tid;
-        if (r < m) offs[r] = (uint32_t)(ex + my_off[it] + incl[it] - cnt[it]);
+        if (r < m) {
+            const uint64_t o = ex + my_off[it] + incl[it] - cnt[it];
+            offs[r] = (uint32_t)o;
+            // emit partitions whose first candidate lies in [o, o + cnt)
+            uint64_t b = (o + kEmitPart - 1) / kEmitPart;
+            for (; b * kEmitPart < o + cnt[it] && b < bstart_cap; ++b) bstart[b] = (uint32_t)r;
+        }
     }
-}
-
-// Largest r in [lo, hi) with offs[r] <= c (offs ascending, offs[lo] <= c).
-__device__ __forceinline__ int64_t upper_rank(const uint32_t* offs, int64_t lo, int64_t hi,
-                                              uint32_t c) {
-    while (hi - lo > 1) {
-        const int64_t mid = (lo + hi) >> 1;
-        if (offs[mid] <= c) lo = mid; else hi = mid;
-    }
-    return lo;
 }
 
 // Pair-centric emission: candidate c -> (rank r, j-th tile of r's rectangle),
-// cull, stable compaction of kept pairs in candidate order.
+// cull, stable compaction of kept pairs in candidate order. The ranks of a
+// partition are [bstart[vid], bstart[vid+1]]; each candidate finds its rank by
+// an inclusive max-scan over rank heads in LDS.
 __global__ __launch_bounds__(kThreads) void k_pair_emit(
     const float4* __restrict__ rect, const float4* __restrict__ cov,
-    const uint32_t* __restrict__ order, const uint32_t* __restrict__ offs, int64_t m,
-    uint32_t p_pre, TileParams tp, uint32_t* __restrict__ pair_tile,
-    uint32_t* __restrict__ pair_id, uint32_t cap, uint64_t* lb_state, uint32_t* ticket,
-    uint32_t* total_out) {
+    const uint32_t* __restrict__ order, const uint32_t* __restrict__ offs,
+    const uint32_t* __restrict__ bstart, int64_t m_cap, const uint32_t* __restrict__ m_dev,
+    uint32_t p_pre_cap, const uint32_t* __restrict__ p_pre_dev, TileParams tp,
+    uint32_t* __restrict__ pair_tile, uint32_t* __restrict__ pair_id, uint32_t cap,
+    uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
+    uint32_t* __restrict__ part_hist) {
     __shared__ uint32_t s_vid;
-    __shared__ int64_t s_rlo, s_rhi;
     __shared__ uint32_t s_off[kEmitPart + 1];
     __shared__ uint32_t s_g[kEmitPart + 1];
-    __shared__ int32_t s_x0[kEmitPart + 1];
-    __shared__ int32_t s_y0[kEmitPart + 1];
-    __shared__ int32_t s_w[kEmitPart + 1];
+    __shared__ uint32_t s_xy[kEmitPart + 1];
+    __shared__ uint32_t s_w[kEmitPart + 1];
+    __shared__ uint32_t s_own[kEmitPart];
+    __shared__ uint32_t s_wmax[kWaves];
     __shared__ uint32_t s_cnt[kEmitItems][kWaves];
+    __shared__ uint32_t s_th[2][256];
     __shared__ uint64_t s_excl;
     const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
     if (tid == 0) s_vid = atomicAdd(ticket, 1u);
-    __syncthreads();
-    const uint32_t vid = s_vid;
-    const uint64_t c0 = (uint64_t)vid * kEmitPart;
-    const uint64_t c1 = min((uint64_t)p_pre, c0 + kEmitPart);
-    if (tid == 0) {
-        s_rlo = upper_rank(offs, 0, m, (uint32_t)c0);
-        s_rhi = upper_rank(offs, 0, m, (uint32_t)(c1 - 1));
+    for (int i = tid; i < kEmitPart; i += kThreads) s_own[i] = 0;
+    if (part_hist != nullptr) {
+        s_th[0][tid] = 0;
+        s_th[1][tid] = 0;
     }
     __syncthreads();
-    const int64_t rlo = s_rlo;
-    // every rank owns >= 1 candidate, so nr <= kEmitPart; clamp defensively
-    const int64_t nr = min(s_rhi - s_rlo + 1, (int64_t)kEmitPart + 1);
+    const uint32_t vid = s_vid;
+    const int64_t m = m_dev ? min(m_cap, (int64_t)*m_dev) : m_cap;
+    const uint32_t p_pre = p_pre_dev ? min(p_pre_cap, *p_pre_dev) : p_pre_cap;
+    const uint32_t nparts = (uint32_t)(((uint64_t)p_pre + kEmitPart - 1) / kEmitPart);
+    if (vid >= nparts) return;  // no later partition has work either
+    const uint64_t c0 = (uint64_t)vid * kEmitPart;
+    const uint64_t c1 = min((uint64_t)p_pre, c0 + kEmitPart);
+    const int64_t rlo = bstart[vid];
+    const int64_t rend = (c1 < (uint64_t)p_pre) ? (int64_t)bstart[vid + 1] + 1 : m;
+    // every rank owns >= 1 candidate, so nr <= kEmitPart + 1; clamp defensively
+    const int64_t nr = min(rend - rlo, (int64_t)kEmitPart + 1);
     for (int64_t k = tid; k < nr; k += kThreads) {
         const int64_t r = rlo + k;
         const uint32_t g = order ? order[r] : (uint32_t)r;
         const Rect q = tile_rect(rect[g], tp);
-        s_off[k] = offs[r];
+        const uint32_t o = offs[r];
+        s_off[k] = o;
         s_g[k] = g;
-        s_x0[k] = q.x0;
-        s_y0[k] = q.y0;
-        s_w[k] = q.x1 - q.x0 + 1;
+        s_xy[k] = (uint32_t)q.x0 | ((uint32_t)q.y0 << 16);
+        s_w[k] = (uint32_t)(q.x1 - q.x0 + 1);
+        if (o > c0 && o < c1) s_own[o - c0] = (uint32_t)k;  // rank head
+    }
+    __syncthreads();
+    // inclusive max-scan of the heads: 8 consecutive slots per thread
+    {
+        uint32_t v[8];
+        uint32_t run = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            run = max(run, s_own[tid * 8 + i]);
+            v[i] = run;
+        }
+        uint32_t inc = run;
+#pragma unroll
+        for (int o = 1; o < GS_WAVE; o <<= 1) {
+            const uint32_t u = __shfl_up(inc, o, GS_WAVE);
+            if (lane >= o) inc = max(inc, u);
+        }
+        if (lane == GS_WAVE - 1) s_wmax[w] = inc;
+        uint32_t pre = __shfl_up(inc, 1, GS_WAVE);
+        if (lane == 0) pre = 0;
+        __syncthreads();
+        for (int ww = 0; ww < w; ++ww) pre = max(pre, s_wmax[ww]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s_own[tid * 8 + i] = max(pre, v[i]);
     }
     __syncthreads();
 
@@ -199,14 +258,13 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
         tile[it] = 0;
         gid[it] = 0;
         if (c < c1) {
-            int lo = 0, hi = (int)nr;
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (s_off[mid] <= (uint32_t)c) lo = mid; else hi = mid;
-            }
+            const uint32_t lo = s_own[it * kThreads + tid];
             const uint32_t j = (uint32_t)c - s_off[lo];
-            const uint32_t wdt = (uint32_t)s_w[lo];
-            const int t = (s_y0[lo] + (int)(j / wdt)) * tp.tiles_x + s_x0[lo] + (int)(j % wdt);
+            const uint32_t wdt = s_w[lo];
+            const uint32_t xy = s_xy[lo];
+            uint32_t row, col;
+            divmod_small(j, wdt, row, col);
+            const int t = (int)((xy >> 16) + row) * tp.tiles_x + (int)((xy & 0xFFFFu) + col);
             const uint32_t g = s_g[lo];
             bool k = true;
             if (tp.cull) {
@@ -219,8 +277,17 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
         }
         bal[it] = __ballot(keep[it]);
         if (lane == 0) s_cnt[it][w] = (uint32_t)__popcll(bal[it]);
+        if (part_hist != nullptr && keep[it]) {
+            // digit histograms of the tile keys, for the tile sort's passes
+            atomicAdd(&s_th[0][tile[it] & 255u], 1u);
+            atomicAdd(&s_th[1][(tile[it] >> 8) & 255u], 1u);
+        }
     }
     __syncthreads();
+    if (part_hist != nullptr) {
+        part_hist[(size_t)vid * 512 + tid] = s_th[0][tid];
+        part_hist[(size_t)vid * 512 + 256 + tid] = s_th[1][tid];
+    }
     uint32_t total = 0, my_off[kEmitItems];
 #pragma unroll
     for (int it = 0; it < kEmitItems; ++it)
@@ -233,7 +300,7 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
         const uint64_t ex = lookback_exclusive(lb_state, vid, total);
         if (lane == 0) {
             s_excl = ex;
-            if (vid == gridDim.x - 1) {
+            if (vid == nparts - 1) {
                 const uint64_t t = ex + total;
                 *total_out = t > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)t;
             }
@@ -253,13 +320,34 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     }
 }
 
-__global__ void k_tile_ranges(const uint32_t* __restrict__ st, uint32_t p,
-                              uint32_t* __restrict__ ranges) {
-    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= p) return;
-    const uint32_t t = st[i];
-    if (i == 0 || st[i - 1] != t) ranges[2 * (size_t)t] = i;
-    if (i == p - 1 || st[i + 1] != t) ranges[2 * (size_t)t + 1] = i + 1;
+__global__ void k_tile_ranges(const uint32_t* __restrict__ st, uint32_t p_cap,
+                              const uint32_t* __restrict__ p_dev, uint32_t* __restrict__ ranges) {
+    const uint32_t p = p_dev ? min(p_cap, *p_dev) : p_cap;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < p;
+         i += gridDim.x * blockDim.x) {
+        const uint32_t t = st[i];
+        if (i == 0 || st[i - 1] != t) ranges[2 * (size_t)t] = i;
+        if (i == p - 1 || st[i + 1] != t) ranges[2 * (size_t)t + 1] = i + 1;
+    }
+}
+
+// out[c] += sum of rows [y*64, y*64+64) of part (rows x cols), rows bounded by
+// ceil(min(*count_dev, count_cap) / per_row) when count_dev is given.
+__global__ void k_reduce_rows(const uint32_t* __restrict__ part, int cols, uint32_t rows_cap,
+                              const uint32_t* __restrict__ count_dev, uint32_t count_cap,
+                              uint32_t per_row, uint32_t* __restrict__ out) {
+    uint32_t rows = rows_cap;
+    if (count_dev) {
+        const uint32_t c = min(*count_dev, count_cap);
+        rows = min(rows_cap, (c + per_row - 1) / per_row);
+    }
+    const int col = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t r0 = blockIdx.y * 64u;
+    if (col >= cols || r0 >= rows) return;
+    const uint32_t r1 = min(rows, r0 + 64u);
+    uint32_t acc = 0;
+    for (uint32_t r = r0; r < r1; ++r) acc += part[(size_t)r * cols + col];
+    if (acc) atomicAdd(&out[col], acc);
 }
 
 // key = (tile << 32) | fp32 depth bits of the pair's Gaussian (sort.cpp:180-205).
@@ -301,32 +389,45 @@ size_t rect_scan_partitions(int64_t m) { return (size_t)((m + kCountPart - 1) / 
 size_t emit_partitions(uint64_t p_pre) { return (size_t)((p_pre + kEmitPart - 1) / kEmitPart); }
 
 hipError_t launch_rect_count_scan(const float4* rect, const uint32_t* order, int64_t m,
-                                  TileParams tp, uint32_t* offs, uint64_t* lb_state,
+                                  const uint32_t* m_dev, TileParams tp, uint32_t* offs,
+                                  uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
                                   uint32_t* ticket, uint32_t* total_out, hipStream_t st) {
     if (m <= 0) return hipSuccess;
     const unsigned grid = (unsigned)rect_scan_partitions(m);
-    k_rect_count_scan<<<grid, kThreads, 0, st>>>(rect, order, m, tp, offs, lb_state, ticket,
-                                                 total_out);
+    k_rect_count_scan<<<grid, kThreads, 0, st>>>(rect, order, m, m_dev, tp, offs, bstart,
+                                                 bstart_cap, lb_state, ticket, total_out);
     return hipGetLastError();
 }
 
 hipError_t launch_pair_emit(const float4* rect, const float4* cov, const uint32_t* order,
-                            const uint32_t* offs, int64_t m, uint32_t p_pre, TileParams tp,
-                            uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
+                            const uint32_t* offs, const uint32_t* bstart, int64_t m,
+                            const uint32_t* m_dev, uint32_t p_pre, const uint32_t* p_pre_dev,
+                            TileParams tp, uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
                             uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
-                            hipStream_t st) {
+                            uint32_t* part_hist, hipStream_t st) {
     if (p_pre == 0 || m <= 0) return hipSuccess;
     const unsigned grid = (unsigned)emit_partitions(p_pre);
-    k_pair_emit<<<grid, kThreads, 0, st>>>(rect, cov, order, offs, m, p_pre, tp, pair_tile,
-                                           pair_id, cap, lb_state, ticket, total_out);
+    k_pair_emit<<<grid, kThreads, 0, st>>>(rect, cov, order, offs, bstart, m, m_dev, p_pre,
+                                           p_pre_dev, tp, pair_tile, pair_id, cap, lb_state,
+                                           ticket, total_out, part_hist);
     return hipGetLastError();
 }
 
-hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, uint32_t* ranges,
-                              int64_t num_tiles, hipStream_t st) {
+hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, const uint32_t* p_dev,
+                              uint32_t* ranges, int64_t num_tiles, hipStream_t st) {
     hipError_t e = launch_fill_u32(ranges, 0u, (size_t)num_tiles * 2, st);
     if (e != hipSuccess || p == 0) return e;
-    k_tile_ranges<<<(p + 255) / 256, 256, 0, st>>>(sorted_tile, p, ranges);
+    const unsigned grid = std::min<unsigned>((p + 255) / 256, 4096u);
+    k_tile_ranges<<<grid, 256, 0, st>>>(sorted_tile, p, p_dev, ranges);
+    return hipGetLastError();
+}
+
+hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,
+                              const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
+                              uint32_t* out, hipStream_t st) {
+    if (rows_cap == 0) return hipSuccess;
+    dim3 grid((cols + 255) / 256, (rows_cap + 63) / 64);
+    k_reduce_rows<<<grid, 256, 0, st>>>(part, cols, rows_cap, count_dev, count_cap, per_row, out);
     return hipGetLastError();
 }
 

@@ -76,6 +76,10 @@ typedef struct gs_stats {
     float ms_blend;
     float ms_total;         /* host wall clock of the whole call */
     int64_t blend_evals;    /* pixel x Gaussian evaluations blended (timing on) */
+    int64_t blend_batches;  /* wave x 32-entry batches culled (timing on) */
+    int64_t blend_iters;    /* wave apply iterations (timing on) */
+    int64_t blend_kept;     /* kept (entry, microblock) pairs seen (timing on) */
+    int64_t blend_max_iters; /* longest wave's apply iterations (timing on) */
 } gs_stats;
 
 /* ---- context -------------------------------------------------------- */
@@ -142,6 +146,9 @@ int gs_dev_alloc(gs_ctx* ctx, int64_t bytes, void** ptr);
 int gs_dev_free(gs_ctx* ctx, void* ptr);
 int gs_memcpy_h2d(gs_ctx* ctx, void* dst, const void* src, int64_t bytes);
 int gs_memcpy_d2h(gs_ctx* ctx, void* dst, const void* src, int64_t bytes);
+/* Device-to-device copy; also the plain copy kernel of known size that HBM
+ * traffic counters are calibrated against. */
+int gs_memcpy_d2d(gs_ctx* ctx, void* dst, const void* src, int64_t bytes);
 int gs_sync(gs_ctx* ctx);
 
 #ifdef __cplusplus
