@@ -53,149 +53,157 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
     return (uint16_t)(u >> 16);
 }
 
-template <int TS, int OUT>
-__global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ brec,
-                                                   const uint32_t* __restrict__ sid,
-                                                   const uint32_t* __restrict__ ranges,
-                                                   BlendParams bp, void* __restrict__ out) {
+// Per-wave geometry of one 16x4 band (two microblocks).
+struct Band {
+    int tile, tile_x, tile_y, mbx, mby;
+    int px_start, py0;
+    float tx_tile, ty_tile, pxs, offx, pxc, pyc, mb_ox, mb_oy;
+    bool emptyA, emptyB, fullA, fullB, full, pix_valid;
+};
+
+template <int TS>
+__device__ __forceinline__ Band make_band(const BlendParams& bp, int lane) {
     constexpr int BX = TS / 16;  // 16-pixel band columns per tile
     constexpr int BY = TS / 4;   // 4-row bands per tile
-
+    Band g;
     const int band = blockIdx.x % (BX * BY);
-    const int tile = blockIdx.x / (BX * BY);
+    g.tile = blockIdx.x / (BX * BY);
     const int bx = band % BX, by = band / BX;
-    const int tile_x = tile % bp.tiles_x, tile_y = tile / bp.tiles_x;
-    const int lane = threadIdx.x;
+    g.tile_x = g.tile % bp.tiles_x;
+    g.tile_y = g.tile / bp.tiles_x;
     const int h = lane >> 5, q = lane & 31, pi = q >> 3, pj = q & 7;
-    const int mbx = bx * 2 + h, mby = by;
-
-    const int px_tile = tile_x * TS, py_tile = tile_y * TS;
+    g.mbx = bx * 2 + h;
+    g.mby = by;
+    const int px_tile = g.tile_x * TS, py_tile = g.tile_y * TS;
     const int px_end_tile = min(px_tile + TS, bp.width);
     const int py_end_tile = min(py_tile + TS, bp.height);
-    // Microblock extents of both halves (wave-uniform).
+    // microblock extents of both halves (wave-uniform)
     const int pxA = px_tile + (bx * 2) * 8, pxB = pxA + 8;
-    const int py0 = py_tile + mby * 4;
-    const int pyE = min(py0 + 4, py_end_tile);
+    g.py0 = py_tile + g.mby * 4;
+    const int pyE = min(g.py0 + 4, py_end_tile);
     const int pxEA = min(pxA + 8, px_end_tile), pxEB = min(pxB + 8, px_end_tile);
-    const bool emptyA = (py0 >= pyE) || (pxA >= pxEA);
-    const bool emptyB = (py0 >= pyE) || (pxB >= pxEB);
-    const bool fullA = !emptyA && (pxEA - pxA == 8) && (pyE - py0 == 4);
-    const bool fullB = !emptyB && (pxEB - pxB == 8) && (pyE - py0 == 4);
-    const int px_start = h ? pxB : pxA;
+    g.emptyA = (g.py0 >= pyE) || (pxA >= pxEA);
+    g.emptyB = (g.py0 >= pyE) || (pxB >= pxEB);
+    g.fullA = !g.emptyA && (pxEA - pxA == 8) && (pyE - g.py0 == 4);
+    g.fullB = !g.emptyB && (pxEB - pxB == 8) && (pyE - g.py0 == 4);
+    g.px_start = h ? pxB : pxA;
     const int px_end = h ? pxEB : pxEA;
-    const bool full = h ? fullB : fullA;
-    const bool pix_valid = !(h ? emptyB : emptyA) && (px_start + pj < px_end) && (py0 + pi < pyE);
+    g.full = h ? g.fullB : g.fullA;
+    g.pix_valid = !(h ? g.emptyB : g.emptyA) && (g.px_start + pj < px_end) && (g.py0 + pi < pyE);
+    g.tx_tile = (float)(g.tile_x * TS);
+    g.ty_tile = (float)(g.tile_y * TS);
+    g.pxs = (float)g.px_start;                  // full path: px_base = pxs - mx
+    g.offx = (float)pj + 0.5f;
+    g.pxc = (float)(g.px_start + pj) + 0.5f;    // scalar path pixel centre
+    g.pyc = (float)(g.py0 + pi) + 0.5f;
+    // microblock cull rectangle (cull_and_blend.cpp:447-498)
+    g.mb_oy = g.ty_tile + (float)(g.mby * 4);
+    g.mb_ox = g.tx_tile + (float)(g.mbx * 8);
+    return g;
+}
 
-    const float tx_tile = (float)(tile_x * TS);
-    const float ty_tile = (float)(tile_y * TS);
-    const float pxs = (float)px_start;                 // full path: px_base = pxs - mx
-    const float offx = (float)pj + 0.5f;
-    const float pxc = (float)(px_start + pj) + 0.5f;   // scalar path pixel centre
-    const float pyc = (float)(py0 + pi) + 0.5f;
-    // Microblock cull rectangle (cull_and_blend.cpp:447-498).
-    const float mb_oy = ty_tile + (float)(mby * 4);
-    const float mb_ox = tx_tile + (float)(mbx * 8);
+// Constrained-minimum cull of one entry against the lane's microblock
+// (cull_and_blend.cpp:447-498).
+__device__ __forceinline__ bool mb_keep(const Band& g, float4 r0, float4 r1, int cull_disabled) {
+    const float lt = r1.w;
+    if (!(lt < 0.0f)) return false;
+    const float mx = r0.x, my = r0.y;
+    const int mx_lo = max(0, (int)floorf(((mx - r0.z) - g.tx_tile) / 8.0f));
+    const int mx_hi = min(3, (int)floorf(((mx + r0.z) - g.tx_tile) / 8.0f));
+    const int my_lo = max(0, (int)floorf(((my - r0.w) - g.ty_tile) / 4.0f));
+    const int my_hi = min(7, (int)floorf(((my + r0.w) - g.ty_tile) / 4.0f));
+    if (!(mx_lo <= g.mbx && g.mbx <= mx_hi && my_lo <= g.mby && g.mby <= my_hi)) return false;
+    const float ci_a = r1.x, ci_b = r1.y, ci_c = r1.z;
+    const float v_lo = g.mb_oy - my;
+    const float v_hi = v_lo + 4.0f;
+    const bool y_in = (v_lo <= 0.0f) && (0.0f <= v_hi);
+    const float v_fix = (v_lo > 0.0f) ? v_lo : v_hi;
+    const float u_lo = g.mb_ox - mx;
+    const float u_hi = u_lo + 8.0f;
+    const bool x_in = (u_lo <= 0.0f) && (0.0f <= u_hi);
+    float m2_min;
+    if (cull_disabled || (x_in && y_in)) {
+        m2_min = 0.0f;
+    } else {
+        float m2_v = __builtin_inff(), m2_h = __builtin_inff();
+        if (!x_in) {
+            const float uf = (u_lo > 0.0f) ? u_lo : u_hi;
+            float vs = -ci_b * uf / fmax_std(ci_c, 1e-12f);
+            vs = fclamp_std(vs, v_lo, v_hi);
+            m2_v = ci_a * uf * uf + 2.0f * ci_b * uf * vs + ci_c * vs * vs;
+        }
+        if (!y_in) {
+            float us = -ci_b * v_fix / fmax_std(ci_a, 1e-12f);
+            us = fclamp_std(us, u_lo, u_hi);
+            m2_h = ci_a * us * us + 2.0f * ci_b * us * v_fix + ci_c * v_fix * v_fix;
+        }
+        m2_min = fmin_std(m2_v, m2_h);
+    }
+    return m2_min <= -2.0f * lt;
+}
 
-    float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
-    bool doneA = emptyA, doneB = emptyB;
-    const uint32_t npixA = emptyA ? 0u : (uint32_t)((pxEA - pxA) * (pyE - py0));
-    const uint32_t npixB = emptyB ? 0u : (uint32_t)((pxEB - pxB) * (pyE - py0));
-    uint64_t evals = 0, n_batch = 0, n_iter = 0, n_kept = 0;
-    uint32_t cntA = 0, cntB = 0;
+__device__ __forceinline__ float rdl(float v, int j) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+}
 
-    const uint32_t start = ranges[2 * tile], end = ranges[2 * tile + 1];
+// The batch loop of one band. INTERIOR: both microblocks lie fully inside the
+// image (AVX2 rule only, every pixel valid). Per-half state lives in VGPRs
+// (uniform within the half): `mine` = the half's kept entries of the batch
+// (cleared once the half is done), `cnt` = entries the half has blended; the
+// scalar unit only walks the union of both halves' masks.
+template <bool INTERIOR>
+__device__ __forceinline__ void blend_band(const Band& g, const float4* __restrict__ brec,
+                                           const uint32_t* __restrict__ sid, uint32_t start,
+                                           uint32_t end, const BlendParams& bp, int lane,
+                                           float& T, float& cr, float& cg, float& cb,
+                                           uint32_t& cnt, uint32_t& n_batch, uint32_t& n_iter,
+                                           uint32_t& n_kept) {
+    const int h = lane >> 5, q = lane & 31;
+    bool doneA = g.emptyA, doneB = g.emptyB;
     for (uint32_t base = start; base < end && !(doneA && doneB); base += 32) {
         const uint32_t idx = base + q;
         const bool has = idx < end;
         float4 r0 = make_float4(0, 0, 0, 0), r1 = r0, r2 = r0;
         if (has) {
-            const uint32_t g = sid[idx];
-            r0 = brec[3 * (size_t)g + 0];
-            r1 = brec[3 * (size_t)g + 1];
-            r2 = brec[3 * (size_t)g + 2];
+            const uint32_t gi = sid[idx];
+            r0 = brec[3 * (size_t)gi + 0];
+            r1 = brec[3 * (size_t)gi + 1];
+            r2 = brec[3 * (size_t)gi + 2];
         }
-        bool keep = false;
         const bool my_done = h ? doneB : doneA;
-        if (has && !my_done) {
-            const float lt = r1.w;
-            if (lt < 0.0f) {
-                const float mx = r0.x, my = r0.y;
-                const int mx_lo = max(0, (int)floorf(((mx - r0.z) - tx_tile) / 8.0f));
-                const int mx_hi = min(3, (int)floorf(((mx + r0.z) - tx_tile) / 8.0f));
-                const int my_lo = max(0, (int)floorf(((my - r0.w) - ty_tile) / 4.0f));
-                const int my_hi = min(7, (int)floorf(((my + r0.w) - ty_tile) / 4.0f));
-                if (mx_lo <= mbx && mbx <= mx_hi && my_lo <= mby && mby <= my_hi) {
-                    const float ci_a = r1.x, ci_b = r1.y, ci_c = r1.z;
-                    const float v_lo = mb_oy - my;
-                    const float v_hi = v_lo + 4.0f;
-                    const bool y_in = (v_lo <= 0.0f) && (0.0f <= v_hi);
-                    const float v_fix = (v_lo > 0.0f) ? v_lo : v_hi;
-                    const float u_lo = mb_ox - mx;
-                    const float u_hi = u_lo + 8.0f;
-                    const bool x_in = (u_lo <= 0.0f) && (0.0f <= u_hi);
-                    float m2_min;
-                    if (bp.cull_disabled || (x_in && y_in)) {
-                        m2_min = 0.0f;
-                    } else {
-                        float m2_v = __builtin_inff(), m2_h = __builtin_inff();
-                        if (!x_in) {
-                            const float uf = (u_lo > 0.0f) ? u_lo : u_hi;
-                            float vs = -ci_b * uf / fmax_std(ci_c, 1e-12f);
-                            vs = fclamp_std(vs, v_lo, v_hi);
-                            m2_v = ci_a * uf * uf + 2.0f * ci_b * uf * vs + ci_c * vs * vs;
-                        }
-                        if (!y_in) {
-                            float us = -ci_b * v_fix / fmax_std(ci_a, 1e-12f);
-                            us = fclamp_std(us, u_lo, u_hi);
-                            m2_h = ci_a * us * us + 2.0f * ci_b * us * v_fix +
-                                   ci_c * v_fix * v_fix;
-                        }
-                        m2_min = fmin_std(m2_v, m2_h);
-                    }
-                    keep = (m2_min <= -2.0f * lt);
-                }
-            }
-        }
+        const bool keep = has && !my_done && mb_keep(g, r0, r1, bp.cull_disabled);
         const uint64_t mask = __ballot(keep);
         ++n_batch;
-        n_kept += (uint64_t)__popcll(mask);
-        // Power coefficients of the AVX2 path (cull_and_blend.cpp:198-200),
-        // computed once per entry in its own lane.
+        n_kept += (uint32_t)__popcll(mask);
+        const uint32_t mA = (uint32_t)mask, mB = (uint32_t)(mask >> 32);
+        uint32_t mine = h ? mB : mA;
+        // power coefficients of the AVX2 path (cull_and_blend.cpp:198-200),
+        // computed once per entry in its own lane
         const float qA = -0.5f * r1.x, qB = -r1.y, qC = -0.5f * r1.z;
-        // Walk the union of both halves' kept entries in depth order; the
-        // entry's parameters are wave-uniform (SGPRs), a half that does not
-        // keep the entry (or is done) is masked off.
-        uint32_t mA = __builtin_amdgcn_readfirstlane((uint32_t)mask);
-        uint32_t mB = __builtin_amdgcn_readfirstlane((uint32_t)(mask >> 32));
         uint32_t uni = mA | mB;
         while (uni) {
             const int j = __builtin_ctz(uni);
             uni &= uni - 1;
-            const bool inA = (mA >> j) & 1u, inB = (mB >> j) & 1u;
-            const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r0.x), j));
-            const float my = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r0.y), j));
-            const float op = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r2.x), j));
-            const float col_r = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r2.y), j));
-            const float col_g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r2.z), j));
-            const float col_b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r2.w), j));
-            // v_readlane reads lane j whatever EXEC is, so every read happens
-            // here, in wave-uniform control flow, before the per-half branch.
-            const float A = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qA), j));
-            const float B = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qB), j));
-            const float C = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qC), j));
+            ++n_iter;
+            // v_readlane reads lane j whatever EXEC is: all reads happen here,
+            // in wave-uniform control flow
+            const float mx = rdl(r0.x, j), my = rdl(r0.y, j);
+            const float op = rdl(r2.x, j);
+            const float col_r = rdl(r2.y, j), col_g = rdl(r2.z, j), col_b = rdl(r2.w, j);
+            const float A = rdl(qA, j), B = rdl(qB, j), C = rdl(qC, j);
             float ci_a = 0.0f, ci_b = 0.0f, ci_c = 0.0f;
-            if (!(fullA && fullB)) {  // image-edge band: scalar-rule parameters
-                ci_a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r1.x), j));
-                ci_b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r1.y), j));
-                ci_c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r1.z), j));
+            if (!INTERIOR) {
+                ci_a = rdl(r1.x, j);
+                ci_b = rdl(r1.y, j);
+                ci_c = rdl(r1.z, j);
             }
-            const bool runA = inA && !doneA, runB = inB && !doneB;
-            if (h ? runB : runA) {
-                if (full) {
-                    const float px_base = pxs - mx;
-                    const float dx = px_base + offx;
+            const bool run = (mine >> j) & 1u;
+            if (run) {
+                if (INTERIOR || g.full) {
+                    const float px_base = g.pxs - mx;
+                    const float dx = px_base + g.offx;
                     const float dx_sq = dx * dx;
-                    const float dy = pyc - my;
+                    const float dy = g.pyc - my;
                     const float y_term = C * dy * dy;
                     const float xy_coef = B * dy;
                     float pwr = __builtin_fmaf(xy_coef, dx, y_term);
@@ -210,9 +218,9 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
                     cg = __builtin_fmaf(at, col_g, cg);
                     cb = __builtin_fmaf(at, col_b, cb);
                     T = T - at;
-                } else if (pix_valid) {
-                    const float dx = pxc - mx;
-                    const float dy = pyc - my;
+                } else if (g.pix_valid) {
+                    const float dx = g.pxc - mx;
+                    const float dy = g.pyc - my;
                     const float power =
                         -0.5f * (ci_a * dx * dx + 2.0f * ci_b * dx * dy + ci_c * dy * dy);
                     const float gw = expf(fmin_std(power, 0.0f));
@@ -223,40 +231,64 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
                     cb += at * col_b;
                     T = T * (1.0f - al);
                 }
+                ++cnt;
             }
-            evals += (runA ? npixA : 0u) + (runB ? npixB : 0u);
-            ++n_iter;
-            bool chkA = false, chkB = false;
-            if (runA) {
-                ++cntA;
-                chkA = fullA ? ((cntA & 3u) == 0u) : true;
-            }
-            if (runB) {
-                ++cntB;
-                chkB = fullB ? ((cntB & 3u) == 0u) : true;
-            }
-            if (chkA || chkB) {
+            // early-out test: every 4 kept entries of a full microblock, after
+            // every entry of an image-edge one (cull_and_blend.cpp:578-616)
+            const bool chk = run && (INTERIOR ? ((cnt & 3u) == 0u) : (!g.full || (cnt & 3u) == 0u));
+            const uint64_t chkm = __ballot(chk);
+            if (chkm != 0) {
                 // max over the microblock's pixels < thr  <=>  no pixel has T >= thr
-                // (T is never NaN; edge pixels outside the image do not vote).
-                const uint64_t live = __ballot(pix_valid && !(T < bp.thr));
-                if (chkA && (uint32_t)live == 0u) doneA = true;
-                if (chkB && (uint32_t)(live >> 32) == 0u) doneB = true;
-                if (doneA && doneB) break;
+                // (T is never NaN; edge pixels outside the image do not vote)
+                const uint64_t live = __ballot((INTERIOR || g.pix_valid) && !(T < bp.thr));
+                const bool deadA = (uint32_t)chkm != 0u && (uint32_t)live == 0u;
+                const bool deadB = (uint32_t)(chkm >> 32) != 0u && (uint32_t)(live >> 32) == 0u;
+                if (deadA) doneA = true;
+                if (deadB) doneB = true;
+                const uint32_t keepA = doneA ? 0u : mA, keepB = doneB ? 0u : mB;
+                uni &= keepA | keepB;
+                mine = h ? keepB : keepA;
+                if (doneA && doneB) return;
             }
         }
     }
+}
 
-    if (bp.evals != nullptr && lane == 0) {
-        // 64 slot groups of 8 counters: spreads the per-wave atomics
-        unsigned long long* slot = bp.evals + (size_t)(blockIdx.x & 63u) * 8;
-        atomicAdd(slot + 0, (unsigned long long)evals);
-        atomicAdd(slot + 1, (unsigned long long)n_batch);
-        atomicAdd(slot + 2, (unsigned long long)n_iter);
-        atomicAdd(slot + 3, (unsigned long long)n_kept);
-        atomicMax(slot + 4, (unsigned long long)n_iter);
+template <int TS, int OUT>
+__global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ brec,
+                                                   const uint32_t* __restrict__ sid,
+                                                   const uint32_t* __restrict__ ranges,
+                                                   BlendParams bp, void* __restrict__ out) {
+    const int lane = threadIdx.x;
+    const Band g = make_band<TS>(bp, lane);
+    float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
+    uint32_t cnt = 0, n_batch = 0, n_iter = 0, n_kept = 0;
+    const uint32_t start = ranges[2 * g.tile], end = ranges[2 * g.tile + 1];
+    if (g.fullA && g.fullB)
+        blend_band<true>(g, brec, sid, start, end, bp, lane, T, cr, cg, cb, cnt, n_batch, n_iter,
+                         n_kept);
+    else
+        blend_band<false>(g, brec, sid, start, end, bp, lane, T, cr, cg, cb, cnt, n_batch, n_iter,
+                          n_kept);
+
+    if (bp.evals != nullptr) {
+        // pixel-Gaussian evaluations = sum over valid pixels of entries blended
+        uint32_t ev = g.pix_valid ? cnt : 0u;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ev += __shfl_xor(ev, o, GS_WAVE);
+        if (lane == 0) {
+            // 64 slot groups of 8 counters: spreads the per-wave atomics
+            unsigned long long* slot = bp.evals + (size_t)(blockIdx.x & 63u) * 8;
+            atomicAdd(slot + 0, (unsigned long long)ev);
+            atomicAdd(slot + 1, (unsigned long long)n_batch);
+            atomicAdd(slot + 2, (unsigned long long)n_iter);
+            atomicAdd(slot + 3, (unsigned long long)n_kept);
+            atomicMax(slot + 4, (unsigned long long)n_iter);
+        }
     }
-    if (!pix_valid) return;
-    const size_t o = ((size_t)(py0 + pi) * bp.width + (size_t)(px_start + pj)) * 3;
+    if (!g.pix_valid) return;
+    const int q = lane & 31, pi = q >> 3, pj = q & 7;
+    const size_t o = ((size_t)(g.py0 + pi) * bp.width + (size_t)(g.px_start + pj)) * 3;
     if (OUT == 2) {
         float* img = static_cast<float*>(out);
         img[o + 0] = cr;

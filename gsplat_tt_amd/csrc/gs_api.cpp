@@ -179,7 +179,8 @@ struct gs_ctx {
         for (DevBuf* b : {&b_mean, &b_cov, &b_opac, &b_col, &b_terms, &b_upload, &b_rect, &b_covc,
                           &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_bstart, &b_pair_tile, &b_pair_id,
                           &b_ranges, &b_out, &b_kalt, &b_valt, &b_hist, &b_state, &b_lb, &b_cnt,
-                          &b_tmp_a, &b_tmp_b, &b_tmp_c, &b_evals})
+                          &b_tmp_a, &b_tmp_b, &b_tmp_c, &b_evals, &b_frame, &b_phist_proj,
+                          &b_phist_emit, &b_rect_r, &b_cov_r})
             b->release();
         if (h_pin) (void)hipHostFree(h_pin);
         for (auto& e : ev)
@@ -397,11 +398,11 @@ struct gs_ctx {
         for (int attempt = 0; attempt < 2; ++attempt) {
             HIPCHK(gs::launch_fill_u32(b_cnt.as<uint32_t>() + 8, 0u, 8, st));
             HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, rparts * 2, st));
-            HIPCHK(gs::launch_rect_count_scan(rect, order, m, nullptr, tp, b_offs.as<uint32_t>(),
-                                              b_bstart.as<uint32_t>(),
+            HIPCHK(gs::launch_rect_count_scan(rect, cov, order, m, nullptr, tp,
+                                              b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(),
                                               (uint32_t)(b_bstart.cap / 4), b_lb.as<uint64_t>(),
                                               b_cnt.as<uint32_t>() + 8, b_cnt.as<uint32_t>() + 9,
-                                              st));
+                                              nullptr, nullptr, st));
             HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
             sync();
             p_pre = h_pin[9];
@@ -429,6 +430,24 @@ struct gs_ctx {
     }
 
     // --------------------------------------------------------- render
+    // Frame-scratch layout (u32 words): counters, histograms, look-back states.
+    static constexpr size_t kFrCnt = 0;         // 64 counters (below)
+    static constexpr size_t kFrDepthHist = 64;  // [4][256] depth-key digits
+    static constexpr size_t kFrTileHist = 64 + 1024;  // [2][256] tile-id digits
+    static constexpr size_t kFrLb = 2048;       // look-back states (u64 each)
+    enum : int {
+        C_PROJ_TICKET = 0, C_M = 1, C_RECT_TICKET = 8, C_PPRE = 9, C_EMIT_TICKET = 10, C_P = 11,
+        C_DSORT_TICKETS = 16, C_TSORT_TICKETS = 24
+    };
+    uint64_t pair_cap = 0;  // candidate-pair capacity of the frame buffers
+    DevBuf b_frame, b_phist_proj, b_phist_emit, b_rect_r, b_cov_r;
+
+    // One frame with no host synchronisation until the end: every size that
+    // only the device knows (visible count, candidate and kept pairs) is read
+    // by the kernels from the counters; grids are sized for capacities (the
+    // scene size, the pair capacity) and partitions beyond the real count exit
+    // at once. If the candidates overflow the pair capacity the frame is run
+    // again with a larger one.
     void render(const gs_view* v, void* out, bool out_dev, gs_stats* stats) {
         const auto t0 = std::chrono::steady_clock::now();
         check_view(v);
@@ -448,89 +467,149 @@ struct gs_ctx {
             dout = b_out.p;
         }
         gs_stats s{};
-        record(0);
-        const int64_t M = run_project(v, false, false);
-        record(1);
-        s.num_visible = M;
-        if (M == 0) {
-            HIPCHK(hipMemsetAsync(dout, 0, px * ebytes, st));
+        const int64_t N = sd.n;
+        ensure_counters();
+        if (N == 0) {
+            HIPCHK(gs::launch_fill_u32(static_cast<uint32_t*>(dout), 0u, px * ebytes / 4, st));
+            if ((px * ebytes) % 4)
+                HIPCHK(hipMemsetAsync(static_cast<char*>(dout) + px * ebytes / 4 * 4, 0,
+                                      (px * ebytes) % 4, st));
             finish(out, dout, out_dev, px * ebytes, stats, s, t0);
             return;
         }
-        // depth order of the visible Gaussians (stable: ties keep index order)
-        ensure_sort(M, 4);
-        HIPCHK(hipStreamSynchronize(st));
-        int passes = 0;
-        void* kf = nullptr;
-        uint32_t* order = nullptr;
-        b_tmp_a.ensure((size_t)M * 4);
-        HIPCHK(gs::radix_sort_pairs(b_dkey.p, b_tmp_a.as<uint32_t>(), M, 4, 0, 32, sort,
-                                    h_pin + 64, st, &passes, true, &kf, &order));
-        record(2);
-        gs::TileParams tp{tiles_x, tiles_y, ts, v->cull_disabled ? 0 : 1};
-        uint64_t p_pre = 0;
-        const uint32_t P = run_tile_assign(b_rect.as<float4>(), b_covc.as<float4>(), order, M, tp,
-                                           &p_pre);
-        record(3);
-        s.pairs_pre = (int64_t)p_pre;
-        s.num_entries = P;
-        // stable tile sort of the depth-ordered pairs
-        ensure_sort(P, 4);
-        void* tiles_sorted = b_pair_tile.p;
-        uint32_t* ids_sorted = b_pair_id.as<uint32_t>();
-        if (P > 0)
-            HIPCHK(gs::radix_sort_pairs(b_pair_tile.p, b_pair_id.as<uint32_t>(), P, 4, 0,
-                                        tile_bits(T), sort, h_pin + 64, st, &passes, false,
-                                        &tiles_sorted, &ids_sorted));
-        b_ranges.ensure((size_t)T * 8);
-        HIPCHK(gs::launch_tile_ranges(static_cast<uint32_t*>(tiles_sorted), P, nullptr,
-                                      b_ranges.as<uint32_t>(), T, st));
-        gs::BlendParams bp{tiles_x, tiles_y, ts, H, W, v->cull_disabled ? 1 : 0,
-                           v->transmittance_threshold, v->out_format, nullptr};
-        if (timing) {
-            b_evals.ensure(64 * 8 * 8);
-            HIPCHK(gs::launch_fill_u32(b_evals.as<uint32_t>(), 0u, 64 * 8 * 2, st));
-            bp.evals = b_evals.as<unsigned long long>();
+        if (pair_cap == 0) pair_cap = std::max<uint64_t>(1u << 20, (uint64_t)N * 4);
+        for (int attempt = 0;; ++attempt) {
+            frame(v, dout, T, tiles_x, tiles_y);
+            if (!out_dev) HIPCHK(hipMemcpyAsync(out, dout, px * ebytes, hipMemcpyDeviceToHost, st));
+            HIPCHK(hipMemcpyAsync(h_pin, b_frame.p, 64 * 4, hipMemcpyDeviceToHost, st));
+            if (timing)
+                HIPCHK(hipMemcpyAsync(h_evals.data(), b_evals.p, 64 * 8 * 8, hipMemcpyDeviceToHost, st));
+            sync();
+            const uint32_t p_pre = h_pin[C_PPRE];
+            if (p_pre == 0xFFFFFFFFu)
+                throw GsError(GS_E_CAPACITY, "render: more than 2^32-1 candidate pairs");
+            if (p_pre <= pair_cap) break;
+            REQUIRE(attempt == 0, "render: pair capacity did not converge");
+            pair_cap = std::min<uint64_t>(0xFFFFFFFFull, (uint64_t)p_pre + p_pre / 8 + 4096);
         }
-        record(4);
-        HIPCHK(gs::launch_blend(b_brec.as<float4>(), ids_sorted, b_ranges.as<uint32_t>(), bp,
-                                dout, st));
-        record(5);
-        finish(out, dout, out_dev, px * ebytes, stats, s, t0);
+        s.num_visible = h_pin[C_M];
+        s.pairs_pre = h_pin[C_PPRE];
+        s.num_entries = h_pin[C_P];
         if (timing) {
             s.ms_project = elapsed(0, 1);
             s.ms_depth_sort = elapsed(1, 2);
             s.ms_tile_assign = elapsed(2, 3);
             s.ms_tile_sort = elapsed(3, 4);
             s.ms_blend = elapsed(4, 5);
-            if (stats) {
-                stats->ms_project = s.ms_project;
-                stats->ms_depth_sort = s.ms_depth_sort;
-                stats->ms_tile_assign = s.ms_tile_assign;
-                stats->ms_tile_sort = s.ms_tile_sort;
-                stats->ms_blend = s.ms_blend;
-            }
+            blend_diag(s);
         }
+        s.ms_total = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() - t0)
+                         .count();
+        if (stats) *stats = s;
+    }
+
+    // Enqueues one frame (project -> depth sort -> tile assign -> tile sort ->
+    // ranges -> blend) on the stream; no host synchronisation.
+    void frame(const gs_view* v, void* dout, int64_t T, int tiles_x, int tiles_y) {
+        const int64_t N = sd.n;
+        const int ts = v->tile_size;
+        const uint32_t pcap = (uint32_t)pair_cap;
+        const size_t pparts = gs::project_partitions(N);
+        const size_t rparts = gs::rect_scan_partitions(N);
+        const size_t eparts = gs::emit_partitions(pcap);
+        // capacities, all allocated before the first launch
+        b_rect.ensure((size_t)N * 16);
+        b_covc.ensure((size_t)N * 16);
+        b_dkey.ensure((size_t)N * 4);
+        b_brec.ensure((size_t)N * 48);
+        b_tmp_a.ensure((size_t)N * 4);
+        b_offs.ensure((size_t)N * 4);
+        b_rect_r.ensure((size_t)N * 16);
+        b_cov_r.ensure((size_t)N * 16);
+        b_bstart.ensure((eparts + 1) * 4);
+        b_pair_tile.ensure((size_t)pcap * 4);
+        b_pair_id.ensure((size_t)pcap * 4);
+        b_ranges.ensure((size_t)T * 8);
+        b_phist_proj.ensure(pparts * 1024 * 4);
+        b_phist_emit.ensure(eparts * 512 * 4);
+        const size_t fwords = kFrLb + 2 * (pparts + rparts + eparts);
+        b_frame.ensure(fwords * 4);
+        ensure_sort(std::max<int64_t>(N, pcap), 4);
+        if (timing) {
+            b_evals.ensure(64 * 8 * 8);
+        }
+        uint32_t* fr = b_frame.as<uint32_t>();
+        uint64_t* lb_proj = reinterpret_cast<uint64_t*>(fr + kFrLb);
+        uint64_t* lb_rect = lb_proj + pparts;
+        uint64_t* lb_emit = lb_rect + rparts;
+        uint32_t* cnt = fr + kFrCnt;
+
+        record(0);
+        HIPCHK(gs::launch_fill_u32(fr, 0u, fwords, st));
+        if (timing) HIPCHK(gs::launch_fill_u32(b_evals.as<uint32_t>(), 0u, 64 * 8 * 2, st));
+        gs::ProjParams p = proj_params(v);
+        gs::Compact c{b_rect.as<float4>(), b_covc.as<float4>(), b_dkey.as<uint32_t>(),
+                      b_brec.as<float4>(), nullptr};
+        HIPCHK(gs::launch_project(sd, p, c, nullptr, lb_proj, cnt + C_PROJ_TICKET, cnt + C_M,
+                                  b_phist_proj.as<uint32_t>(), st));
+        HIPCHK(gs::launch_reduce_rows(b_phist_proj.as<uint32_t>(), 1024, (uint32_t)pparts, nullptr,
+                                      0, 0, fr + kFrDepthHist, st));
+        record(1);
+        // depth order of the visible Gaussians (stable: ties keep index order)
+        void* kf = nullptr;
+        uint32_t* order = nullptr;
+        HIPCHK(gs::radix_sort_pairs_dev(b_dkey.p, b_tmp_a.as<uint32_t>(), N, cnt + C_M, 4, 0, 32,
+                                        fr + kFrDepthHist, cnt + C_DSORT_TICKETS, sort, st, true,
+                                        &kf, &order));
+        record(2);
+        gs::TileParams tp{tiles_x, tiles_y, ts, v->cull_disabled ? 0 : 1};
+        HIPCHK(gs::launch_rect_count_scan(b_rect.as<float4>(), b_covc.as<float4>(), order, N,
+                                          cnt + C_M, tp, b_offs.as<uint32_t>(),
+                                          b_bstart.as<uint32_t>(), (uint32_t)(eparts + 1), lb_rect,
+                                          cnt + C_RECT_TICKET, cnt + C_PPRE,
+                                          b_rect_r.as<float4>(), b_cov_r.as<float4>(), st));
+        HIPCHK(gs::launch_pair_emit(b_rect_r.as<float4>(), b_cov_r.as<float4>(), order,
+                                    b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(), N, cnt + C_M,
+                                    pcap, cnt + C_PPRE, tp, b_pair_tile.as<uint32_t>(),
+                                    b_pair_id.as<uint32_t>(), pcap, lb_emit, cnt + C_EMIT_TICKET,
+                                    cnt + C_P, b_phist_emit.as<uint32_t>(), st));
+        HIPCHK(gs::launch_reduce_rows(b_phist_emit.as<uint32_t>(), 512, (uint32_t)eparts,
+                                      cnt + C_PPRE, pcap, gs::kEmitPartition, fr + kFrTileHist, st));
+        record(3);
+        // stable tile sort of the depth-ordered pairs
+        void* tiles_sorted = nullptr;
+        uint32_t* ids_sorted = nullptr;
+        HIPCHK(gs::radix_sort_pairs_dev(b_pair_tile.p, b_pair_id.as<uint32_t>(), pcap, cnt + C_P, 4,
+                                        0, tile_bits(T), fr + kFrTileHist, cnt + C_TSORT_TICKETS,
+                                        sort, st, false, &tiles_sorted, &ids_sorted));
+        HIPCHK(gs::launch_tile_bounds(static_cast<uint32_t*>(tiles_sorted), pcap, cnt + C_P,
+                                      b_ranges.as<uint32_t>(), T, st));
+        record(4);
+        gs::BlendParams bp{tiles_x, tiles_y, ts, v->image_height, v->image_width,
+                           v->cull_disabled ? 1 : 0, v->transmittance_threshold, v->out_format,
+                           timing ? b_evals.as<unsigned long long>() : nullptr};
+        HIPCHK(gs::launch_blend(b_brec.as<float4>(), ids_sorted, b_ranges.as<uint32_t>(), bp,
+                                dout, st));
+        record(5);
+    }
+
+    void blend_diag(gs_stats& s) {
+        uint64_t e[5] = {0, 0, 0, 0, 0};
+        for (int k = 0; k < 64; ++k) {
+            for (int c = 0; c < 4; ++c) e[c] += h_evals[k * 8 + c];
+            e[4] = std::max<uint64_t>(e[4], h_evals[k * 8 + 4]);
+        }
+        s.blend_evals = (int64_t)e[0];
+        s.blend_batches = (int64_t)e[1];
+        s.blend_iters = (int64_t)e[2];
+        s.blend_kept = (int64_t)e[3];
+        s.blend_max_iters = (int64_t)e[4];
     }
 
     void finish(void* out, void* dout, bool out_dev, size_t bytes, gs_stats* stats, gs_stats s,
                 std::chrono::steady_clock::time_point t0) {
         if (!out_dev) HIPCHK(hipMemcpyAsync(out, dout, bytes, hipMemcpyDeviceToHost, st));
-        if (timing && s.num_entries > 0)
-            HIPCHK(hipMemcpyAsync(h_evals.data(), b_evals.p, 64 * 8 * 8, hipMemcpyDeviceToHost, st));
         sync();
-        if (timing && s.num_entries > 0) {
-            uint64_t e[5] = {0, 0, 0, 0, 0};
-            for (int k = 0; k < 64; ++k) {
-                for (int c = 0; c < 4; ++c) e[c] += h_evals[k * 8 + c];
-                e[4] = std::max<uint64_t>(e[4], h_evals[k * 8 + 4]);
-            }
-            s.blend_evals = (int64_t)e[0];
-            s.blend_batches = (int64_t)e[1];
-            s.blend_iters = (int64_t)e[2];
-            s.blend_kept = (int64_t)e[3];
-            s.blend_max_iters = (int64_t)e[4];
-        }
         s.ms_total = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() - t0)
                          .count();
         if (stats) *stats = s;

@@ -103,19 +103,28 @@ struct TileParams {
 // Sizes: m / p_pre / p are host capacities sizing the grids; when the *_dev
 // pointer is given the real count is read on the device (min with the
 // capacity) and partitions beyond it exit at once.
-hipError_t launch_rect_count_scan(const float4* rect, const uint32_t* order, int64_t m,
-                                  const uint32_t* m_dev, TileParams tp, uint32_t* offs,
+// rect_r / cov_r (optional): rect[order[r]] / cov[order[r]] gathered into
+// rank order (cov_r only with the cull on), the inputs of launch_pair_emit.
+hipError_t launch_rect_count_scan(const float4* rect, const float4* cov, const uint32_t* order,
+                                  int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
                                   uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
-                                  uint32_t* ticket, uint32_t* total_out, hipStream_t st);
-// part_hist (optional): per-partition digit histograms [emit_partitions][2][256]
-// of the kept pairs' tile ids (bits 0-7, 8-15).
-hipError_t launch_pair_emit(const float4* rect, const float4* cov, const uint32_t* order,
+                                  uint32_t* ticket, uint32_t* total_out, float4* rect_r,
+                                  float4* cov_r, hipStream_t st);
+// rect_r / cov_r are indexed by rank (rect[order[r]], ...; the plain arrays
+// when order is null); pair ids are order[r]. part_hist (optional):
+// per-partition digit histograms [emit_partitions][2][256] of the kept pairs'
+// tile ids (bits 0-7, 8-15).
+hipError_t launch_pair_emit(const float4* rect_r, const float4* cov_r, const uint32_t* order,
                             const uint32_t* offs, const uint32_t* bstart, int64_t m,
                             const uint32_t* m_dev, uint32_t p_pre, const uint32_t* p_pre_dev,
                             TileParams tp, uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
                             uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
                             uint32_t* part_hist, hipStream_t st);
 hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, const uint32_t* p_dev,
+                              uint32_t* ranges, int64_t num_tiles, hipStream_t st);
+// Same ranges by per-tile binary search over the sorted tile keys (reads
+// O(tiles * log p) keys instead of all p; no clearing pass).
+hipError_t launch_tile_bounds(const uint32_t* sorted_tile, uint32_t p_cap, const uint32_t* p_dev,
                               uint32_t* ranges, int64_t num_tiles, hipStream_t st);
 // out[c] += sum over rows of part[r][c] (out must be cleared by the caller).
 hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,

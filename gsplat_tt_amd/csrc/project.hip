@@ -21,6 +21,7 @@ namespace {
 constexpr int kProjThreads = 256;
 constexpr int kProjItems = 4;
 constexpr int kProjPart = kProjThreads * kProjItems;
+static_assert(kProjPart == (int)kProjPartition, "project partition size is part of the interface");
 
 __device__ __forceinline__ float fmin_std(float a, float b) { return (b < a) ? b : a; }
 __device__ __forceinline__ float fmax_std(float a, float b) { return (a < b) ? b : a; }

@@ -24,6 +24,7 @@ constexpr int kCountItems = 4;
 constexpr int kCountPart = kThreads * kCountItems;   // ranks per scan partition
 constexpr int kEmitItems = 8;
 constexpr int kEmitPart = kThreads * kEmitItems;     // candidates per emit partition
+static_assert(kEmitPart == (int)kEmitPartition, "emit partition size is part of the interface");
 
 __device__ __forceinline__ float fmin_std(float a, float b) { return (b < a) ? b : a; }
 __device__ __forceinline__ float fmax_std(float a, float b) { return (a < b) ? b : a; }
@@ -59,15 +60,15 @@ __device__ __forceinline__ Rect tile_rect(float4 r, const TileParams& tp) {
 }
 
 // tile_assign.cpp:151-290, one (Gaussian, tile) pair.
-__device__ __forceinline__ bool pair_keep(float px, float py, float4 cv, int tile_id,
+__device__ __forceinline__ bool pair_keep(float px, float py, float4 cv, int tile_x, int tile_y,
                                           const TileParams& tp) {
     const float m2thr = cv.w;
     if (!(m2thr >= 0.0f)) return false;  // opacity <= floor
     const float a = cv.x, b = cv.y, c = cv.z;
     const float det = fmax_std(a * c - b * b, 1e-6f);
     const float ts = (float)tp.tile_size;
-    const float tx_tile = (float)(tile_id % tp.tiles_x) * ts;
-    const float ty_tile = (float)(tile_id / tp.tiles_x) * ts;
+    const float tx_tile = (float)tile_x * ts;
+    const float ty_tile = (float)tile_y * ts;
     const float u_lo = tx_tile - px;
     const float u_hi = u_lo + ts;
     const float v_lo = ty_tile - py;
@@ -97,8 +98,10 @@ __device__ __forceinline__ bool pair_keep(float px, float py, float4 cv, int til
 // Rectangle area per rank, exclusive scan -> offs[r]; last partition writes
 // the total candidate count (saturated to 0xFFFFFFFF on overflow).
 // Also records, for every emit partition b (candidates [b*kEmitPart, ...)),
-// the rank that owns its first candidate: bstart[b].
+// the rank that owns its first candidate: bstart[b]. With rect_r / cov_r
+// given, the rectangles and conics are also gathered into rank order.
 __global__ __launch_bounds__(kThreads) void k_rect_count_scan(const float4* __restrict__ rect,
+                                                              const float4* __restrict__ cov,
                                                               const uint32_t* __restrict__ order,
                                                               int64_t m_cap,
                                                               const uint32_t* __restrict__ m_dev,
@@ -108,7 +111,9 @@ __global__ __launch_bounds__(kThreads) void k_rect_count_scan(const float4* __re
                                                               uint32_t bstart_cap,
                                                               uint64_t* lb_state,
                                                               uint32_t* ticket,
-                                                              uint32_t* total_out) {
+                                                              uint32_t* total_out,
+                                                              float4* __restrict__ rect_r,
+                                                              float4* __restrict__ cov_r) {
     __shared__ uint32_t s_vid;
     __shared__ uint32_t s_wsum[kCountItems][kWaves];
     __shared__ uint64_t s_excl;
@@ -128,8 +133,13 @@ __global__ __launch_bounds__(kThreads) void k_rect_count_scan(const float4* __re
         uint32_t c = 0;
         if (r < m) {
             const uint32_t g = order ? order[r] : (uint32_t)r;
-            const Rect q = tile_rect(rect[g], tp);
+            const float4 rr = rect[g];
+            const Rect q = tile_rect(rr, tp);
             c = (uint32_t)((q.x1 - q.x0 + 1) * (q.y1 - q.y0 + 1));
+            if (rect_r != nullptr) {
+                rect_r[r] = rr;
+                if (tp.cull) cov_r[r] = cov[g];
+            }
         }
         cnt[it] = c;
         incl[it] = wave_incl_scan(c);
@@ -175,7 +185,7 @@ __global__ __launch_bounds__(kThreads) void k_rect_count_scan(const float4* __re
 // partition are [bstart[vid], bstart[vid+1]]; each candidate finds its rank by
 // an inclusive max-scan over rank heads in LDS.
 __global__ __launch_bounds__(kThreads) void k_pair_emit(
-    const float4* __restrict__ rect, const float4* __restrict__ cov,
+    const float4* __restrict__ rect_r, const float4* __restrict__ cov_r,
     const uint32_t* __restrict__ order, const uint32_t* __restrict__ offs,
     const uint32_t* __restrict__ bstart, int64_t m_cap, const uint32_t* __restrict__ m_dev,
     uint32_t p_pre_cap, const uint32_t* __restrict__ p_pre_dev, TileParams tp,
@@ -214,7 +224,7 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     for (int64_t k = tid; k < nr; k += kThreads) {
         const int64_t r = rlo + k;
         const uint32_t g = order ? order[r] : (uint32_t)r;
-        const Rect q = tile_rect(rect[g], tp);
+        const Rect q = tile_rect(rect_r[r], tp);
         const uint32_t o = offs[r];
         s_off[k] = o;
         s_g[k] = g;
@@ -264,12 +274,15 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
             const uint32_t xy = s_xy[lo];
             uint32_t row, col;
             divmod_small(j, wdt, row, col);
-            const int t = (int)((xy >> 16) + row) * tp.tiles_x + (int)((xy & 0xFFFFu) + col);
+            const int ty = (int)((xy >> 16) + row), tx = (int)((xy & 0xFFFFu) + col);
+            const int t = ty * tp.tiles_x + tx;
             const uint32_t g = s_g[lo];
             bool k = true;
             if (tp.cull) {
-                const float4 rr = rect[g];
-                k = pair_keep(rr.x, rr.y, cov[g], t, tp);
+                // rank-ordered records: the partition's few ranks stay in L1
+                const int64_t r = rlo + lo;
+                const float4 rr = rect_r[r];
+                k = pair_keep(rr.x, rr.y, cov_r[r], tx, ty, tp);
             }
             keep[it] = k;
             tile[it] = (uint32_t)t;
@@ -331,23 +344,75 @@ __global__ void k_tile_ranges(const uint32_t* __restrict__ st, uint32_t p_cap,
     }
 }
 
-// out[c] += sum of rows [y*64, y*64+64) of part (rows x cols), rows bounded by
-// ceil(min(*count_dev, count_cap) / per_row) when count_dev is given.
+// First index in [0, p) whose key is >= t, by a wave-wide 64-ary search
+// (about log64(p) dependent loads). Keys are sorted ascending.
+__device__ __forceinline__ uint32_t wave_lower_bound(const uint32_t* __restrict__ keys,
+                                                     uint32_t p, uint32_t t, int lane) {
+    uint32_t lo = 0, hi = p;  // answer in [lo, hi]
+    while (hi - lo > (uint32_t)GS_WAVE) {
+        const uint32_t step = (hi - lo + GS_WAVE - 1) / GS_WAVE;
+        const uint64_t q = (uint64_t)lo + (uint64_t)(lane + 1) * step - 1;
+        const bool pred = q < hi && keys[q] < t;
+        const uint32_t c = (uint32_t)__popcll(__ballot(pred));
+        const uint64_t nhi = (uint64_t)lo + (uint64_t)(c + 1) * step - 1;
+        lo += c * step;
+        hi = (uint32_t)min((uint64_t)hi, nhi);
+    }
+    const uint32_t q = lo + (uint32_t)lane;
+    const bool pred = q < hi && keys[q] < t;
+    return lo + (uint32_t)__popcll(__ballot(pred));
+}
+
+// ranges[t] = [first, end) of tile t in the tile-sorted pairs, (0, 0) when
+// empty; one wave per tile, no clearing pass needed.
+__global__ __launch_bounds__(256) void k_tile_bounds(const uint32_t* __restrict__ st,
+                                                     uint32_t p_cap,
+                                                     const uint32_t* __restrict__ p_dev,
+                                                     uint32_t* __restrict__ ranges,
+                                                     uint32_t num_tiles) {
+    const uint32_t p = p_dev ? min(p_cap, *p_dev) : p_cap;
+    const uint32_t t = blockIdx.x * (256 / GS_WAVE) + threadIdx.x / GS_WAVE;
+    const int lane = lane_id();
+    if (t >= num_tiles) return;
+    const uint32_t a = wave_lower_bound(st, p, t, lane);
+    const uint32_t b = wave_lower_bound(st, p, t + 1, lane);
+    if (lane == 0) {
+        ranges[2 * (size_t)t] = a < b ? a : 0u;
+        ranges[2 * (size_t)t + 1] = a < b ? b : 0u;
+    }
+}
+
+// out[c] += sum of rows [y*kRedRows, ...) of part (rows x cols, cols % 4 == 0),
+// rows bounded by ceil(min(*count_dev, count_cap) / per_row) when count_dev is
+// given. One thread per 4 columns, 16-byte loads, 8 rows in flight.
+constexpr int kRedRows = 32;
 __global__ void k_reduce_rows(const uint32_t* __restrict__ part, int cols, uint32_t rows_cap,
                               const uint32_t* __restrict__ count_dev, uint32_t count_cap,
                               uint32_t per_row, uint32_t* __restrict__ out) {
     uint32_t rows = rows_cap;
     if (count_dev) {
         const uint32_t c = min(*count_dev, count_cap);
-        rows = min(rows_cap, (c + per_row - 1) / per_row);
+        rows = min(rows_cap, (uint32_t)(((uint64_t)c + per_row - 1) / per_row));
     }
-    const int col = blockIdx.x * blockDim.x + threadIdx.x;
-    const uint32_t r0 = blockIdx.y * 64u;
-    if (col >= cols || r0 >= rows) return;
-    const uint32_t r1 = min(rows, r0 + 64u);
-    uint32_t acc = 0;
-    for (uint32_t r = r0; r < r1; ++r) acc += part[(size_t)r * cols + col];
-    if (acc) atomicAdd(&out[col], acc);
+    const int c4 = blockIdx.x * blockDim.x + threadIdx.x;  // column quad
+    const uint32_t r0 = blockIdx.y * (uint32_t)kRedRows;
+    if (c4 * 4 >= cols || r0 >= rows) return;
+    const uint32_t r1 = min(rows, r0 + (uint32_t)kRedRows);
+    const uint4* p = reinterpret_cast<const uint4*>(part) + (size_t)r0 * (cols / 4) + c4;
+    uint4 acc = make_uint4(0, 0, 0, 0);
+#pragma unroll 8
+    for (uint32_t r = r0; r < r1; ++r, p += cols / 4) {
+        const uint4 v = *p;
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+    }
+    uint32_t* o = out + c4 * 4;
+    if (acc.x) atomicAdd(o + 0, acc.x);
+    if (acc.y) atomicAdd(o + 1, acc.y);
+    if (acc.z) atomicAdd(o + 2, acc.z);
+    if (acc.w) atomicAdd(o + 3, acc.w);
 }
 
 // key = (tile << 32) | fp32 depth bits of the pair's Gaussian (sort.cpp:180-205).
@@ -388,18 +453,20 @@ hipError_t launch_tile_ranges64(const uint64_t* keys, uint32_t p, uint32_t* rang
 size_t rect_scan_partitions(int64_t m) { return (size_t)((m + kCountPart - 1) / kCountPart); }
 size_t emit_partitions(uint64_t p_pre) { return (size_t)((p_pre + kEmitPart - 1) / kEmitPart); }
 
-hipError_t launch_rect_count_scan(const float4* rect, const uint32_t* order, int64_t m,
-                                  const uint32_t* m_dev, TileParams tp, uint32_t* offs,
+hipError_t launch_rect_count_scan(const float4* rect, const float4* cov, const uint32_t* order,
+                                  int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
                                   uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
-                                  uint32_t* ticket, uint32_t* total_out, hipStream_t st) {
+                                  uint32_t* ticket, uint32_t* total_out, float4* rect_r,
+                                  float4* cov_r, hipStream_t st) {
     if (m <= 0) return hipSuccess;
     const unsigned grid = (unsigned)rect_scan_partitions(m);
-    k_rect_count_scan<<<grid, kThreads, 0, st>>>(rect, order, m, m_dev, tp, offs, bstart,
-                                                 bstart_cap, lb_state, ticket, total_out);
+    k_rect_count_scan<<<grid, kThreads, 0, st>>>(rect, cov, order, m, m_dev, tp, offs, bstart,
+                                                 bstart_cap, lb_state, ticket, total_out, rect_r,
+                                                 cov_r);
     return hipGetLastError();
 }
 
-hipError_t launch_pair_emit(const float4* rect, const float4* cov, const uint32_t* order,
+hipError_t launch_pair_emit(const float4* rect_r, const float4* cov_r, const uint32_t* order,
                             const uint32_t* offs, const uint32_t* bstart, int64_t m,
                             const uint32_t* m_dev, uint32_t p_pre, const uint32_t* p_pre_dev,
                             TileParams tp, uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
@@ -407,7 +474,7 @@ hipError_t launch_pair_emit(const float4* rect, const float4* cov, const uint32_
                             uint32_t* part_hist, hipStream_t st) {
     if (p_pre == 0 || m <= 0) return hipSuccess;
     const unsigned grid = (unsigned)emit_partitions(p_pre);
-    k_pair_emit<<<grid, kThreads, 0, st>>>(rect, cov, order, offs, bstart, m, m_dev, p_pre,
+    k_pair_emit<<<grid, kThreads, 0, st>>>(rect_r, cov_r, order, offs, bstart, m, m_dev, p_pre,
                                            p_pre_dev, tp, pair_tile, pair_id, cap, lb_state,
                                            ticket, total_out, part_hist);
     return hipGetLastError();
@@ -422,12 +489,24 @@ hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, const uin
     return hipGetLastError();
 }
 
+hipError_t launch_tile_bounds(const uint32_t* sorted_tile, uint32_t p_cap, const uint32_t* p_dev,
+                              uint32_t* ranges, int64_t num_tiles, hipStream_t st) {
+    if (num_tiles <= 0) return hipSuccess;
+    const unsigned grid = (unsigned)((num_tiles + 3) / 4);
+    k_tile_bounds<<<grid, 256, 0, st>>>(sorted_tile, p_cap, p_dev, ranges, (uint32_t)num_tiles);
+    return hipGetLastError();
+}
+
 hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,
                               const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
                               uint32_t* out, hipStream_t st) {
     if (rows_cap == 0) return hipSuccess;
-    dim3 grid((cols + 255) / 256, (rows_cap + 63) / 64);
-    k_reduce_rows<<<grid, 256, 0, st>>>(part, cols, rows_cap, count_dev, count_cap, per_row, out);
+    if (cols % 4 != 0) return hipErrorInvalidValue;
+    const int quads = cols / 4;
+    const int block = std::min(quads, 256);
+    dim3 grid((quads + block - 1) / block, (rows_cap + kRedRows - 1) / kRedRows);
+    k_reduce_rows<<<grid, block, 0, st>>>(part, cols, rows_cap, count_dev, count_cap, per_row,
+                                          out);
     return hipGetLastError();
 }
 
