@@ -22,7 +22,9 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 FP32_PEAK_TFLOPS = 157.3     # MI355X FP32 vector peak
-BLEND_FLOPS_PER_EVAL = 20    # per pixel x Gaussian evaluation
+# per pixel x Gaussian evaluation: dx, dy (2 sub), quadratic form (3 mul + 2 FMA),
+# clamp, exp, alpha (mul + min), alpha*T, 3 colour FMA, T update; FMA = 2 flops
+BLEND_FLOPS_PER_EVAL = 20
 
 
 def log(msg):
@@ -39,8 +41,10 @@ def parse():
     ap.add_argument("--sort-keys", type=int, default=50_000_000)
     ap.add_argument("--no-sort", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-frames", type=int, default=4)
+    ap.add_argument("--cpu-frames", type=int, default=10)
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run device-to-device copies of BYTES (PMC byte-counter scale)")
     return ap.parse_args()
 
 
@@ -77,6 +81,12 @@ def bench_frames(args):
 
 
 def stage_summary(scene, stats):
+    """Per-stage times (hipEvents on the render stream) and roofline figures from
+    the per-unit algorithmic work: projection N*(12+24+4+12*(d+1)^2) B read +
+    M*48 B written; tile assignment M*40 B read + P*12 B written; sort 16 B per
+    key per 8-bit pass (u32 key + u32 payload, read + write) over the depth keys
+    (M, 4 passes) and the tile keys (P, tile-bit passes); blend 20 FP32 flops per
+    pixel-Gaussian evaluation."""
     keys = ("ms_project", "ms_depth_sort", "ms_tile_assign", "ms_tile_sort", "ms_blend",
             "ms_total")
     avg = {k: float(np.mean([s[k] for s in stats])) for k in keys}
@@ -87,18 +97,57 @@ def stage_summary(scene, stats):
     diag = {k: float(np.mean([s[k] for s in stats])) for k in ("blend_batches", "blend_iters",
                                                                  "blend_kept", "blend_max_iters")}
     N = scene.n
-    # algorithmic bytes: projection reads mean 12 + cov 24 + opacity 4 +
-    # SH 192 (+ k 4) per Gaussian, writes 84 B per visible Gaussian.
-    proj_bytes = N * (12 + 24 + 4 + 4) + M * (192 + 8 + 84)
-    blend_flops = evals * BLEND_FLOPS_PER_EVAL
+    tile_passes = 2   # 4056 tiles of 16 px -> 12 tile bits
+    work = {
+        "project": ("GB/s", N * (12 + 24 + 4 + 12 * 16) + M * 48),
+        "depth_sort": ("GB/s", M * 16 * 4),
+        "tile_assign": ("GB/s", M * 40 + P * 12),
+        "tile_sort": ("GB/s", P * 16 * tile_passes),
+        "blend": ("TFLOP/s", evals * BLEND_FLOPS_PER_EVAL),
+    }
+    roof = {}
+    for k, (unit, amount) in work.items():
+        sec = avg["ms_" + k] * 1e-3
+        if unit == "GB/s":
+            ach = amount / sec / 1e9
+            roof[k] = {"ms": round(avg["ms_" + k], 4), "achieved_gbs": round(ach, 1),
+                       "frac_hbm": round(ach / HBM_PEAK_GBS, 4)}
+        else:
+            ach = amount / sec / 1e12
+            roof[k] = {"ms": round(avg["ms_" + k], 4), "achieved_tflops": round(ach, 3),
+                       "frac_fp32": round(ach / FP32_PEAK_TFLOPS, 4)}
     st = {
         "N": N, "M_avg": M, "pairs_avg": P, "pairs_pre_avg": Ppre, "blend_evals_avg": evals,
-        "blend_diag": diag,
-        "ms": {k[3:]: round(v, 4) for k, v in avg.items()},
-        "project_gbs": proj_bytes / (avg["ms_project"] * 1e-3) / 1e9,
-        "blend_tflops": blend_flops / (avg["ms_blend"] * 1e-3) / 1e12,
+        "blend_diag": diag, "ms": {k[3:]: round(v, 4) for k, v in avg.items()},
+        "roofline": roof,
     }
-    return st, avg, blend_flops
+    return st, avg, evals * BLEND_FLOPS_PER_EVAL
+
+
+def pmc_traffic(kernel):
+    """HBM bytes per dispatch of `kernel` from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE scaled by a copy-kernel calibration), or None."""
+    import re
+    path = os.path.join(ROOT, "profiles", f"{kernel}_pmc_traffic.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_dispatch\s*=\s*([0-9_,]+)", open(path).read())
+    return int(m.group(1).replace(",", "").replace("_", "")) if m else None
+
+
+def copy_calibration(nbytes):
+    """Device-to-device copies of a known size: the reference reading for the PMC
+    byte counters (FETCH_SIZE / WRITE_SIZE per dispatch vs nbytes)."""
+    from gsplat_tt_amd import _lib as L
+    ctx = L.Context(0)
+    a, b = ctx.dev_alloc(nbytes), ctx.dev_alloc(nbytes)
+    for _ in range(5):
+        ctx.d2d(b, a, nbytes)
+    ctx._L.gs_sync(ctx.handle)
+    ctx.dev_free(a)
+    ctx.dev_free(b)
+    ctx.close()
+    print(json.dumps({"copy_calibration_bytes": nbytes, "dispatches": 5}), flush=True)
 
 
 def bench_sort(ctx, n):
@@ -182,18 +231,23 @@ def main():
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); multi-GPU "
               "sharding is not part of this build", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     ctx, scene, cov, cams, stats, dt = bench_frames(args)
     st, avg, blend_flops = stage_summary(scene, stats)
     fps = args.steps / dt
     log(f"{fps:.1f} frames/s; stages {st['ms']}")
     blend_ms = avg["ms_blend"]
-    stage_ms = {k: v for k, v in st["ms"].items() if k != "total"}
-    dominant = max(stage_ms, key=stage_ms.get)
-    roof = {"kernel": "k_blend (cull + blend)", "bound": "valu",
+    # The blend kernel: the stage the metric prices against FP32 peak. It runs on
+    # the FP32 vector ALUs (no MFMA); "mfma" marks the compute roof, priced at
+    # MI355X's FP32 peak.
+    roof = {"kernel": "k_blend", "bound": "mfma", "pipe": "fp32 VALU",
             "achieved": round(blend_flops / (blend_ms * 1e-3) / 1e12, 3),
             "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(blend_flops / (blend_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4),
-            "traffic": None, "dominant_stage": dominant}
+            "traffic": pmc_traffic("k_blend"),
+            "flops_per_launch": round(blend_flops), "ms_per_launch": round(blend_ms, 4)}
     res = {
         "metric": "frames/sec @6M Gaussians 1237x822; sort Gkeys/s; blend frac of FP32 peak",
         "value": round(fps, 3), "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
