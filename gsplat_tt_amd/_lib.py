@@ -23,7 +23,11 @@ EXPORTED = (
     "gs_scene_set", "gs_render", "gs_project", "gs_tile_assign", "gs_sort_and_bin",
     "gs_cull_and_blend", "gs_sort_pairs_u64_dev", "gs_last_sort_pass_ms", "gs_dev_alloc",
     "gs_dev_free", "gs_memcpy_h2d", "gs_memcpy_d2h", "gs_memcpy_d2d", "gs_sync",
+    "gs_train_init", "gs_train_read", "gs_train_write", "gs_train_set_step",
+    "gs_train_set_visible", "gs_train_forward", "gs_train_backward", "gs_train_adam",
+    "gs_train_step",
 )
+TRAIN_PARAMS = ("means", "log_scales", "quats", "opacity_logits", "sh")
 
 
 class GsScene(ctypes.Structure):
@@ -55,6 +59,56 @@ class GsStats(ctypes.Structure):
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+class GsTrainArrays(ctypes.Structure):
+    _fields_ = [(k, ctypes.c_void_p) for k in ("means", "log_scales", "quats", "opacity_logits",
+                                                "sh")]
+
+
+class GsTrainCfg(ctypes.Structure):
+    _fields_ = [("near_plane", ctypes.c_float), ("lowpass", ctypes.c_float),
+                ("alpha_max", ctypes.c_float), ("alpha_min", ctypes.c_float),
+                ("t_min", ctypes.c_float), ("background", ctypes.c_float * 3),
+                ("loss_scale", ctypes.c_float),
+                ("lr_means", ctypes.c_double), ("lr_log_scales", ctypes.c_double),
+                ("lr_quats", ctypes.c_double), ("lr_opacity", ctypes.c_double),
+                ("lr_sh_dc", ctypes.c_double), ("lr_sh_rest", ctypes.c_double),
+                ("beta1", ctypes.c_double), ("beta2", ctypes.c_double), ("eps", ctypes.c_double)]
+
+
+class GsTrainStats(ctypes.Structure):
+    _fields_ = [("num_blendable", ctypes.c_int64), ("num_entries", ctypes.c_int64),
+                ("step", ctypes.c_int64), ("loss", ctypes.c_double),
+                ("ms_forward", ctypes.c_float), ("ms_backward", ctypes.c_float),
+                ("ms_adam", ctypes.c_float), ("ms_total", ctypes.c_float)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+class GsTrainProj(ctypes.Structure):
+    _fields_ = [(k, ctypes.c_void_p) for k in ("means2d", "conic", "opacity", "colors", "depth",
+                                                "valid", "visible")]
+
+
+def make_train_cfg(near=0.2, lowpass=0.3, alpha_max=0.99, alpha_min=1.0 / 255.0, t_min=1e-4,
+                   background=(0.0, 0.0, 0.0), loss_scale=1.0, lr=None, betas=(0.9, 0.999),
+                   eps=1e-15) -> GsTrainCfg:
+    """Training configuration: gsplat/train_oracle.py RenderConfig (:63-71) and the
+    3DGS learning rates of DEFAULT_LR (:421-423)."""
+    lr = dict({"means": 1.6e-4, "log_scales": 5e-3, "quats": 1e-3, "opacity_logits": 0.05,
+               "sh_dc": 2.5e-3, "sh_rest": 2.5e-3 / 20.0}, **(lr or {}))
+    c = GsTrainCfg()
+    c.near_plane, c.lowpass, c.alpha_max, c.alpha_min, c.t_min = near, lowpass, alpha_max, \
+        alpha_min, t_min
+    for i in range(3):
+        c.background[i] = float(background[i])
+    c.loss_scale = float(loss_scale)
+    c.lr_means, c.lr_log_scales, c.lr_quats = lr["means"], lr["log_scales"], lr["quats"]
+    c.lr_opacity, c.lr_sh_dc, c.lr_sh_rest = lr["opacity_logits"], lr["sh_dc"], lr["sh_rest"]
+    c.beta1, c.beta2, c.eps = float(betas[0]), float(betas[1]), float(eps)
+    return c
 
 
 _LIB = None
@@ -308,3 +362,104 @@ class Context:
             self.dev_free(dk)
             self.dev_free(dv)
         return ko, vo, passes
+
+
+class Trainer:
+    """Training on the GPU (forward with the 3DGS rules, L1, backward, sparse Adam)
+    through the gs_train_* entry points of one Context. Parameters are dicts of
+    numpy arrays in optimizer space: means (n,3), log_scales (n,3), quats (n,4),
+    opacity_logits (n,), sh (n,(d+1)^2,3)."""
+
+    def __init__(self, ctx: "Context", params: dict, sh_degree: int):
+        self.ctx, self._L = ctx, ctx._L
+        self.n = int(np.asarray(params["means"]).shape[0])
+        self.deg = int(sh_degree)
+        self.K = (self.deg + 1) ** 2
+        arrs, keep = self._arrays(params)
+        _check(self._L.gs_train_init(ctx.handle, ctypes.byref(arrs), ctypes.c_int64(self.n),
+                                     self.deg))
+
+    def _shapes(self):
+        n, K = self.n, self.K
+        return {"means": (n, 3), "log_scales": (n, 3), "quats": (n, 4), "opacity_logits": (n,),
+                "sh": (n, K, 3)}
+
+    def _arrays(self, params):
+        keep = {}
+        a = GsTrainArrays()
+        for k, shp in self._shapes().items():
+            arr = np.ascontiguousarray(np.asarray(params[k], np.float32).reshape(shp))
+            keep[k] = arr
+            setattr(a, k, arr.ctypes.data)
+        return a, keep
+
+    def read(self, which=0) -> dict:
+        """which: 0 parameters, 1 first moments, 2 second moments, 3 gradients."""
+        out = {k: np.empty(shp, np.float32) for k, shp in self._shapes().items()}
+        a, _ = self._arrays(out)
+        for k in out:   # _arrays copies only when needed; bind the real buffers
+            setattr(a, k, out[k].ctypes.data)
+        _check(self._L.gs_train_read(self.ctx.handle, int(which), ctypes.byref(a)))
+        return out
+
+    def write(self, which, arrays: dict):
+        a, keep = self._arrays(arrays)
+        _check(self._L.gs_train_write(self.ctx.handle, int(which), ctypes.byref(a)))
+
+    def set_step(self, step: int):
+        _check(self._L.gs_train_set_step(self.ctx.handle, ctypes.c_int64(step)))
+
+    def set_visible(self, visible):
+        v = np.ascontiguousarray(np.asarray(visible, bool).astype(np.uint8))
+        _check(self._L.gs_train_set_visible(self.ctx.handle, _ptr(v)))
+
+    def forward(self, view: GsView, cfg: GsTrainCfg, target=None, want_proj=False):
+        H, W = view.image_height, view.image_width
+        img = np.empty((H, W, 3), np.float32)
+        T = np.empty((H, W), np.float32)
+        tgt = None if target is None else _f32(target).reshape(H, W, 3)
+        proj = None
+        pj = None
+        if want_proj:
+            n = self.n
+            proj = dict(means2d=np.empty((n, 2), np.float32), conic=np.empty((n, 3), np.float32),
+                        opacity=np.empty(n, np.float32), colors=np.empty((n, 3), np.float32),
+                        depth=np.empty(n, np.float32), valid=np.empty(n, np.uint8),
+                        visible=np.empty(n, np.uint8))
+            pj = GsTrainProj()
+            for k, v in proj.items():
+                setattr(pj, k, v.ctypes.data)
+        st = GsTrainStats()
+        _check(self._L.gs_train_forward(self.ctx.handle, ctypes.byref(view), ctypes.byref(cfg),
+                                        _ptr(tgt), _ptr(img), _ptr(T),
+                                        ctypes.byref(pj) if pj is not None else None,
+                                        ctypes.byref(st)))
+        if proj is not None:
+            proj["valid"] = proj["valid"].astype(bool)
+            proj["visible"] = proj["visible"].astype(bool)
+        return img, T, proj, st.as_dict()
+
+    def backward(self, cfg: GsTrainCfg, dimage=None, want_g2d=False):
+        g2d = np.empty((self.n, 9), np.float32) if want_g2d else None
+        d = None if dimage is None else _f32(dimage)
+        st = GsTrainStats()
+        _check(self._L.gs_train_backward(self.ctx.handle, ctypes.byref(cfg), _ptr(d), _ptr(g2d),
+                                         ctypes.byref(st)))
+        return g2d, st.as_dict()
+
+    def adam(self, cfg: GsTrainCfg):
+        st = GsTrainStats()
+        _check(self._L.gs_train_adam(self.ctx.handle, ctypes.byref(cfg), ctypes.byref(st)))
+        return st.as_dict()
+
+    def step(self, view: GsView, cfg: GsTrainCfg, target, target_on_device=False):
+        st = GsTrainStats()
+        if target_on_device:
+            ptr = ctypes.c_void_p(int(target))
+            keep = None
+        else:
+            keep = _f32(target)
+            ptr = _ptr(keep)
+        _check(self._L.gs_train_step(self.ctx.handle, ctypes.byref(view), ctypes.byref(cfg), ptr,
+                                     int(bool(target_on_device)), ctypes.byref(st)))
+        return st.as_dict()

@@ -187,6 +187,11 @@ struct gs_ctx {
             if (e) (void)hipEventDestroy(e);
         for (auto& e : sort_ev)
             if (e) (void)hipEventDestroy(e);
+        for (auto& e : tev)
+            if (e) (void)hipEventDestroy(e);
+        for (DevBuf* b : {&t_p, &t_m, &t_v, &t_g, &t_cidx, &t_vis, &t_grad2d, &t_img, &t_T, &t_stop,
+                          &t_dimg, &t_tgt, &t_loss, &t_dbg})
+            b->release();
         if (st) (void)hipStreamDestroy(st);
     }
 
@@ -350,7 +355,9 @@ struct gs_ctx {
     }
 
     void record(int i) {
-        if (timing) HIPCHK(hipEventRecord(ev[i], st));
+        if (!timing) return;
+        if (!ev[i]) HIPCHK(hipEventCreate(&ev[i]));
+        HIPCHK(hipEventRecord(ev[i], st));
     }
     float elapsed(int a, int b) {
         if (!timing) return 0.0f;
@@ -450,6 +457,7 @@ struct gs_ctx {
     // again with a larger one.
     void render(const gs_view* v, void* out, bool out_dev, gs_stats* stats) {
         const auto t0 = std::chrono::steady_clock::now();
+        tr.fwd_valid = false;  // the frame buffers are about to be reused
         check_view(v);
         REQUIRE(out != nullptr, "render: null output");
         ensure_terms(v);
@@ -510,51 +518,55 @@ struct gs_ctx {
 
     // Enqueues one frame (project -> depth sort -> tile assign -> tile sort ->
     // ranges -> blend) on the stream; no host synchronisation.
-    void frame(const gs_view* v, void* dout, int64_t T, int tiles_x, int tiles_y) {
-        const int64_t N = sd.n;
-        const int ts = v->tile_size;
-        const uint32_t pcap = (uint32_t)pair_cap;
-        const size_t pparts = gs::project_partitions(N);
-        const size_t rparts = gs::rect_scan_partitions(N);
-        const size_t eparts = gs::emit_partitions(pcap);
-        // capacities, all allocated before the first launch
+    // Frame buffers for N Gaussians, T tiles and the current pair capacity, all
+    // allocated before the first launch of a frame.
+    struct FrameLayout {
+        uint32_t* fr;
+        uint32_t* cnt;
+        uint64_t *lb_proj, *lb_rect, *lb_emit;
+        size_t fwords, pparts, rparts, eparts;
+        uint32_t pcap;
+    };
+    FrameLayout frame_prepare(int64_t N, int64_t T) {
+        FrameLayout L{};
+        L.pcap = (uint32_t)pair_cap;
+        L.pparts = gs::project_partitions(N);
+        L.rparts = gs::rect_scan_partitions(N);
+        L.eparts = gs::emit_partitions(L.pcap);
         b_rect.ensure((size_t)N * 16);
         b_covc.ensure((size_t)N * 16);
         b_dkey.ensure((size_t)N * 4);
         b_brec.ensure((size_t)N * 48);
+        b_src.ensure((size_t)N * 4);
         b_tmp_a.ensure((size_t)N * 4);
         b_offs.ensure((size_t)N * 4);
         b_rect_r.ensure((size_t)N * 16);
         b_cov_r.ensure((size_t)N * 16);
-        b_bstart.ensure((eparts + 1) * 4);
-        b_pair_tile.ensure((size_t)pcap * 4);
-        b_pair_id.ensure((size_t)pcap * 4);
+        b_bstart.ensure((L.eparts + 1) * 4);
+        b_pair_tile.ensure((size_t)L.pcap * 4);
+        b_pair_id.ensure((size_t)L.pcap * 4);
         b_ranges.ensure((size_t)T * 8);
-        b_phist_proj.ensure(pparts * 1024 * 4);
-        b_phist_emit.ensure(eparts * 512 * 4);
-        const size_t fwords = kFrLb + 2 * (pparts + rparts + eparts);
-        b_frame.ensure(fwords * 4);
-        ensure_sort(std::max<int64_t>(N, pcap), 4);
-        if (timing) {
-            b_evals.ensure(64 * 8 * 8);
-        }
-        uint32_t* fr = b_frame.as<uint32_t>();
-        uint64_t* lb_proj = reinterpret_cast<uint64_t*>(fr + kFrLb);
-        uint64_t* lb_rect = lb_proj + pparts;
-        uint64_t* lb_emit = lb_rect + rparts;
-        uint32_t* cnt = fr + kFrCnt;
+        b_phist_proj.ensure(L.pparts * 1024 * 4);
+        b_phist_emit.ensure(L.eparts * 512 * 4);
+        L.fwords = kFrLb + 2 * (L.pparts + L.rparts + L.eparts);
+        b_frame.ensure(L.fwords * 4);
+        ensure_sort(std::max<int64_t>(N, L.pcap), 4);
+        if (timing) b_evals.ensure(64 * 8 * 8);
+        L.fr = b_frame.as<uint32_t>();
+        L.lb_proj = reinterpret_cast<uint64_t*>(L.fr + kFrLb);
+        L.lb_rect = L.lb_proj + L.pparts;
+        L.lb_emit = L.lb_rect + L.rparts;
+        L.cnt = L.fr + kFrCnt;
+        return L;
+    }
 
-        record(0);
-        HIPCHK(gs::launch_fill_u32(fr, 0u, fwords, st));
-        if (timing) HIPCHK(gs::launch_fill_u32(b_evals.as<uint32_t>(), 0u, 64 * 8 * 2, st));
-        gs::ProjParams p = proj_params(v);
-        gs::Compact c{b_rect.as<float4>(), b_covc.as<float4>(), b_dkey.as<uint32_t>(),
-                      b_brec.as<float4>(), nullptr};
-        HIPCHK(gs::launch_project(sd, p, c, nullptr, lb_proj, cnt + C_PROJ_TICKET, cnt + C_M,
-                                  b_phist_proj.as<uint32_t>(), st));
-        HIPCHK(gs::launch_reduce_rows(b_phist_proj.as<uint32_t>(), 1024, (uint32_t)pparts, nullptr,
-                                      0, 0, fr + kFrDepthHist, st));
-        record(1);
+    // From the compact records of the M visible Gaussians (count on the device at
+    // cnt[C_M], depth-key histograms reduced) to the tile-sorted compact ids and
+    // tile ranges: depth sort, candidate scan, pair emission + cull, tile sort,
+    // tile bounds. Returns the sorted compact ids.
+    uint32_t* frame_tiles(const FrameLayout& L, int64_t N, int64_t T, const gs::TileParams& tp) {
+        uint32_t* fr = L.fr;
+        uint32_t* cnt = L.cnt;
         // depth order of the visible Gaussians (stable: ties keep index order)
         void* kf = nullptr;
         uint32_t* order = nullptr;
@@ -562,35 +574,361 @@ struct gs_ctx {
                                         fr + kFrDepthHist, cnt + C_DSORT_TICKETS, sort, st, true,
                                         &kf, &order));
         record(2);
-        gs::TileParams tp{tiles_x, tiles_y, ts, v->cull_disabled ? 0 : 1};
         HIPCHK(gs::launch_rect_count_scan(b_rect.as<float4>(), b_covc.as<float4>(), order, N,
                                           cnt + C_M, tp, b_offs.as<uint32_t>(),
-                                          b_bstart.as<uint32_t>(), (uint32_t)(eparts + 1), lb_rect,
-                                          cnt + C_RECT_TICKET, cnt + C_PPRE,
+                                          b_bstart.as<uint32_t>(), (uint32_t)(L.eparts + 1),
+                                          L.lb_rect, cnt + C_RECT_TICKET, cnt + C_PPRE,
                                           b_rect_r.as<float4>(), b_cov_r.as<float4>(), st));
         HIPCHK(gs::launch_pair_emit(b_rect_r.as<float4>(), b_cov_r.as<float4>(), order,
                                     b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(), N, cnt + C_M,
-                                    pcap, cnt + C_PPRE, tp, b_pair_tile.as<uint32_t>(),
-                                    b_pair_id.as<uint32_t>(), pcap, lb_emit, cnt + C_EMIT_TICKET,
-                                    cnt + C_P, b_phist_emit.as<uint32_t>(), st));
-        HIPCHK(gs::launch_reduce_rows(b_phist_emit.as<uint32_t>(), 512, (uint32_t)eparts,
-                                      cnt + C_PPRE, pcap, gs::kEmitPartition, fr + kFrTileHist, st));
+                                    L.pcap, cnt + C_PPRE, tp, b_pair_tile.as<uint32_t>(),
+                                    b_pair_id.as<uint32_t>(), L.pcap, L.lb_emit,
+                                    cnt + C_EMIT_TICKET, cnt + C_P, b_phist_emit.as<uint32_t>(),
+                                    st));
+        HIPCHK(gs::launch_reduce_rows(b_phist_emit.as<uint32_t>(), 512, (uint32_t)L.eparts,
+                                      cnt + C_PPRE, L.pcap, gs::kEmitPartition, fr + kFrTileHist,
+                                      st));
         record(3);
         // stable tile sort of the depth-ordered pairs
         void* tiles_sorted = nullptr;
         uint32_t* ids_sorted = nullptr;
-        HIPCHK(gs::radix_sort_pairs_dev(b_pair_tile.p, b_pair_id.as<uint32_t>(), pcap, cnt + C_P, 4,
-                                        0, tile_bits(T), fr + kFrTileHist, cnt + C_TSORT_TICKETS,
-                                        sort, st, false, &tiles_sorted, &ids_sorted));
-        HIPCHK(gs::launch_tile_bounds(static_cast<uint32_t*>(tiles_sorted), pcap, cnt + C_P,
+        HIPCHK(gs::radix_sort_pairs_dev(b_pair_tile.p, b_pair_id.as<uint32_t>(), L.pcap,
+                                        cnt + C_P, 4, 0, tile_bits(T), fr + kFrTileHist,
+                                        cnt + C_TSORT_TICKETS, sort, st, false, &tiles_sorted,
+                                        &ids_sorted));
+        HIPCHK(gs::launch_tile_bounds(static_cast<uint32_t*>(tiles_sorted), L.pcap, cnt + C_P,
                                       b_ranges.as<uint32_t>(), T, st));
+        return ids_sorted;
+    }
+
+    // Enqueues one frame (project -> depth sort -> tile assign -> tile sort ->
+    // ranges -> blend) on the stream; no host synchronisation.
+    void frame(const gs_view* v, void* dout, int64_t T, int tiles_x, int tiles_y) {
+        const int64_t N = sd.n;
+        const FrameLayout L = frame_prepare(N, T);
+        record(0);
+        HIPCHK(gs::launch_fill_u32(L.fr, 0u, L.fwords, st));
+        if (timing) HIPCHK(gs::launch_fill_u32(b_evals.as<uint32_t>(), 0u, 64 * 8 * 2, st));
+        gs::ProjParams p = proj_params(v);
+        gs::Compact c{b_rect.as<float4>(), b_covc.as<float4>(), b_dkey.as<uint32_t>(),
+                      b_brec.as<float4>(), nullptr};
+        HIPCHK(gs::launch_project(sd, p, c, nullptr, L.lb_proj, L.cnt + C_PROJ_TICKET,
+                                  L.cnt + C_M, b_phist_proj.as<uint32_t>(), st));
+        HIPCHK(gs::launch_reduce_rows(b_phist_proj.as<uint32_t>(), 1024, (uint32_t)L.pparts,
+                                      nullptr, 0, 0, L.fr + kFrDepthHist, st));
+        record(1);
+        gs::TileParams tp{tiles_x, tiles_y, v->tile_size, v->cull_disabled ? 0 : 1};
+        uint32_t* ids_sorted = frame_tiles(L, N, T, tp);
         record(4);
-        gs::BlendParams bp{tiles_x, tiles_y, ts, v->image_height, v->image_width,
+        gs::BlendParams bp{tiles_x, tiles_y, v->tile_size, v->image_height, v->image_width,
                            v->cull_disabled ? 1 : 0, v->transmittance_threshold, v->out_format,
                            timing ? b_evals.as<unsigned long long>() : nullptr};
         HIPCHK(gs::launch_blend(b_brec.as<float4>(), ids_sorted, b_ranges.as<uint32_t>(), bp,
                                 dout, st));
         record(5);
+    }
+
+    // ------------------------------------------------------------ training
+    struct TrainState {
+        int64_t n = 0;
+        int deg = -1;
+        int planes = 0;
+        int64_t step = 0;
+        bool ready = false;
+        bool fwd_valid = false;   // the frame buffers hold the last training forward
+        bool has_dimage = false;
+        bool grads_valid = false;
+        int H = 0, W = 0, tiles_x = 0, tiles_y = 0;
+        gs::TrainCam cam{};
+        uint32_t M = 0, P = 0;
+        uint32_t* ids = nullptr;  // tile-sorted compact ids of the last forward
+        double loss = 0.0;
+    } tr;
+    DevBuf t_p, t_m, t_v, t_g, t_cidx, t_vis, t_grad2d, t_img, t_T, t_stop, t_dimg, t_tgt,
+        t_loss, t_dbg;
+    std::vector<float> t_host;
+    hipEvent_t tev[6] = {};
+
+    gs::TrainParamsDev tplanes(DevBuf& b) {
+        gs::TrainParamsDev d{};
+        float* base = b.as<float>();
+        const size_t n = (size_t)tr.n;
+        for (int c = 0; c < 3; ++c) d.mean[c] = base + c * n;
+        for (int c = 0; c < 3; ++c) d.ls[c] = base + (3 + c) * n;
+        for (int c = 0; c < 4; ++c) d.quat[c] = base + (6 + c) * n;
+        d.ol = base + 10 * n;
+        d.sh = base + 11 * n;
+        d.n = tr.n;
+        d.sh_degree = tr.deg;
+        return d;
+    }
+
+    // AoS host arrays <-> SoA planes (mean 3, log-scale 3, quat 4, logit 1, SH 3K).
+    void train_upload(DevBuf& b, const gs_train_arrays* a) {
+        REQUIRE(a && a->means && a->log_scales && a->quats && a->opacity_logits && a->sh,
+                "train: null parameter array");
+        const int64_t n = tr.n;
+        const int K = (tr.deg + 1) * (tr.deg + 1);
+        t_host.resize((size_t)tr.planes * (size_t)std::max<int64_t>(n, 1));
+        float* h = t_host.data();
+        parallel_for(n, [&](int64_t lo, int64_t hi) {
+            for (int64_t i = lo; i < hi; ++i) {
+                for (int c = 0; c < 3; ++c) {
+                    h[c * n + i] = a->means[3 * i + c];
+                    h[(3 + c) * n + i] = a->log_scales[3 * i + c];
+                }
+                for (int c = 0; c < 4; ++c) h[(6 + c) * n + i] = a->quats[4 * i + c];
+                h[10 * n + i] = a->opacity_logits[i];
+                for (int k = 0; k < K; ++k)
+                    for (int c = 0; c < 3; ++c)
+                        h[(11 + 3 * k + c) * n + i] = a->sh[(i * K + k) * 3 + c];
+            }
+        });
+        HIPCHK(hipMemcpyAsync(b.p, h, (size_t)tr.planes * n * 4, hipMemcpyHostToDevice, st));
+        sync();
+    }
+    void train_download(DevBuf& b, gs_train_arrays* a) {
+        REQUIRE(a && a->means && a->log_scales && a->quats && a->opacity_logits && a->sh,
+                "train: null output array");
+        const int64_t n = tr.n;
+        const int K = (tr.deg + 1) * (tr.deg + 1);
+        t_host.resize((size_t)tr.planes * (size_t)std::max<int64_t>(n, 1));
+        float* h = t_host.data();
+        HIPCHK(hipMemcpyAsync(h, b.p, (size_t)tr.planes * n * 4, hipMemcpyDeviceToHost, st));
+        sync();
+        parallel_for(n, [&](int64_t lo, int64_t hi) {
+            for (int64_t i = lo; i < hi; ++i) {
+                for (int c = 0; c < 3; ++c) {
+                    a->means[3 * i + c] = h[c * n + i];
+                    a->log_scales[3 * i + c] = h[(3 + c) * n + i];
+                }
+                for (int c = 0; c < 4; ++c) a->quats[4 * i + c] = h[(6 + c) * n + i];
+                a->opacity_logits[i] = h[10 * n + i];
+                for (int k = 0; k < K; ++k)
+                    for (int c = 0; c < 3; ++c)
+                        a->sh[(i * K + k) * 3 + c] = h[(11 + 3 * k + c) * n + i];
+            }
+        });
+    }
+
+    void train_init(const gs_train_arrays* a, int64_t n, int deg) {
+        REQUIRE(n >= 0 && n < ((int64_t)1 << 31), "train: n out of range");
+        REQUIRE(deg >= 0 && deg <= 3, "train: sh_degree must be 0..3");
+        sync();
+        tr = TrainState{};
+        tr.n = n;
+        tr.deg = deg;
+        tr.planes = 11 + 3 * (deg + 1) * (deg + 1);
+        const size_t bytes = (size_t)tr.planes * (size_t)std::max<int64_t>(n, 1) * 4;
+        for (DevBuf* b : {&t_p, &t_m, &t_v, &t_g}) b->ensure(bytes);
+        HIPCHK(gs::launch_fill_u32(t_m.as<uint32_t>(), 0u, bytes / 4, st));
+        HIPCHK(gs::launch_fill_u32(t_v.as<uint32_t>(), 0u, bytes / 4, st));
+        HIPCHK(gs::launch_fill_u32(t_g.as<uint32_t>(), 0u, bytes / 4, st));
+        t_cidx.ensure((size_t)std::max<int64_t>(n, 1) * 4);
+        t_vis.ensure((size_t)std::max<int64_t>(n, 1));
+        HIPCHK(hipMemsetAsync(t_vis.p, 0, (size_t)std::max<int64_t>(n, 1), st));
+        train_upload(t_p, a);
+        tr.ready = true;
+    }
+
+    gs::TrainCam train_cam(const gs_view* v, const gs_train_cfg* c) {
+        gs::TrainCam cam{};
+        const float* e = v->extrinsics;
+        const float* K = v->intrinsics;
+        const int ri[9] = {0, 1, 2, 4, 5, 6, 8, 9, 10};
+        for (int j = 0; j < 9; ++j) cam.r[j] = e[ri[j]];
+        cam.t[0] = e[3];
+        cam.t[1] = e[7];
+        cam.t[2] = e[11];
+        cam.fx = K[0];
+        cam.fy = K[4];
+        cam.cx = K[2];
+        cam.cy = K[5];
+        cam.ccx = -(e[0] * cam.t[0] + e[4] * cam.t[1] + e[8] * cam.t[2]);
+        cam.ccy = -(e[1] * cam.t[0] + e[5] * cam.t[1] + e[9] * cam.t[2]);
+        cam.ccz = -(e[2] * cam.t[0] + e[6] * cam.t[1] + e[10] * cam.t[2]);
+        cam.near = c->near_plane;
+        cam.lowpass = c->lowpass;
+        cam.alpha_min = c->alpha_min;
+        cam.H = v->image_height;
+        cam.W = v->image_width;
+        return cam;
+    }
+
+    void train_check(const gs_view* v, const gs_train_cfg* c) {
+        REQUIRE(tr.ready, "train: gs_train_init first");
+        REQUIRE(c != nullptr, "train: null cfg");
+        check_view(v);
+        REQUIRE(v->tile_size == 16, "train: tile_size must be 16");
+        REQUIRE(c->alpha_min > 0.0f && c->alpha_max >= c->alpha_min && c->alpha_max < 1.0f,
+                "train: need 0 < alpha_min <= alpha_max < 1");
+        REQUIRE(c->t_min > 0.0f, "train: t_min must be > 0");
+    }
+
+    // Enqueues projection, tiles and the forward (+ L1 with a device target).
+    void train_forward_enqueue(const gs_view* v, const gs_train_cfg* c, const float* tgt_dev,
+                               const gs::TrainDebug& dbg) {
+        const int64_t N = tr.n;
+        const int H = v->image_height, W = v->image_width;
+        tr.H = H;
+        tr.W = W;
+        tr.tiles_x = (W + 15) / 16;
+        tr.tiles_y = (H + 15) / 16;
+        const int64_t T = (int64_t)tr.tiles_x * tr.tiles_y;
+        tr.cam = train_cam(v, c);
+        const FrameLayout L = frame_prepare(std::max<int64_t>(N, 1), T);
+        const size_t px = (size_t)H * W;
+        t_img.ensure(px * 12);
+        t_T.ensure(px * 4);
+        t_stop.ensure(px * 4);
+        t_dimg.ensure(px * 12);
+        t_loss.ensure(16);
+        if (timing)
+            for (auto& e : tev)
+                if (!e) HIPCHK(hipEventCreate(&e));
+        if (timing) HIPCHK(hipEventRecord(tev[0], st));
+        HIPCHK(gs::launch_fill_u32(L.fr, 0u, L.fwords, st));
+        HIPCHK(gs::launch_fill_u32(t_loss.as<uint32_t>(), 0u, 4, st));
+        gs::Compact cpt{b_rect.as<float4>(), b_covc.as<float4>(), b_dkey.as<uint32_t>(),
+                        nullptr, b_src.as<uint32_t>()};
+        HIPCHK(gs::launch_train_project(tplanes(t_p), tr.cam, cpt, b_brec.as<float4>(),
+                                        t_cidx.as<uint32_t>(), t_vis.as<uint8_t>(), L.lb_proj,
+                                        L.cnt + C_PROJ_TICKET, L.cnt + C_M,
+                                        b_phist_proj.as<uint32_t>(), dbg, st));
+        HIPCHK(gs::launch_reduce_rows(b_phist_proj.as<uint32_t>(), 1024, (uint32_t)L.pparts,
+                                      nullptr, 0, 0, L.fr + kFrDepthHist, st));
+        gs::TileParams tp{tr.tiles_x, tr.tiles_y, 16, 1};
+        tr.ids = frame_tiles(L, std::max<int64_t>(N, 1), T, tp);
+        gs::TrainFwdParams fp{};
+        fp.tiles_x = tr.tiles_x;
+        fp.tiles_y = tr.tiles_y;
+        fp.width = W;
+        fp.height = H;
+        fp.alpha_max = c->alpha_max;
+        fp.alpha_min = c->alpha_min;
+        fp.t_min = c->t_min;
+        for (int k = 0; k < 3; ++k) fp.bg[k] = c->background[k];
+        fp.image = t_img.as<float>();
+        fp.final_T = t_T.as<float>();
+        fp.stop = t_stop.as<uint32_t>();
+        fp.target = tgt_dev;
+        fp.dimage = t_dimg.as<float>();
+        fp.grad_scale = (float)((double)c->loss_scale / (3.0 * (double)px));
+        fp.loss = reinterpret_cast<double*>(t_loss.p);
+        HIPCHK(gs::launch_train_fwd(b_brec.as<float4>(), tr.ids, b_ranges.as<uint32_t>(), fp, st));
+        if (timing) HIPCHK(hipEventRecord(tev[1], st));
+    }
+
+    // Forward with the pair-capacity retry; one host synchronisation.
+    void train_forward(const gs_view* v, const gs_train_cfg* c, const float* target,
+                       bool target_dev, const gs::TrainDebug& dbg) {
+        const size_t px = (size_t)v->image_height * v->image_width;
+        const float* tgt = nullptr;
+        if (target != nullptr) {
+            if (target_dev) {
+                tgt = target;
+            } else {
+                t_tgt.ensure(px * 12);
+                HIPCHK(hipMemcpyAsync(t_tgt.p, target, px * 12, hipMemcpyHostToDevice, st));
+                tgt = t_tgt.as<float>();
+            }
+        }
+        ensure_counters();
+        tr.fwd_valid = false;
+        tr.grads_valid = false;
+        if (pair_cap == 0) pair_cap = std::max<uint64_t>(1u << 20, (uint64_t)tr.n * 4);
+        for (int attempt = 0;; ++attempt) {
+            train_forward_enqueue(v, c, tgt, dbg);
+            HIPCHK(hipMemcpyAsync(h_pin, b_frame.p, 64 * 4, hipMemcpyDeviceToHost, st));
+            HIPCHK(hipMemcpyAsync(h_pin + 64, t_loss.p, 8, hipMemcpyDeviceToHost, st));
+            sync();
+            const uint32_t p_pre = h_pin[C_PPRE];
+            if (p_pre == 0xFFFFFFFFu)
+                throw GsError(GS_E_CAPACITY, "train: more than 2^32-1 candidate pairs");
+            if (p_pre <= pair_cap) break;
+            REQUIRE(attempt == 0, "train: pair capacity did not converge");
+            pair_cap = std::min<uint64_t>(0xFFFFFFFFull, (uint64_t)p_pre + p_pre / 8 + 4096);
+        }
+        tr.M = h_pin[C_M];
+        tr.P = h_pin[C_P];
+        double lsum;
+        std::memcpy(&lsum, h_pin + 64, 8);
+        tr.loss = tgt ? (double)c->loss_scale * lsum / (3.0 * (double)px) : 0.0;
+        tr.fwd_valid = true;
+        tr.has_dimage = tgt != nullptr;
+    }
+
+    // Enqueues the blend backward and the projection backward (gradients in t_g).
+    void train_backward_enqueue(const gs_train_cfg* c) {
+        const int64_t N = tr.n;
+        t_grad2d.ensure((size_t)std::max<uint32_t>(tr.M, 1) * 36);
+        if (timing) HIPCHK(hipEventRecord(tev[2], st));
+        HIPCHK(gs::launch_fill_u32(t_grad2d.as<uint32_t>(), 0u, (size_t)tr.M * 9, st));
+        gs::TrainBwdParams bp{};
+        bp.tiles_x = tr.tiles_x;
+        bp.tiles_y = tr.tiles_y;
+        bp.width = tr.W;
+        bp.height = tr.H;
+        bp.alpha_max = c->alpha_max;
+        bp.alpha_min = c->alpha_min;
+        for (int k = 0; k < 3; ++k) bp.bg[k] = c->background[k];
+        bp.final_T = t_T.as<float>();
+        bp.stop = t_stop.as<uint32_t>();
+        bp.dimage = t_dimg.as<float>();
+        bp.grad2d = t_grad2d.as<float>();
+        if (tr.M > 0 && tr.P > 0)
+            HIPCHK(gs::launch_train_bwd(b_brec.as<float4>(), tr.ids, b_ranges.as<uint32_t>(), bp, st));
+        HIPCHK(gs::launch_train_param_grads(tplanes(t_p), tr.cam, t_cidx.as<uint32_t>(),
+                                            t_grad2d.as<float>(), tplanes(t_g), st));
+        if (timing) HIPCHK(hipEventRecord(tev[3], st));
+        (void)N;
+    }
+
+    void train_adam_enqueue(const gs_train_cfg* c) {
+        const double b1 = c->beta1, b2 = c->beta2;
+        const int64_t t = tr.step + 1;
+        const double bc1 = 1.0 - std::pow(b1, (double)t), bc2 = 1.0 - std::pow(b2, (double)t);
+        gs::AdamParams ap{};
+        ap.beta1 = (float)b1;
+        ap.beta2 = (float)b2;
+        ap.one_minus_beta1 = (float)(1.0 - b1);
+        ap.one_minus_beta2 = (float)(1.0 - b2);
+        ap.sqrt_bc2 = (float)std::sqrt(bc2);
+        ap.eps = (float)c->eps;
+        const double lr_geo[4] = {c->lr_means, c->lr_log_scales, c->lr_quats, c->lr_opacity};
+        const int geo_planes[4] = {3, 3, 4, 1};
+        int j = 0;
+        for (int gidx = 0; gidx < 4; ++gidx)
+            for (int k = 0; k < geo_planes[gidx]; ++k) ap.step[j++] = (float)(lr_geo[gidx] / bc1);
+        const int K = (tr.deg + 1) * (tr.deg + 1);
+        for (int k = 0; k < K; ++k)
+            for (int ch = 0; ch < 3; ++ch)
+                ap.step[j++] = (float)(k == 0 ? c->lr_sh_dc : c->lr_sh_rest) / (float)bc1;
+        if (timing) HIPCHK(hipEventRecord(tev[4], st));
+        HIPCHK(gs::launch_sparse_adam(t_p.as<float>(), t_m.as<float>(), t_v.as<float>(),
+                                      t_g.as<float>(), t_vis.as<uint8_t>(), tr.n, tr.planes, ap,
+                                      st));
+        if (timing) HIPCHK(hipEventRecord(tev[5], st));
+        ++tr.step;
+    }
+
+    void train_stats(gs_train_stats* s, bool fwd, bool bwd, bool adam,
+                     std::chrono::steady_clock::time_point t0) {
+        if (!s) return;
+        gs_train_stats o{};
+        o.num_blendable = tr.M;
+        o.num_entries = tr.P;
+        o.step = tr.step;
+        o.loss = tr.loss;
+        if (timing) {
+            float ms = 0.0f;
+            if (fwd && hipEventElapsedTime(&ms, tev[0], tev[1]) == hipSuccess) o.ms_forward = ms;
+            if (bwd && hipEventElapsedTime(&ms, tev[2], tev[3]) == hipSuccess) o.ms_backward = ms;
+            if (adam && hipEventElapsedTime(&ms, tev[4], tev[5]) == hipSuccess) o.ms_adam = ms;
+        }
+        o.ms_total = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() - t0)
+                         .count();
+        *s = o;
     }
 
     void blend_diag(gs_stats& s) {
@@ -930,6 +1268,166 @@ int gs_last_sort_pass_ms(gs_ctx* ctx, float* ms, int max_passes) {
         ms[i] = v;
     }
     return np;
+}
+
+int gs_train_init(gs_ctx* ctx, const gs_train_arrays* params, int64_t n, int sh_degree) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->train_init(params, n, sh_degree);
+    });
+}
+
+int gs_train_read(gs_ctx* ctx, int which, gs_train_arrays* out) {
+    return guard([&] {
+        REQUIRE(ctx && ctx->tr.ready, "train: gs_train_init first");
+        REQUIRE(which >= 0 && which <= 3, "train: which must be 0..3");
+        HIPCHK(hipSetDevice(ctx->device));
+        DevBuf* b[4] = {&ctx->t_p, &ctx->t_m, &ctx->t_v, &ctx->t_g};
+        ctx->train_download(*b[which], out);
+    });
+}
+
+int gs_train_write(gs_ctx* ctx, int which, const gs_train_arrays* in) {
+    return guard([&] {
+        REQUIRE(ctx && ctx->tr.ready, "train: gs_train_init first");
+        REQUIRE(which >= 0 && which <= 3, "train: which must be 0..3");
+        HIPCHK(hipSetDevice(ctx->device));
+        DevBuf* b[4] = {&ctx->t_p, &ctx->t_m, &ctx->t_v, &ctx->t_g};
+        ctx->sync();
+        ctx->train_upload(*b[which], in);
+        if (which == 0) ctx->tr.fwd_valid = false;
+        if (which == 3) ctx->tr.grads_valid = true;
+    });
+}
+
+int gs_train_set_step(gs_ctx* ctx, int64_t step) {
+    return guard([&] {
+        REQUIRE(ctx && ctx->tr.ready, "train: gs_train_init first");
+        REQUIRE(step >= 0, "train: step must be >= 0");
+        ctx->tr.step = step;
+    });
+}
+
+int gs_train_set_visible(gs_ctx* ctx, const uint8_t* visible) {
+    return guard([&] {
+        REQUIRE(ctx && ctx->tr.ready, "train: gs_train_init first");
+        REQUIRE(visible != nullptr || ctx->tr.n == 0, "train: null mask");
+        HIPCHK(hipSetDevice(ctx->device));
+        if (ctx->tr.n > 0)
+            HIPCHK(hipMemcpyAsync(ctx->t_vis.p, visible, (size_t)ctx->tr.n, hipMemcpyHostToDevice,
+                                  ctx->st));
+        ctx->sync();
+    });
+}
+
+int gs_train_forward(gs_ctx* ctx, const gs_view* view, const gs_train_cfg* cfg,
+                     const float* target, float* image, float* final_T, gs_train_proj* proj,
+                     gs_train_stats* stats) {
+    return guard([&] {
+        const auto t0 = std::chrono::steady_clock::now();
+        REQUIRE(ctx, "null ctx");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->train_check(view, cfg);
+        const int64_t n = ctx->tr.n;
+        gs::TrainDebug dbg{};
+        if (proj != nullptr) {
+            const size_t nn = (size_t)std::max<int64_t>(n, 1);
+            ctx->t_dbg.ensure(nn * 41);  // 10 floats + 1 byte per Gaussian
+            float* f = ctx->t_dbg.as<float>();
+            dbg.means2d = f;
+            dbg.conic = f + 2 * nn;
+            dbg.opacity = f + 5 * nn;
+            dbg.colors = f + 6 * nn;
+            dbg.depth = f + 9 * nn;
+            dbg.valid = reinterpret_cast<uint8_t*>(f + 10 * nn);
+        }
+        ctx->train_forward(view, cfg, target, false, dbg);
+        const size_t px = (size_t)view->image_height * view->image_width;
+        if (image) HIPCHK(hipMemcpyAsync(image, ctx->t_img.p, px * 12, hipMemcpyDeviceToHost, ctx->st));
+        if (final_T) HIPCHK(hipMemcpyAsync(final_T, ctx->t_T.p, px * 4, hipMemcpyDeviceToHost, ctx->st));
+        if (proj != nullptr && n > 0) {
+            const size_t nn = (size_t)n;
+            struct { void* dst; const void* src; size_t bytes; } cp[7] = {
+                {proj->means2d, dbg.means2d, nn * 8}, {proj->conic, dbg.conic, nn * 12},
+                {proj->opacity, dbg.opacity, nn * 4}, {proj->colors, dbg.colors, nn * 12},
+                {proj->depth, dbg.depth, nn * 4},     {proj->valid, dbg.valid, nn},
+                {proj->visible, ctx->t_vis.p, nn}};
+            for (auto& c : cp)
+                if (c.dst) HIPCHK(hipMemcpyAsync(c.dst, c.src, c.bytes, hipMemcpyDeviceToHost, ctx->st));
+        }
+        ctx->sync();
+        ctx->train_stats(stats, true, false, false, t0);
+    });
+}
+
+int gs_train_backward(gs_ctx* ctx, const gs_train_cfg* cfg, const float* dimage, float* g2d,
+                      gs_train_stats* stats) {
+    return guard([&] {
+        const auto t0 = std::chrono::steady_clock::now();
+        REQUIRE(ctx && ctx->tr.ready, "train: gs_train_init first");
+        REQUIRE(cfg != nullptr, "train: null cfg");
+        REQUIRE(ctx->tr.fwd_valid, "train: no current forward (run gs_train_forward first)");
+        REQUIRE(dimage != nullptr || ctx->tr.has_dimage,
+                "train: no dL/dimage (forward without a target and none given)");
+        HIPCHK(hipSetDevice(ctx->device));
+        const size_t px = (size_t)ctx->tr.H * ctx->tr.W;
+        if (dimage)
+            HIPCHK(hipMemcpyAsync(ctx->t_dimg.p, dimage, px * 12, hipMemcpyHostToDevice, ctx->st));
+        ctx->train_backward_enqueue(cfg);
+        if (g2d != nullptr) {
+            const int64_t n = ctx->tr.n;
+            const uint32_t M = ctx->tr.M;
+            std::vector<float> gm((size_t)M * 9);
+            std::vector<uint32_t> src(M);
+            if (M > 0) {
+                HIPCHK(hipMemcpyAsync(gm.data(), ctx->t_grad2d.p, (size_t)M * 36,
+                                      hipMemcpyDeviceToHost, ctx->st));
+                HIPCHK(hipMemcpyAsync(src.data(), ctx->b_src.p, (size_t)M * 4,
+                                      hipMemcpyDeviceToHost, ctx->st));
+            }
+            ctx->sync();
+            std::fill(g2d, g2d + (size_t)n * 9, 0.0f);
+            for (uint32_t m = 0; m < M; ++m)
+                std::memcpy(g2d + (size_t)src[m] * 9, gm.data() + (size_t)m * 9, 36);
+        }
+        ctx->sync();
+        ctx->tr.grads_valid = true;
+        ctx->train_stats(stats, false, true, false, t0);
+    });
+}
+
+int gs_train_adam(gs_ctx* ctx, const gs_train_cfg* cfg, gs_train_stats* stats) {
+    return guard([&] {
+        const auto t0 = std::chrono::steady_clock::now();
+        REQUIRE(ctx && ctx->tr.ready, "train: gs_train_init first");
+        REQUIRE(cfg != nullptr, "train: null cfg");
+        REQUIRE(ctx->tr.grads_valid, "train: no gradients (run gs_train_backward first)");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->train_adam_enqueue(cfg);
+        ctx->sync();
+        ctx->tr.fwd_valid = false;  // parameters changed
+        ctx->tr.grads_valid = false;
+        ctx->train_stats(stats, false, false, true, t0);
+    });
+}
+
+int gs_train_step(gs_ctx* ctx, const gs_view* view, const gs_train_cfg* cfg, const float* target,
+                  int target_on_device, gs_train_stats* stats) {
+    return guard([&] {
+        const auto t0 = std::chrono::steady_clock::now();
+        REQUIRE(ctx, "null ctx");
+        REQUIRE(target != nullptr, "train: null target");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->train_check(view, cfg);
+        ctx->train_forward(view, cfg, target, target_on_device != 0, gs::TrainDebug{});
+        ctx->train_backward_enqueue(cfg);
+        ctx->train_adam_enqueue(cfg);
+        ctx->sync();
+        ctx->tr.fwd_valid = false;
+        ctx->tr.grads_valid = false;
+        ctx->train_stats(stats, true, true, true, t0);
+    });
 }
 
 int gs_dev_alloc(gs_ctx* ctx, int64_t bytes, void** ptr) {

@@ -155,4 +155,85 @@ struct BlendParams {
 hipError_t launch_blend(const float4* brec, const uint32_t* sorted_id, const uint32_t* ranges,
                         BlendParams bp, void* out, hipStream_t st);
 
+// ---- train.hip: training step (3DGS forward rules, L1, backward, sparse Adam)
+constexpr int kMaxTrainPlanes = 64;  // 11 geometry/opacity planes + 3 (d+1)^2 SH planes
+
+// Optimizer-space parameters (or gradients / moments of the same shape) as SoA
+// planes of n floats: mean x y z, log-scale 0..2, quaternion w x y z, opacity
+// logit, then SH plane 3k+c for coefficient k, channel c.
+struct TrainParamsDev {
+    float* mean[3];
+    float* ls[3];
+    float* quat[4];
+    float* ol;
+    float* sh;
+    int64_t n;
+    int sh_degree;
+};
+
+struct TrainCam {
+    float r[9], t[3];          // world-to-camera rotation (row-major) and translation
+    float fx, fy, cx, cy;
+    float ccx, ccy, ccz;       // camera centre -R^T t
+    float near, lowpass, alpha_min;
+    int H, W;
+};
+
+// Optional Gaussian-indexed copies of the projection values (parity tests).
+struct TrainDebug {
+    float* means2d;   // (n,2)
+    float* conic;     // (n,3)
+    float* opacity;
+    float* colors;    // (n,3)
+    float* depth;
+    uint8_t* valid;
+};
+
+struct TrainFwdParams {
+    int tiles_x, tiles_y, width, height;
+    float alpha_max, alpha_min, t_min;
+    float bg[3];
+    float* image;          // (H,W,3)
+    float* final_T;        // (H,W)
+    uint32_t* stop;        // (H,W) entries of the tile list the pixel considered
+    const float* target;   // (H,W,3) or null (no loss)
+    float* dimage;         // dL/dimage (H,W,3), written with a target
+    float grad_scale;      // loss_scale / (3HW)
+    double* loss;          // accumulates sum |image - target|
+};
+
+struct TrainBwdParams {
+    int tiles_x, tiles_y, width, height;
+    float alpha_max, alpha_min;
+    float bg[3];
+    const float* final_T;
+    const uint32_t* stop;
+    const float* dimage;
+    float* grad2d;         // (M,9) per compact Gaussian: dmx dmy dA dB dC dop dr dg db
+};
+
+struct AdamParams {
+    float beta1, beta2, one_minus_beta1, one_minus_beta2, sqrt_bc2, eps;
+    float step[kMaxTrainPlanes];  // learning rate / (1 - beta1^t), per plane
+};
+
+// Compact outputs: rect (u, v, rx, ry), cov (a, b, c, 2 ln(op/alpha_min)), depth
+// keys, src (compact -> Gaussian) and the forward record trec (3 float4 per
+// compact Gaussian: (u, v, op), (A, B, C), (r, g, b)); cidx maps Gaussian ->
+// compact index or 0xFFFFFFFF; visible marks the sparse-Adam rows.
+hipError_t launch_train_project(const TrainParamsDev& P, const TrainCam& cam, Compact out,
+                                float4* trec, uint32_t* cidx, uint8_t* visible,
+                                uint64_t* lb_state, uint32_t* ticket, uint32_t* count_out,
+                                uint32_t* part_hist, const TrainDebug& dbg, hipStream_t st);
+hipError_t launch_train_fwd(const float4* trec, const uint32_t* sid, const uint32_t* ranges,
+                            const TrainFwdParams& fp, hipStream_t st);
+hipError_t launch_train_bwd(const float4* trec, const uint32_t* sid, const uint32_t* ranges,
+                            const TrainBwdParams& bp, hipStream_t st);
+hipError_t launch_train_param_grads(const TrainParamsDev& P, const TrainCam& cam,
+                                    const uint32_t* cidx, const float* grad2d,
+                                    const TrainParamsDev& G, hipStream_t st);
+hipError_t launch_sparse_adam(float* p, float* m, float* v, const float* g,
+                              const uint8_t* visible, int64_t n, int planes, const AdamParams& ap,
+                              hipStream_t st);
+
 }  // namespace gs

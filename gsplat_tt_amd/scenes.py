@@ -214,3 +214,16 @@ def config5(seed: int = 5, n: int = 1_000_000, degree: int = 1):
     tgt.sh[:, 0, :] += rng.normal(0, 0.05 / 0.28209479177387814, (n, 3)).astype(np.float32)
     scene.meta["config"] = 5
     return scene, tgt, cams
+
+
+def train_params(scene: "Scene") -> dict:
+    """Optimizer-space parameters of a scene (gsplat/train_oracle.py conventions):
+    means, log_scales = log(scales), quats (w x y z), opacity_logits = logit(op), sh."""
+    op = np.clip(scene.opacities.astype(np.float64), 1e-6, 1 - 1e-6)
+    return {
+        "means": scene.means.astype(np.float32),
+        "log_scales": np.log(scene.scales).astype(np.float32),
+        "quats": scene.quats.astype(np.float32),
+        "opacity_logits": np.log(op / (1.0 - op)).astype(np.float32),
+        "sh": scene.sh.astype(np.float32),
+    }

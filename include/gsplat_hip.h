@@ -141,6 +141,89 @@ int gs_sort_pairs_u64_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n
  * gs_sort_pairs_u64_dev call when timing is on; returns the pass count. */
 int gs_last_sort_pass_ms(gs_ctx* ctx, float* ms, int max_passes);
 
+/* ---- training (3DGS rules: forward, L1, backward, sparse Adam) ---------
+ * Follows the reference's training oracle gsplat/train_oracle.py (forward
+ * :125-233, sparse Adam :434-470), the L1 gradient of gsplat/train_loss.py:166-171,
+ * the blend backward of gsplat/blend_backward_ref.py:134-250 and the projection
+ * backward of gsplat/t2_param_backward.py:123-192 (extended to SH degrees 1-3).
+ * Parameters live on the device in optimizer space; one step = forward + L1 +
+ * backward + sparse Adam, fp32 throughout. tile_size of the view must be 16. */
+
+/* Host arrays in optimizer space (row-major, the reference's shapes). */
+typedef struct gs_train_arrays {
+    float* means;           /* (n,3) */
+    float* log_scales;      /* (n,3) */
+    float* quats;           /* (n,4) w x y z, unnormalised */
+    float* opacity_logits;  /* (n) */
+    float* sh;              /* (n,(d+1)^2,3) */
+} gs_train_arrays;
+
+typedef struct gs_train_cfg {
+    float near_plane;       /* 0.2 */
+    float lowpass;          /* 0.3, added to the 2D covariance diagonal */
+    float alpha_max;        /* 0.99 */
+    float alpha_min;        /* 1/255: pairs below are skipped */
+    float t_min;            /* 1e-4: a pixel stops before T (1 - alpha) drops below */
+    float background[3];
+    float loss_scale;       /* dL/dimage = loss_scale * sign(image - target) / (3HW) */
+    /* Adam hyper-parameters in double, as the reference forms its fp32 step sizes
+     * (float(lr / (1 - beta1^t)), float(1 - beta1), ...) from Python floats. */
+    double lr_means, lr_log_scales, lr_quats, lr_opacity, lr_sh_dc, lr_sh_rest;
+    double beta1, beta2, eps;
+} gs_train_cfg;
+
+typedef struct gs_train_stats {
+    int64_t num_blendable;  /* Gaussians that reach alpha_min somewhere (M) */
+    int64_t num_entries;    /* tile-Gaussian pairs after the cull (P) */
+    int64_t step;           /* Adam steps taken so far */
+    double loss;            /* loss_scale * mean |image - target| (with a target) */
+    float ms_forward;       /* device time: projection + tiles + forward + L1 */
+    float ms_backward;      /* blend backward + projection backward */
+    float ms_adam;
+    float ms_total;         /* host wall clock of the call */
+} gs_train_stats;
+
+/* Gaussian-indexed projection values of the last forward (parity tests). */
+typedef struct gs_train_proj {
+    float* means2d;         /* (n,2) */
+    float* conic;           /* (n,3) A B C, power = -0.5 (A dx^2 + 2B dx dy + C dy^2) */
+    float* opacity;         /* (n) */
+    float* colors;          /* (n,3) max(SH + 0.5, 0) */
+    float* depth;           /* (n) */
+    uint8_t* valid;         /* (n) z > near */
+    uint8_t* visible;       /* (n) sparse-Adam rows */
+} gs_train_proj;
+
+/* Uploads the parameters (n Gaussians, SH degree 0..3), zeroes the Adam
+ * moments and the step count. */
+int gs_train_init(gs_ctx* ctx, const gs_train_arrays* params, int64_t n, int sh_degree);
+/* which: 0 parameters, 1 first moments, 2 second moments, 3 gradients of the
+ * last backward. Read copies device -> host; write replaces the device copy. */
+int gs_train_read(gs_ctx* ctx, int which, gs_train_arrays* out);
+int gs_train_write(gs_ctx* ctx, int which, const gs_train_arrays* in);
+int gs_train_set_step(gs_ctx* ctx, int64_t step);
+/* Replaces the sparse-Adam row mask (n bytes) of the last forward. */
+int gs_train_set_visible(gs_ctx* ctx, const uint8_t* visible);
+
+/* Forward of the current parameters for `view` (camera, image size, tile 16).
+ * With a target (H,W,3) it also forms the L1 gradient and the loss. Outputs are
+ * optional host arrays: image (H,W,3), final_T (H,W), projection values. */
+int gs_train_forward(gs_ctx* ctx, const gs_view* view, const gs_train_cfg* cfg,
+                     const float* target, float* image, float* final_T,
+                     gs_train_proj* proj, gs_train_stats* stats);
+/* Backward of the last forward. dimage (H,W,3) replaces the L1 gradient when
+ * given. Writes the gradients (gs_train_read(ctx, 3, ...)); g2d (n,9) receives
+ * the Gaussian-indexed 2D gradients dmx dmy dA dB dC dop dr dg db when given. */
+int gs_train_backward(gs_ctx* ctx, const gs_train_cfg* cfg, const float* dimage, float* g2d,
+                      gs_train_stats* stats);
+/* Sparse Adam over the rows visible in the last forward (or set), with the
+ * gradients of the last backward; the step count then increments. */
+int gs_train_adam(gs_ctx* ctx, const gs_train_cfg* cfg, gs_train_stats* stats);
+/* One whole step: forward + L1 against `target` (H,W,3; host memory unless
+ * target_on_device) + backward + sparse Adam, one host synchronisation. */
+int gs_train_step(gs_ctx* ctx, const gs_view* view, const gs_train_cfg* cfg,
+                  const float* target, int target_on_device, gs_train_stats* stats);
+
 /* ---- device memory helpers (for callers without a GPU framework) ------ */
 int gs_dev_alloc(gs_ctx* ctx, int64_t bytes, void** ptr);
 int gs_dev_free(gs_ctx* ctx, void* ptr);

@@ -48,6 +48,11 @@ def test_struct_layout_matches_header():
 int main(void) {
   printf("gs_scene %zu\ngs_view %zu\ngs_stats %zu\n", sizeof(gs_scene), sizeof(gs_view),
          sizeof(gs_stats));
+  printf("gs_train_cfg %zu\ngs_train_stats %zu\ngs_train_proj %zu\ngs_train_arrays %zu\n",
+         sizeof(gs_train_cfg), sizeof(gs_train_stats), sizeof(gs_train_proj),
+         sizeof(gs_train_arrays));
+  P(gs_train_cfg, loss_scale) P(gs_train_cfg, lr_means) P(gs_train_cfg, eps)
+  P(gs_train_stats, loss) P(gs_train_stats, ms_total) P(gs_train_proj, visible)
   P(gs_scene, n) P(gs_scene, version) P(gs_view, image_height) P(gs_view, tile_size)
   P(gs_view, k_cap) P(gs_view, out_format) P(gs_view, sh_clamp_hi)
   P(gs_stats, ms_project) P(gs_stats, blend_max_iters)
@@ -65,10 +70,15 @@ int main(void) {
     assert int(got["gs_scene"]) == ctypes.sizeof(L.GsScene)
     assert int(got["gs_view"]) == ctypes.sizeof(L.GsView)
     assert int(got["gs_stats"]) == ctypes.sizeof(L.GsStats)
+    classes = {"gs_scene": L.GsScene, "gs_view": L.GsView, "gs_stats": L.GsStats,
+               "gs_train_cfg": L.GsTrainCfg, "gs_train_stats": L.GsTrainStats,
+               "gs_train_proj": L.GsTrainProj, "gs_train_arrays": L.GsTrainArrays}
+    for t, cls in classes.items():
+        assert int(got[t]) == ctypes.sizeof(cls), t
     for key, val in got.items():
         if "." in key:
             t, f = key.split(".")
-            cls = {"gs_scene": L.GsScene, "gs_view": L.GsView, "gs_stats": L.GsStats}[t]
+            cls = classes[t]
             assert getattr(cls, f).offset == int(val), key
 
 

@@ -1,0 +1,124 @@
+"""The HIP training path (gs_train_* entry points) against the reference's own
+training dumps (tests/golden/t0_*: fp64 autograd of gsplat/train_oracle.py) and
+against the training oracle (oracle/train_oracle.py) on a C5-shaped scene.
+Bars: forward values 1e-5 relative, images 1e-4 absolute; gradients rel 1e-2 in
+the reference's rel_error (its gate for the device backward); Adam moments
+bit-exact, parameters within 1e-7."""
+import numpy as np
+import pytest
+
+from gsplat_tt_amd import _lib as L
+from gsplat_tt_amd import scenes
+from oracle import train_oracle as TO
+from tests import golden_io
+from tests.test_train_oracle import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _fixture(name):
+    g = golden_io.load(name)
+    c = g["cfg_json"]
+    cfg = L.make_train_cfg(near=c["near"], lowpass=c["lowpass"], alpha_max=c["alpha_max"],
+                           alpha_min=c["alpha_min"], t_min=c["t_min"],
+                           background=c["background"], lr=g["adam_lr_json"],
+                           betas=tuple(g["adam_betas"]), eps=float(g["adam_eps"]))
+    view = L.make_view(g["w2c"], g["K"], g["H"], g["W"], tile_size=16)
+    params = {k: g["param_" + k].astype(np.float32) for k in TO.PARAM_NAMES}
+    return g, cfg, view, params
+
+
+@pytest.mark.parametrize("name", golden_io.TRAIN_CASES)
+def test_train_forward_matches_dump(gpu_ctx, name):
+    print("train forward", name, flush=True)
+    g, cfg, view, params = _fixture(name)
+    tr = L.Trainer(gpu_ctx, params, g["sh_degree"])
+    img, T, pj, st = tr.forward(view, cfg, want_proj=True)
+    assert np.array_equal(pj["valid"], g["valid"])
+    assert np.array_equal(pj["visible"], g["visible"])
+    v = g["valid"]
+    for k in ("means2d", "conic", "colors", "opacity", "depth"):
+        assert np.allclose(pj[k][v], g[k][v], rtol=2e-5, atol=1e-6), k
+    assert float(np.abs(img - g["image"]).max()) < 1e-4
+    assert float(np.abs(T - g["final_T"]).max()) < 1e-4
+
+
+@pytest.mark.parametrize("name", golden_io.TRAIN_CASES)
+def test_train_backward_matches_dump(gpu_ctx, name):
+    print("train backward", name, flush=True)
+    g, cfg, view, params = _fixture(name)
+    tr = L.Trainer(gpu_ctx, params, g["sh_degree"])
+    tr.forward(view, cfg)
+    g2d, _ = tr.backward(cfg, dimage=g["dL_dimage"].astype(np.float32), want_g2d=True)
+    ref = {"dL_dmeans2d": g2d[:, 0:2], "dL_dconic": g2d[:, 2:5], "dL_dopacity": g2d[:, 5],
+           "dL_dcolors": g2d[:, 6:9]}
+    for k, a in ref.items():
+        e = rel_err(a, g[k])
+        print(k, e)
+        assert e < 1e-2, k
+    grads = tr.read(3)
+    for k in TO.PARAM_NAMES:
+        e = rel_err(grads[k], g["grad_" + k])
+        print("grad", k, e)
+        assert e < 1e-2, k
+
+
+@pytest.mark.parametrize("name", golden_io.TRAIN_CASES)
+def test_train_adam_matches_dump(gpu_ctx, name):
+    print("train adam", name, flush=True)
+    g, cfg, view, params = _fixture(name)
+    tr = L.Trainer(gpu_ctx, params, g["sh_degree"])
+    tr.write(1, {k: g["adam_m_in_" + k] for k in TO.PARAM_NAMES})
+    tr.write(2, {k: g["adam_v_in_" + k] for k in TO.PARAM_NAMES})
+    tr.write(3, {k: g["grad_" + k].astype(np.float32) for k in TO.PARAM_NAMES})
+    tr.set_visible(g["visible"])
+    tr.set_step(int(g["adam_step_in"]))
+    tr.adam(cfg)
+    p, m, v = tr.read(0), tr.read(1), tr.read(2)
+    for k in TO.PARAM_NAMES:
+        assert np.array_equal(m[k], g["adam_fp32_m_" + k]), k
+        assert np.array_equal(v[k], g["adam_fp32_v_" + k]), k
+        assert np.allclose(p[k], g["adam_fp32_param_" + k], rtol=0, atol=1e-7), k
+
+
+def _c5_small(n=1500, H=90, W=160, seed=55):
+    scene, tgt_scene, cams = scenes.config5(seed=seed, n=n)
+    K = scenes.intrinsics(0.5 * W / np.tan(np.deg2rad(25.0)), 0.5 * W / np.tan(np.deg2rad(25.0)),
+                          W / 2, H / 2)
+    return scenes.train_params(scene), scenes.train_params(tgt_scene), cams[0].w2c, K, H, W
+
+
+def test_train_steps_match_oracle(gpu_ctx):
+    """Three whole steps (forward + L1 + backward + sparse Adam) of a C5-shaped
+    scene (SH degree 1) against the oracle's steps from the same parameters."""
+    print("train steps c5-shaped", flush=True)
+    params, tparams, w2c, K, H, W = _c5_small()
+    cfg_o = TO.Cfg(sh_degree=1)
+    cfg = L.make_train_cfg()
+    view = L.make_view(w2c, K, H, W, tile_size=16)
+    # target: the oracle's render of the perturbed copy
+    _, target, _, _, _ = TO.forward(tparams, w2c, K, H, W, cfg_o)
+    target = target.astype(np.float32)
+    tr = L.Trainer(gpu_ctx, params, 1)
+    p_o = {k: v.astype(np.float32) for k, v in params.items()}
+    m_o = {k: np.zeros_like(v) for k, v in p_o.items()}
+    v_o = {k: np.zeros_like(v) for k, v in p_o.items()}
+    for step in range(3):
+        st = tr.step(view, cfg, target)
+        pr, img, fT, order, live = TO.forward(p_o, w2c, K, H, W, cfg_o)
+        loss, dimg = TO.l1_loss_grad(img, target)
+        g2 = TO.blend_backward(pr, order, live, fT, dimg, H, W, cfg_o)
+        grads = TO.projection_backward(pr, g2, cfg_o)
+        out = TO.sparse_adam(p_o, grads, m_o, v_o, step, pr["visible"])
+        p_o = {k: out[k][0] for k in out}
+        m_o = {k: out[k][1] for k in out}
+        v_o = {k: out[k][2] for k in out}
+        print(f"step {step}: loss gpu {st['loss']:.6f} oracle {loss:.6f}, M {st['num_blendable']}"
+              f" P {st['num_entries']}")
+        assert abs(st["loss"] - loss) <= 1e-4 * max(loss, 1e-6) + 1e-7
+    p = tr.read(0)
+    for k in TO.PARAM_NAMES:
+        d = np.abs(p[k] - p_o[k]).max()
+        moved = np.abs(p_o[k] - params[k]).max()
+        print(k, "max diff", d, "moved", moved)
+        assert d <= 1e-2 * max(moved, 1e-12) + 1e-6, k
