@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--n", type=int, default=6_000_000)
     ap.add_argument("--sort-keys", type=int, default=50_000_000)
     ap.add_argument("--no-sort", action="store_true")
+    ap.add_argument("--no-train", action="store_true")
+    ap.add_argument("--train-steps", type=int, default=20)
+    ap.add_argument("--train-n", type=int, default=1_000_000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-frames", type=int, default=10)
     ap.add_argument("--cpu-threads", type=int, default=16)
@@ -193,6 +196,44 @@ def bench_sort(ctx, n):
     }
 
 
+def bench_train(ctx, n, steps):
+    """Config 5: one training step = forward (3DGS rules) + L1 against a target +
+    blend/projection backward + sparse Adam, fp32, 1M Gaussians, SH degree 1,
+    1280x720. The target is the GPU forward of the perturbed copy."""
+    from gsplat_tt_amd import _lib as L
+    from gsplat_tt_amd import scenes
+
+    t = time.time()
+    scene, tgt_scene, cams = scenes.config5(n=n)
+    cam = cams[0]
+    log(f"train scene generated in {time.time() - t:.1f}s")
+    cfg = L.make_train_cfg()
+    view = L.make_view(cam.w2c, cam.K, cam.height, cam.width, tile_size=16)
+    tr = L.Trainer(ctx, scenes.train_params(tgt_scene), 1)
+    target, _, _, _ = tr.forward(view, cfg)
+    tr = L.Trainer(ctx, scenes.train_params(scene), 1)
+    H, W = cam.height, cam.width
+    dt = ctx.dev_alloc(H * W * 12)
+    ctx.h2d(dt, np.ascontiguousarray(target, np.float32))
+    for _ in range(2):
+        tr.step(view, cfg, dt, target_on_device=True)
+    stats = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        stats.append(tr.step(view, cfg, dt, target_on_device=True))
+    el = time.perf_counter() - t0
+    ctx.dev_free(dt)
+    avg = {k: float(np.mean([s[k] for s in stats])) for k in ("ms_forward", "ms_backward",
+                                                               "ms_adam")}
+    return {"workload": "training step, 1M Gaussians (64-component mixture), SH degree 1, "
+                        "1280x720, L1 vs render of a perturbed copy, sparse Adam, fp32",
+            "steps": steps, "ms_per_step": round(el / steps * 1e3, 4),
+            "steps_per_s": round(steps / el, 2),
+            "ms": {k[3:]: round(v, 4) for k, v in avg.items()},
+            "M": stats[-1]["num_blendable"], "pairs": stats[-1]["num_entries"],
+            "loss_first": round(stats[0]["loss"], 6), "loss_last": round(stats[-1]["loss"], 6)}
+
+
 def cpu_baseline(scene, cov, cams, frames, threads):
     """The reference's own CPU renderer (_gsplat_cpu.render_full, compiled from its
     sources into oracle/_ref) on a bounded sample of the same workload; SH colour
@@ -264,6 +305,9 @@ def main():
     if not args.no_sort:
         res["sort"] = bench_sort(ctx, args.sort_keys)
         log(f"sort: {res['sort']}")
+    if not args.no_train:
+        res["train"] = bench_train(ctx, args.train_n, args.train_steps)
+        log(f"train: {res['train']}")
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(scene, cov, cams, args.cpu_frames, args.cpu_threads)
     else:
