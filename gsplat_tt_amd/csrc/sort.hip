@@ -36,6 +36,25 @@ __device__ __forceinline__ uint64_t make_desc(uint32_t epoch, uint32_t flag, uin
     return ((uint64_t)epoch << 34) | ((uint64_t)flag << 32) | v;
 }
 
+// Look-back descriptors. 32-bit: [31:30] flag, [29:0] count, the array cleared
+// before every pass (key counts below 2^30). 64-bit: the epoch tag above, never
+// cleared.
+template <bool D32> struct Desc;
+template <> struct Desc<true> {
+    using T = uint32_t;
+    __device__ static T make(uint32_t, uint32_t flag, uint32_t v) { return (flag << 30) | v; }
+    __device__ static uint32_t flag(T s, uint32_t) { return s >> 30; }
+    __device__ static uint32_t val(T s) { return s & 0x3FFFFFFFu; }
+};
+template <> struct Desc<false> {
+    using T = uint64_t;
+    __device__ static T make(uint32_t e, uint32_t flag, uint32_t v) { return make_desc(e, flag, v); }
+    __device__ static uint32_t flag(T s, uint32_t e) {
+        return (uint32_t)(s >> 34) == e ? (uint32_t)(s >> 32) & 3u : 0u;
+    }
+    __device__ static uint32_t val(T s) { return (uint32_t)s; }
+};
+
 template <typename K>
 __device__ __forceinline__ uint32_t digit_of(K k, int shift, uint32_t mask) {
     return (uint32_t)(k >> shift) & mask;
@@ -56,23 +75,45 @@ __device__ __forceinline__ uint32_t block_excl_scan256(uint32_t v, uint32_t* s_t
     return pre + incl - v;
 }
 
+// Digit histograms of every pass in one read of the keys. Four keys per thread
+// per step keep several loads in flight; per wave and pass, the lanes whose digit
+// equals lane 0's add as one (skewed digits, e.g. the high bits of Zipf tile ids,
+// would otherwise serialise up to 64 lanes on one LDS bin).
+constexpr int kHistItems = 4;
 template <typename K>
 __global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ keys, int64_t n,
                                                        int begin_bit, int end_bit, int npass,
                                                        uint32_t* __restrict__ g_hist) {
     __shared__ uint32_t h[kWaves][kMaxPasses][256];
     const int w = threadIdx.x / GS_WAVE;
+    const int lane = lane_id();
     for (int i = threadIdx.x; i < kWaves * kMaxPasses * 256; i += kHistThreads)
         (&h[0][0][0])[i] = 0;
     __syncthreads();
-    const int64_t stride = (int64_t)gridDim.x * kHistThreads;
-    for (int64_t i = (int64_t)blockIdx.x * kHistThreads + threadIdx.x; i < n; i += stride) {
-        const K k = keys[i];
-        for (int p = 0; p < npass; ++p) {
-            const int shift = begin_bit + 8 * p;
-            const int bits = min(8, end_bit - shift);
-            const uint32_t d = digit_of(k, shift, (1u << bits) - 1u);
-            atomicAdd(&h[w][p][d], 1u);
+    constexpr int64_t kStep = (int64_t)kHistThreads * kHistItems;
+    const int64_t stride = (int64_t)gridDim.x * kStep;
+    // the loop bound is uniform over the workgroup, so every lane takes part in
+    // the ballots; lanes past n carry ok = false
+    for (int64_t base = (int64_t)blockIdx.x * kStep; base < n; base += stride) {
+        K k[kHistItems];
+        bool ok[kHistItems];
+#pragma unroll
+        for (int it = 0; it < kHistItems; ++it) {
+            const int64_t i = base + it * kHistThreads + threadIdx.x;
+            ok[it] = i < n;
+            k[it] = ok[it] ? keys[i] : K(0);
+        }
+#pragma unroll
+        for (int it = 0; it < kHistItems; ++it) {
+            for (int p = 0; p < npass; ++p) {
+                const int shift = begin_bit + 8 * p;
+                const int bits = min(8, end_bit - shift);
+                const uint32_t d = digit_of(k[it], shift, (1u << bits) - 1u);
+                const uint32_t d0 = __builtin_amdgcn_readfirstlane(d);
+                const uint64_t same = __ballot(ok[it] && d == d0);
+                if (ok[it] && d != d0) atomicAdd(&h[w][p][d], 1u);
+                if (lane == 0 && same != 0ull) atomicAdd(&h[w][p][d0], (uint32_t)__popcll(same));
+            }
         }
     }
     __syncthreads();
@@ -85,12 +126,15 @@ __global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ key
     }
 }
 
-template <typename K, bool IOTA, int THREADS, int ITEMS>
+template <typename K, bool IOTA, int THREADS, int ITEMS, bool D32>
 __global__ __launch_bounds__(THREADS) void k_onesweep(
     const K* __restrict__ kin, const uint32_t* __restrict__ vin, K* __restrict__ kout,
     uint32_t* __restrict__ vout, int64_t n_cap, const uint32_t* __restrict__ n_dev, int shift,
-    int bits, const uint32_t* __restrict__ g_hist_pass, uint64_t* __restrict__ state,
+    int bits, const uint32_t* __restrict__ g_hist_pass, void* __restrict__ state_raw,
     uint32_t* __restrict__ ticket, uint32_t epoch) {
+    using D = Desc<D32>;
+    using DT = typename D::T;
+    DT* state = static_cast<DT*>(state_raw);
     constexpr int WAVES = THREADS / GS_WAVE;
     constexpr int PART = THREADS * ITEMS;
     static_assert(THREADS >= 256, "one thread per digit");
@@ -164,29 +208,31 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
             s_wcnt[ww][tid] = tot;
             tot += c;
         }
-        if (vid == 0) {
-            st_agent(&state[tid], make_desc(epoch, 2u, tot));
+        // a digit absent from the whole pass publishes nothing and looks back at
+        // nothing (all partitions agree: the histogram is global)
+        if (g_hist_pass[tid] == 0u) {
+        } else if (vid == 0) {
+            st_agent(&state[tid], D::make(epoch, 2u, tot));
         } else {
-            st_agent(&state[(size_t)vid * 256 + tid], make_desc(epoch, 1u, tot));
+            st_agent(&state[(size_t)vid * 256 + tid], D::make(epoch, 1u, tot));
             // Look back kLbBatch predecessors per round trip: the loads are
             // independent, so one memory latency covers the whole batch.
             int64_t j = (int64_t)vid - 1;
             uint32_t spins = 0;
             bool done = false;
             while (!done) {
-                uint64_t sv[kLbBatch];
+                DT sv[kLbBatch];
 #pragma unroll
                 for (int q = 0; q < kLbBatch; ++q)
                     sv[q] = (j - q >= 0) ? ld_agent(&state[(size_t)(j - q) * 256 + tid])
-                                         : make_desc(epoch, 2u, 0u);
+                                         : D::make(epoch, 2u, 0u);
                 int used = 0;
 #pragma unroll
                 for (int q = 0; q < kLbBatch; ++q) {
                     if (done || used < q) continue;  // stop at the first gap
-                    const uint64_t s = sv[q];
-                    const uint32_t flag = (uint32_t)(s >> 32) & 3u;
-                    if ((uint32_t)(s >> 34) != epoch || flag == 0u) continue;
-                    excl += (uint32_t)s;
+                    const uint32_t flag = D::flag(sv[q], epoch);
+                    if (flag == 0u) continue;
+                    excl += D::val(sv[q]);
                     ++used;
                     if (flag == 2u) done = true;
                 }
@@ -200,7 +246,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
                     }
                 }
             }
-            st_agent(&state[(size_t)vid * 256 + tid], make_desc(epoch, 2u, excl + tot));
+            st_agent(&state[(size_t)vid * 256 + tid], D::make(epoch, 2u, excl + tot));
         }
     }
     // Exclusive scans over the 256 digits: partition-local offsets (tot) and
@@ -278,6 +324,32 @@ __global__ void k_iota_u32(uint32_t* p, size_t n) {
     if (i < n) p[i] = (uint32_t)i;
 }
 
+// One digit pass: clears the look-back descriptors of `grid` partitions (32-bit
+// ones below 2^30 keys, else 64-bit), then runs the onesweep kernel.
+template <typename K>
+hipError_t launch_pass(bool iota, const K* kin, const uint32_t* vin, K* kout, uint32_t* vout,
+                       int64_t n_cap, const uint32_t* n_dev, int shift, int bits,
+                       const uint32_t* hist_pass, SortTemp& tmp, uint32_t* ticket,
+                       hipStream_t st) {
+    constexpr int T = SweepCfg<K>::T, I = SweepCfg<K>::I;
+    const unsigned grid = (unsigned)((n_cap + T * I - 1) / (T * I));
+    const bool d32 = n_cap < ((int64_t)1 << 30);
+    const size_t words = (size_t)grid * 256 * (d32 ? 1 : 2);
+    k_fill_u32<<<(unsigned)((words + 255) / 256), 256, 0, st>>>(
+        reinterpret_cast<uint32_t*>(tmp.state), 0u, words);
+    const uint32_t epoch = ++tmp.epoch;
+#define GS_OS(IO, DD)                                                                        \
+    k_onesweep<K, IO, T, I, DD><<<grid, T, 0, st>>>(kin, vin, kout, vout, n_cap, n_dev, shift, \
+                                                    bits, hist_pass, tmp.state, ticket, epoch)
+    if (iota) {
+        if (d32) GS_OS(true, true); else GS_OS(true, false);
+    } else {
+        if (d32) GS_OS(false, true); else GS_OS(false, false);
+    }
+#undef GS_OS
+    return hipGetLastError();
+}
+
 template <typename K>
 hipError_t sort_impl(K* keys, uint32_t* vals, int64_t n, int begin_bit, int end_bit,
                      SortTemp& tmp, uint32_t* host_hist, hipStream_t st, int* passes_run,
@@ -295,7 +367,8 @@ hipError_t sort_impl(K* keys, uint32_t* vals, int64_t n, int begin_bit, int end_
         const size_t words = (size_t)kMaxPasses * 256 + kMaxPasses;
         k_fill_u32<<<(unsigned)((words + 255) / 256), 256, 0, st>>>(tmp.hist, 0u, words);
     }
-    const unsigned hgrid = (unsigned)std::min<int64_t>((n + 4095) / 4096, 1024);
+    const unsigned hgrid =
+        (unsigned)std::min<int64_t>((n + kHistThreads * kHistItems - 1) / (kHistThreads * kHistItems), 2048);
     k_hist<K><<<hgrid, kHistThreads, 0, st>>>(keys, n, begin_bit, end_bit, npass, tmp.hist);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = hipMemcpyAsync(host_hist, tmp.hist, (size_t)npass * 256 * 4,
@@ -308,8 +381,6 @@ hipError_t sort_impl(K* keys, uint32_t* vals, int64_t n, int begin_bit, int end_
     K* kalt = static_cast<K*>(tmp.keys_alt);
     uint32_t* valt = tmp.vals_alt;
     bool iota_pending = vals_iota;
-    constexpr int T = SweepCfg<K>::T, I = SweepCfg<K>::I;
-    const unsigned grid = (unsigned)((n + T * I - 1) / (T * I));
     uint32_t* tickets = tmp.hist + (size_t)kMaxPasses * 256;
     for (int p = 0; p < npass; ++p) {
         bool trivial = false;
@@ -318,20 +389,12 @@ hipError_t sort_impl(K* keys, uint32_t* vals, int64_t n, int begin_bit, int end_
         if (trivial) continue;
         const int shift = begin_bit + 8 * p;
         const int bits = std::min(8, end_bit - shift);
-        const uint32_t epoch = ++tmp.epoch;
         const bool timed = tmp.pass_events != nullptr && *passes_run < tmp.max_timed_passes;
         if (timed) (void)hipEventRecord(tmp.pass_events[2 * *passes_run], st);
-        if (iota_pending) {
-            k_onesweep<K, true, T, I><<<grid, T, 0, st>>>(
-                kin, vin, kalt, valt, n, nullptr, shift, bits, tmp.hist + p * 256,
-                tmp.state, tickets + p, epoch);
-            iota_pending = false;
-        } else {
-            k_onesweep<K, false, T, I><<<grid, T, 0, st>>>(
-                kin, vin, kalt, valt, n, nullptr, shift, bits, tmp.hist + p * 256,
-                tmp.state, tickets + p, epoch);
-        }
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        e = launch_pass<K>(iota_pending, kin, vin, kalt, valt, n, nullptr, shift, bits,
+                           tmp.hist + p * 256, tmp, tickets + p, st);
+        iota_pending = false;
+        if (e != hipSuccess) return e;
         if (timed) (void)hipEventRecord(tmp.pass_events[2 * *passes_run + 1], st);
         std::swap(kin, kalt);
         std::swap(vin, valt);
@@ -363,21 +426,11 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
     uint32_t* vin = vals;
     K* kalt = static_cast<K*>(tmp.keys_alt);
     uint32_t* valt = tmp.vals_alt;
-    constexpr int T = SweepCfg<K>::T, I = SweepCfg<K>::I;
-    const unsigned grid = (unsigned)((n_cap + T * I - 1) / (T * I));
     for (int p = 0; p < npass; ++p) {
         const int shift = begin_bit + 8 * p;
         const int bits = std::min(8, end_bit - shift);
-        const uint32_t epoch = ++tmp.epoch;
-        if (p == 0 && vals_iota)
-            k_onesweep<K, true, T, I><<<grid, T, 0, st>>>(kin, vin, kalt, valt, n_cap, n_dev,
-                                                          shift, bits, hist + p * 256, tmp.state,
-                                                          tickets + p, epoch);
-        else
-            k_onesweep<K, false, T, I><<<grid, T, 0, st>>>(kin, vin, kalt, valt, n_cap, n_dev,
-                                                           shift, bits, hist + p * 256, tmp.state,
-                                                           tickets + p, epoch);
-        hipError_t e = hipGetLastError();
+        hipError_t e = launch_pass<K>(p == 0 && vals_iota, kin, vin, kalt, valt, n_cap, n_dev,
+                                      shift, bits, hist + p * 256, tmp, tickets + p, st);
         if (e != hipSuccess) return e;
         std::swap(kin, kalt);
         std::swap(vin, valt);
