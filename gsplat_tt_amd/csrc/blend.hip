@@ -142,22 +142,29 @@ __device__ __forceinline__ bool mb_keep(const Band& g, float4 r0, float4 r1, int
     return m2_min <= -2.0f * lt;
 }
 
-__device__ __forceinline__ float rdl(float v, int j) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
-}
-
 // The batch loop of one band. INTERIOR: both microblocks lie fully inside the
 // image (AVX2 rule only, every pixel valid). Per-half state lives in VGPRs
 // (uniform within the half): `mine` = the half's kept entries of the batch
 // (cleared once the half is done), `cnt` = entries the half has blended; the
 // scalar unit only walks the union of both halves' masks.
+// The batch loop of one band. INTERIOR: both microblocks lie fully inside the
+// image (AVX2 rule only, every pixel valid). Per-half state lives in VGPRs
+// (uniform within the half): `mine` = the half's kept entries of the batch
+// (cleared once the half is done), `cnt` = entries the half has blended; the
+// scalar unit only walks the union of both halves' masks. The batch's entry
+// parameters are staged in LDS (mx, my, op | -ci_a/2, -ci_b, -ci_c/2 | r, g, b)
+// and read back with wave-uniform addresses (a broadcast, on the LDS pipe).
+struct BatchRec {
+    float4 p0, p1, p2;
+};
+
 template <bool INTERIOR>
 __device__ __forceinline__ void blend_band(const Band& g, const float4* __restrict__ brec,
                                            const uint32_t* __restrict__ sid, uint32_t start,
                                            uint32_t end, const BlendParams& bp, int lane,
-                                           float& T, float& cr, float& cg, float& cb,
-                                           uint32_t& cnt, uint32_t& n_batch, uint32_t& n_iter,
-                                           uint32_t& n_kept) {
+                                           BatchRec* s_rec, float& T, float& cr, float& cg,
+                                           float& cb, uint32_t& cnt, uint32_t& n_batch,
+                                           uint32_t& n_iter, uint32_t& n_kept) {
     const int h = lane >> 5, q = lane & 31;
     bool doneA = g.emptyA, doneB = g.emptyB;
     for (uint32_t base = start; base < end && !(doneA && doneB); base += 32) {
@@ -177,26 +184,22 @@ __device__ __forceinline__ void blend_band(const Band& g, const float4* __restri
         n_kept += (uint32_t)__popcll(mask);
         const uint32_t mA = (uint32_t)mask, mB = (uint32_t)(mask >> 32);
         uint32_t mine = h ? mB : mA;
-        // power coefficients of the AVX2 path (cull_and_blend.cpp:198-200),
-        // computed once per entry in its own lane
-        const float qA = -0.5f * r1.x, qB = -r1.y, qC = -0.5f * r1.z;
+        // power coefficients of the AVX2 path (cull_and_blend.cpp:198-200): exact
+        // scalings of the conic, so the image-edge rule recovers it exactly
+        if (h == 0) {
+            s_rec[q].p0 = make_float4(r0.x, r0.y, r2.x, 0.0f);
+            s_rec[q].p1 = make_float4(-0.5f * r1.x, -r1.y, -0.5f * r1.z, 0.0f);
+            s_rec[q].p2 = make_float4(r2.y, r2.z, r2.w, 0.0f);
+        }
+        __syncthreads();  // one wave per workgroup: orders the LDS writes and reads
         uint32_t uni = mA | mB;
         while (uni) {
             const int j = __builtin_ctz(uni);
             uni &= uni - 1;
             ++n_iter;
-            // v_readlane reads lane j whatever EXEC is: all reads happen here,
-            // in wave-uniform control flow
-            const float mx = rdl(r0.x, j), my = rdl(r0.y, j);
-            const float op = rdl(r2.x, j);
-            const float col_r = rdl(r2.y, j), col_g = rdl(r2.z, j), col_b = rdl(r2.w, j);
-            const float A = rdl(qA, j), B = rdl(qB, j), C = rdl(qC, j);
-            float ci_a = 0.0f, ci_b = 0.0f, ci_c = 0.0f;
-            if (!INTERIOR) {
-                ci_a = rdl(r1.x, j);
-                ci_b = rdl(r1.y, j);
-                ci_c = rdl(r1.z, j);
-            }
+            const float4 e0 = s_rec[j].p0, e1 = s_rec[j].p1, e2 = s_rec[j].p2;
+            const float mx = e0.x, my = e0.y, op = e0.z;
+            const float A = e1.x, B = e1.y, C = e1.z;
             const bool run = (mine >> j) & 1u;
             if (run) {
                 if (INTERIOR || g.full) {
@@ -214,11 +217,12 @@ __device__ __forceinline__ void blend_band(const Band& g, const float4* __restri
                     float al = op * gw;
                     al = (al < 0.99f) ? al : 0.99f;
                     const float at = al * T;
-                    cr = __builtin_fmaf(at, col_r, cr);
-                    cg = __builtin_fmaf(at, col_g, cg);
-                    cb = __builtin_fmaf(at, col_b, cb);
+                    cr = __builtin_fmaf(at, e2.x, cr);
+                    cg = __builtin_fmaf(at, e2.y, cg);
+                    cb = __builtin_fmaf(at, e2.z, cb);
                     T = T - at;
                 } else if (g.pix_valid) {
+                    const float ci_a = -2.0f * A, ci_b = -B, ci_c = -2.0f * C;
                     const float dx = g.pxc - mx;
                     const float dy = g.pyc - my;
                     const float power =
@@ -226,9 +230,9 @@ __device__ __forceinline__ void blend_band(const Band& g, const float4* __restri
                     const float gw = expf(fmin_std(power, 0.0f));
                     const float al = fmin_std(op * gw, 0.99f);
                     const float at = al * T;
-                    cr += at * col_r;
-                    cg += at * col_g;
-                    cb += at * col_b;
+                    cr += at * e2.x;
+                    cg += at * e2.y;
+                    cb += at * e2.z;
                     T = T * (1.0f - al);
                 }
                 ++cnt;
@@ -251,6 +255,7 @@ __device__ __forceinline__ void blend_band(const Band& g, const float4* __restri
                 if (doneA && doneB) return;
             }
         }
+        __syncthreads();  // the next batch overwrites the staged records
     }
 }
 
@@ -264,12 +269,13 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
     float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
     uint32_t cnt = 0, n_batch = 0, n_iter = 0, n_kept = 0;
     const uint32_t start = ranges[2 * g.tile], end = ranges[2 * g.tile + 1];
+    __shared__ BatchRec s_rec[32];
     if (g.fullA && g.fullB)
-        blend_band<true>(g, brec, sid, start, end, bp, lane, T, cr, cg, cb, cnt, n_batch, n_iter,
-                         n_kept);
+        blend_band<true>(g, brec, sid, start, end, bp, lane, s_rec, T, cr, cg, cb, cnt, n_batch,
+                         n_iter, n_kept);
     else
-        blend_band<false>(g, brec, sid, start, end, bp, lane, T, cr, cg, cb, cnt, n_batch, n_iter,
-                          n_kept);
+        blend_band<false>(g, brec, sid, start, end, bp, lane, s_rec, T, cr, cg, cb, cnt, n_batch,
+                          n_iter, n_kept);
 
     if (bp.evals != nullptr) {
         // pixel-Gaussian evaluations = sum over valid pixels of entries blended
