@@ -24,6 +24,7 @@ constexpr int kCountItems = 4;
 constexpr int kCountPart = kThreads * kCountItems;   // ranks per scan partition
 constexpr int kEmitItems = 8;
 constexpr int kEmitPart = kThreads * kEmitItems;     // candidates per emit partition
+constexpr int kRankCache = 384;
 static_assert(kEmitPart == (int)kEmitPartition, "emit partition size is part of the interface");
 
 __device__ __forceinline__ float fmin_std(float a, float b) { return (b < a) ? b : a; }
@@ -198,6 +199,10 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     __shared__ uint32_t s_xy[kEmitPart + 1];
     __shared__ uint32_t s_w[kEmitPart + 1];
     __shared__ uint32_t s_own[kEmitPart];
+    // centre and conic of the first kRankCache ranks (the usual partition has
+    // ~10x fewer ranks than candidates; larger ones read them from memory)
+    __shared__ float2 s_pc[kRankCache];
+    __shared__ float4 s_cv[kRankCache];
     __shared__ uint32_t s_wmax[kWaves];
     __shared__ uint32_t s_cnt[kEmitItems][kWaves];
     __shared__ uint32_t s_th[2][256];
@@ -224,8 +229,13 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     for (int64_t k = tid; k < nr; k += kThreads) {
         const int64_t r = rlo + k;
         const uint32_t g = order ? order[r] : (uint32_t)r;
-        const Rect q = tile_rect(rect_r[r], tp);
+        const float4 rr = rect_r[r];
+        const Rect q = tile_rect(rr, tp);
         const uint32_t o = offs[r];
+        if (k < kRankCache) {
+            s_pc[k] = make_float2(rr.x, rr.y);
+            if (tp.cull) s_cv[k] = cov_r[r];
+        }
         s_off[k] = o;
         s_g[k] = g;
         s_xy[k] = (uint32_t)q.x0 | ((uint32_t)q.y0 << 16);
@@ -279,10 +289,14 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
             const uint32_t g = s_g[lo];
             bool k = true;
             if (tp.cull) {
-                // rank-ordered records: the partition's few ranks stay in L1
-                const int64_t r = rlo + lo;
-                const float4 rr = rect_r[r];
-                k = pair_keep(rr.x, rr.y, cov_r[r], tx, ty, tp);
+                if (nr <= kRankCache) {
+                    const float2 pc = s_pc[lo];
+                    k = pair_keep(pc.x, pc.y, s_cv[lo], tx, ty, tp);
+                } else {
+                    const int64_t r = rlo + lo;
+                    const float4 rr = rect_r[r];
+                    k = pair_keep(rr.x, rr.y, cov_r[r], tx, ty, tp);
+                }
             }
             keep[it] = k;
             tile[it] = (uint32_t)t;
