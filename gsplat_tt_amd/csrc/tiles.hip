@@ -302,6 +302,11 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
             tile[it] = (uint32_t)t;
             gid[it] = g;
         }
+    }
+    // bookkeeping after all candidates are evaluated, so the evaluations of the
+    // eight candidates can overlap
+#pragma unroll
+    for (int it = 0; it < kEmitItems; ++it) {
         bal[it] = __ballot(keep[it]);
         if (lane == 0) s_cnt[it][w] = (uint32_t)__popcll(bal[it]);
         if (part_hist != nullptr && keep[it]) {
