@@ -53,6 +53,16 @@ __device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
     return v;
 }
 
+// LDS histogram increment of `bin` for the lanes with `on` set: the lanes whose
+// bin equals lane 0's add as one atomic (a skewed digit would otherwise
+// serialise up to 64 lanes on one LDS address). Call from uniform control flow.
+__device__ __forceinline__ void hist_add_wave(uint32_t* hist, uint32_t bin, bool on) {
+    const uint32_t b0 = __builtin_amdgcn_readfirstlane(bin);
+    const uint64_t same = __ballot(on && bin == b0);
+    if (on && bin != b0) atomicAdd(&hist[bin], 1u);
+    if (lane_id() == 0 && same != 0ull) atomicAdd(&hist[b0], (uint32_t)__popcll(same));
+}
+
 // ---------------------------------------------------------------------------
 // Decoupled look-back over a chain of 64-bit partition descriptors.
 // Descriptor = flag (2 bits, 62..63) | value (62 bits). flag 0 = not yet

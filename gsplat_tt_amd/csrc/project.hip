@@ -178,13 +178,13 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
         }
         bal[it] = __ballot(valid[it]);
         if (lane == 0) s_cnt[it][w] = (uint32_t)__popcll(bal[it]);
-        if (part_hist != nullptr && valid[it]) {
+        if (part_hist != nullptr) {
             // digit histograms of the depth keys, for the depth sort's passes
             const uint32_t k = __float_as_uint(vtz[it]);
-            atomicAdd(&s_hist[0][k & 255u], 1u);
-            atomicAdd(&s_hist[1][(k >> 8) & 255u], 1u);
-            atomicAdd(&s_hist[2][(k >> 16) & 255u], 1u);
-            atomicAdd(&s_hist[3][k >> 24], 1u);
+            hist_add_wave(s_hist[0], k & 255u, valid[it]);
+            hist_add_wave(s_hist[1], (k >> 8) & 255u, valid[it]);
+            hist_add_wave(s_hist[2], (k >> 16) & 255u, valid[it]);
+            hist_add_wave(s_hist[3], k >> 24, valid[it]);
         }
     }
     __syncthreads();

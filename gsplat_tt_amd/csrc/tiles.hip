@@ -309,10 +309,10 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     for (int it = 0; it < kEmitItems; ++it) {
         bal[it] = __ballot(keep[it]);
         if (lane == 0) s_cnt[it][w] = (uint32_t)__popcll(bal[it]);
-        if (part_hist != nullptr && keep[it]) {
+        if (part_hist != nullptr) {
             // digit histograms of the tile keys, for the tile sort's passes
-            atomicAdd(&s_th[0][tile[it] & 255u], 1u);
-            atomicAdd(&s_th[1][(tile[it] >> 8) & 255u], 1u);
+            hist_add_wave(s_th[0], tile[it] & 255u, keep[it]);
+            hist_add_wave(s_th[1], (tile[it] >> 8) & 255u, keep[it]);
         }
     }
     __syncthreads();

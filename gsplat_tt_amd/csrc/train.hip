@@ -212,6 +212,7 @@ __global__ __launch_bounds__(kTThreads) void k_train_project(
     for (int it = 0; it < kTItems; ++it) {
         const int64_t i = base + it * kTThreads + tid;
         keep[it] = false;
+        depth[it] = 0.0f;
         if (i < n) {
             Geo g;
             geometry(P, i, cam, g);
@@ -258,13 +259,13 @@ __global__ __launch_bounds__(kTThreads) void k_train_project(
                 dbg.valid[i] = g.valid ? 1 : 0;
             }
             if (!k) cidx[i] = 0xFFFFFFFFu;
-            if (k) {
-                const uint32_t key = __float_as_uint(g.z);
-                atomicAdd(&s_hist[0][key & 255u], 1u);
-                atomicAdd(&s_hist[1][(key >> 8) & 255u], 1u);
-                atomicAdd(&s_hist[2][(key >> 16) & 255u], 1u);
-                atomicAdd(&s_hist[3][key >> 24], 1u);
-            }
+        }
+        {
+            const uint32_t key = __float_as_uint(depth[it]);
+            hist_add_wave(s_hist[0], key & 255u, keep[it]);
+            hist_add_wave(s_hist[1], (key >> 8) & 255u, keep[it]);
+            hist_add_wave(s_hist[2], (key >> 16) & 255u, keep[it]);
+            hist_add_wave(s_hist[3], key >> 24, keep[it]);
         }
         bal[it] = __ballot(keep[it]);
         if (lane == 0) s_cnt[it][w] = (uint32_t)__popcll(bal[it]);
