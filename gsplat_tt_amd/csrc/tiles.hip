@@ -37,17 +37,11 @@ struct Rect {
 // q = j / w, r = j % w for j < 2^24 and a quotient below 2^16 (a tile row of a
 // Gaussian's rectangle): float reciprocal estimate, then one exact correction.
 __device__ __forceinline__ void divmod_small(uint32_t j, uint32_t w, uint32_t& q, uint32_t& r) {
-    int qi = (int)((float)j * __builtin_amdgcn_rcpf((float)w));
-    int ri = (int)j - qi * (int)w;
-    if (ri < 0) {
-        --qi;
-        ri += (int)w;
-    } else if (ri >= (int)w) {
-        ++qi;
-        ri -= (int)w;
-    }
-    q = (uint32_t)qi;
-    r = (uint32_t)ri;
+    const int qi = (int)((float)j * __builtin_amdgcn_rcpf((float)w));
+    const int ri = (int)j - qi * (int)w;
+    const int fix = (ri < 0) ? -1 : ((ri >= (int)w) ? 1 : 0);
+    q = (uint32_t)(qi + fix);
+    r = (uint32_t)(ri - fix * (int)w);
 }
 
 __device__ __forceinline__ Rect tile_rect(float4 r, const TileParams& tp) {
@@ -60,11 +54,13 @@ __device__ __forceinline__ Rect tile_rect(float4 r, const TileParams& tp) {
     return o;
 }
 
-// tile_assign.cpp:151-290, one (Gaussian, tile) pair.
+// tile_assign.cpp:151-290, one (Gaussian, tile) pair. Both edge distances are
+// always evaluated and the unused one is selected away, so the test has no
+// branches and the evaluations of several candidates can be interleaved; the
+// values compared are the same expressions as in the reference's test.
 __device__ __forceinline__ bool pair_keep(float px, float py, float4 cv, int tile_x, int tile_y,
                                           const TileParams& tp) {
     const float m2thr = cv.w;
-    if (!(m2thr >= 0.0f)) return false;  // opacity <= floor
     const float a = cv.x, b = cv.y, c = cv.z;
     const float det = fmax_std(a * c - b * b, 1e-6f);
     const float ts = (float)tp.tile_size;
@@ -74,26 +70,24 @@ __device__ __forceinline__ bool pair_keep(float px, float py, float4 cv, int til
     const float u_hi = u_lo + ts;
     const float v_lo = ty_tile - py;
     const float v_hi = v_lo + ts;
-    const bool x_in = (u_lo <= 0.0f) && (0.0f <= u_hi);
-    const bool y_in = (v_lo <= 0.0f) && (0.0f <= v_hi);
+    const bool x_in = (u_lo <= 0.0f) & (0.0f <= u_hi);
+    const bool y_in = (v_lo <= 0.0f) & (0.0f <= v_hi);
     const float scaled = det * m2thr;
-    if (x_in && y_in) return true;
-    float m2_v = __builtin_inff(), m2_h = __builtin_inff();
-    if (!x_in) {
-        const float uf = (u_lo > 0.0f) ? u_lo : u_hi;
-        const float a_safe = fmax_std(a, 1e-12f);
-        float vs = (b * uf) / a_safe;
-        vs = fmax_std(v_lo, fmin_std(vs, v_hi));
-        m2_v = c * uf * uf - 2.0f * b * uf * vs + a * vs * vs;
-    }
-    if (!y_in) {
-        const float vf = (v_lo > 0.0f) ? v_lo : v_hi;
-        const float c_safe = fmax_std(c, 1e-12f);
-        float us = (b * vf) / c_safe;
-        us = fmax_std(u_lo, fmin_std(us, u_hi));
-        m2_h = c * us * us - 2.0f * b * us * vf + a * vf * vf;
-    }
-    return fmin_std(m2_v, m2_h) <= scaled;
+    // nearest point on the vertical edge facing the centre (used when !x_in)
+    const float uf = (u_lo > 0.0f) ? u_lo : u_hi;
+    const float a_safe = fmax_std(a, 1e-12f);
+    float vs = (b * uf) / a_safe;
+    vs = fmax_std(v_lo, fmin_std(vs, v_hi));
+    const float m2_v = x_in ? __builtin_inff() : c * uf * uf - 2.0f * b * uf * vs + a * vs * vs;
+    // nearest point on the horizontal edge facing the centre (used when !y_in)
+    const float vf = (v_lo > 0.0f) ? v_lo : v_hi;
+    const float c_safe = fmax_std(c, 1e-12f);
+    float us = (b * vf) / c_safe;
+    us = fmax_std(u_lo, fmin_std(us, u_hi));
+    const float m2_h = y_in ? __builtin_inff() : c * us * us - 2.0f * b * us * vf + a * vf * vf;
+    // opacity <= floor (m2thr < 0 or NaN) never keeps
+    // bitwise operators: no short-circuit branches around the divisions
+    return (m2thr >= 0.0f) & ((x_in & y_in) | (fmin_std(m2_v, m2_h) <= scaled));
 }
 
 // Rectangle area per rank, exclusive scan -> offs[r]; last partition writes
@@ -268,39 +262,55 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     }
     __syncthreads();
 
+    // Every slot of s_own holds a rank in [0, nr), also past c1, so all LDS
+    // reads below are issued unconditionally, item by item in stages, and the
+    // eight evaluations overlap instead of waiting on each other.
     bool keep[kEmitItems];
     uint32_t tile[kEmitItems], gid[kEmitItems];
     uint64_t bal[kEmitItems];
+    uint32_t lo[kEmitItems], off[kEmitItems], wdt[kEmitItems], xy[kEmitItems];
+    int tx[kEmitItems], ty[kEmitItems];
+#pragma unroll
+    for (int it = 0; it < kEmitItems; ++it) lo[it] = s_own[it * kThreads + tid];
+#pragma unroll
+    for (int it = 0; it < kEmitItems; ++it) {
+        off[it] = s_off[lo[it]];
+        wdt[it] = s_w[lo[it]];
+        xy[it] = s_xy[lo[it]];
+        gid[it] = s_g[lo[it]];
+    }
 #pragma unroll
     for (int it = 0; it < kEmitItems; ++it) {
         const uint64_t c = c0 + it * kThreads + tid;
-        keep[it] = false;
-        tile[it] = 0;
-        gid[it] = 0;
-        if (c < c1) {
-            const uint32_t lo = s_own[it * kThreads + tid];
-            const uint32_t j = (uint32_t)c - s_off[lo];
-            const uint32_t wdt = s_w[lo];
-            const uint32_t xy = s_xy[lo];
-            uint32_t row, col;
-            divmod_small(j, wdt, row, col);
-            const int ty = (int)((xy >> 16) + row), tx = (int)((xy & 0xFFFFu) + col);
-            const int t = ty * tp.tiles_x + tx;
-            const uint32_t g = s_g[lo];
-            bool k = true;
-            if (tp.cull) {
-                if (nr <= kRankCache) {
-                    const float2 pc = s_pc[lo];
-                    k = pair_keep(pc.x, pc.y, s_cv[lo], tx, ty, tp);
-                } else {
-                    const int64_t r = rlo + lo;
-                    const float4 rr = rect_r[r];
-                    k = pair_keep(rr.x, rr.y, cov_r[r], tx, ty, tp);
-                }
+        uint32_t row, col;
+        divmod_small((uint32_t)c - off[it], wdt[it], row, col);
+        ty[it] = (int)((xy[it] >> 16) + row);
+        tx[it] = (int)((xy[it] & 0xFFFFu) + col);
+        tile[it] = (uint32_t)(ty[it] * tp.tiles_x + tx[it]);
+        keep[it] = c < c1;
+    }
+    if (tp.cull) {
+        if (nr <= kRankCache) {
+            float2 pc[kEmitItems];
+            float4 cv[kEmitItems];
+#pragma unroll
+            for (int it = 0; it < kEmitItems; ++it) {
+                pc[it] = s_pc[lo[it]];
+                cv[it] = s_cv[lo[it]];
             }
-            keep[it] = k;
-            tile[it] = (uint32_t)t;
-            gid[it] = g;
+#pragma unroll
+            for (int it = 0; it < kEmitItems; ++it)
+                keep[it] = keep[it] & pair_keep(pc[it].x, pc[it].y, cv[it], tx[it], ty[it], tp);
+        } else {
+            float4 rr[kEmitItems], cv[kEmitItems];
+#pragma unroll
+            for (int it = 0; it < kEmitItems; ++it) {
+                rr[it] = rect_r[rlo + lo[it]];
+                cv[it] = cov_r[rlo + lo[it]];
+            }
+#pragma unroll
+            for (int it = 0; it < kEmitItems; ++it)
+                keep[it] = keep[it] & pair_keep(rr[it].x, rr[it].y, cv[it], tx[it], ty[it], tp);
         }
     }
     // bookkeeping after all candidates are evaluated, so the evaluations of the
