@@ -10,7 +10,9 @@ out analytically:
     3-sigma visibility for sparse Adam, per-pixel front-to-back blend: skip
     alpha < alpha_min, stop - without blending - when T * (1 - alpha) < t_min,
     alpha clamp alpha_max, out = C + T * background);
-  * L1 gradient: train_loss.py:166-171 (mean |x - y| over 3HW, sign(0) = 0);
+  * L1 gradient: train_loss.py:166-171 (mean |x - y| over 3HW, sign(0) = 0; the
+    reference's device step also scales it by 1 - lambda_dssim = 0.8, here a
+    `scale` argument);
   * blend backward: the reverse recursion over each pixel's live pairs;
   * projection backward: conic -> cov2d -> (J, cov3d) -> means / log-scales /
     quaternions, opacity logit, SH coefficients and the SH view direction;
