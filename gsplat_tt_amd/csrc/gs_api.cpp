@@ -217,7 +217,7 @@ struct gs_ctx {
         b_opac.ensure(std::max<int64_t>(n, 1) * 4);
         b_col.ensure(std::max<int64_t>(n, 1) * col_planes * 4);
         b_terms.ensure(std::max<int64_t>(n, 1) * 3 * 4);
-        const int max_cols = std::max(std::max(3, s->cov3d_stride), col_planes);
+        const int max_cols = std::max(3, s->cov3d_stride);
         b_upload.ensure(std::max<int64_t>(n, 1) * max_cols * 4);
         float* up = b_upload.as<float>();
         auto transpose = [&](const float* host, int cols, const int* map, int planes, float* dst) {
@@ -231,9 +231,10 @@ struct gs_ctx {
         const int u9[6] = {0, 1, 2, 4, 5, 8};
         const int u6[6] = {0, 1, 2, 3, 4, 5};
         transpose(s->cov3d, s->cov3d_stride, s->cov3d_stride == 9 ? u9 : u6, 6, b_cov.as<float>());
-        std::vector<int> cmap(col_planes);
-        for (int j = 0; j < col_planes; ++j) cmap[j] = j;
-        transpose(s->colors, col_planes, cmap.data(), col_planes, b_col.as<float>());
+        // colour records stay per Gaussian (only visible ones are read)
+        if (n > 0)
+            HIPCHK(hipMemcpyAsync(b_col.p, s->colors, (size_t)n * col_planes * 4,
+                                  hipMemcpyHostToDevice, st));
         has_opac = s->opacities != nullptr;
         h_opac.assign(has_opac ? (size_t)n : 0, 0.0f);
         if (has_opac && n > 0) {
@@ -247,11 +248,7 @@ struct gs_ctx {
         for (int c = 0; c < 3; ++c) sd.mean[c] = b_mean.as<float>() + (size_t)c * n;
         for (int c = 0; c < 6; ++c) sd.cov[c] = b_cov.as<float>() + (size_t)c * n;
         sd.opac = has_opac ? b_opac.as<float>() : nullptr;
-        if (s->sh_degree < 0) {
-            for (int c = 0; c < 3; ++c) sd.col[c] = b_col.as<float>() + (size_t)c * n;
-        } else {
-            sd.sh = b_col.as<float>();
-        }
+        sd.sh = b_col.as<float>();
         sd.kfac = b_terms.as<float>();
         sd.m2thr = b_terms.as<float>() + (size_t)n;
         sd.lthr = b_terms.as<float>() + 2 * (size_t)n;

@@ -16,7 +16,8 @@ struct SceneDev {
     float* mean[3] = {nullptr, nullptr, nullptr};
     float* cov[6] = {};        // c00 c01 c02 c11 c12 c22
     float* opac = nullptr;
-    float* col[3] = {nullptr, nullptr, nullptr};
+    // per-Gaussian colour record, n x 3K floats as the scene gives it: RGB
+    // (K = 1, sh_degree -1) or SH coefficient k channel c at [i*3K + k*3 + c]
     float* sh = nullptr;
     // Per-Gaussian terms that depend only on opacity and the floors; they
     // are computed on the host with the C library's logf so every log on the

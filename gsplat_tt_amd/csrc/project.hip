@@ -27,10 +27,30 @@ __device__ __forceinline__ float fmin_std(float a, float b) { return (b < a) ? b
 __device__ __forceinline__ float fmax_std(float a, float b) { return (a < b) ? b : a; }
 
 // 3DGS real SH basis (gsplat/train_oracle.py:46-52, 99-122), fp32,
-// left-to-right. `sh` planes: coefficient k, channel c at sh[(k*3+c)*n + i].
+// left-to-right. `rec` is one Gaussian's record of (DEG+1)^2 coefficients x 3
+// channels, coefficient k channel c at rec[k*3 + c] (the scene's own layout).
+// Only visible Gaussians are evaluated, so a per-Gaussian record touches just
+// the cache lines of the Gaussians on screen, where planes would touch nearly
+// every line of every plane.
 template <int DEG>
-__device__ __forceinline__ void sh_eval(const float* __restrict__ sh, int64_t n, int64_t i,
-                                        float x, float y, float z, int clamp_hi, float* rgb) {
+__device__ __forceinline__ void sh_eval(const float* __restrict__ rec, float x, float y, float z,
+                                        int clamp_hi, float* rgb) {
+    constexpr int K = (DEG + 1) * (DEG + 1);
+    float v[3 * K];
+    if constexpr ((3 * K) % 4 == 0) {
+        // records of degree 1 and 3 are 16-byte aligned: whole-vector loads
+#pragma unroll
+        for (int q = 0; q < 3 * K / 4; ++q) {
+            const float4 t = reinterpret_cast<const float4*>(rec)[q];
+            v[4 * q + 0] = t.x;
+            v[4 * q + 1] = t.y;
+            v[4 * q + 2] = t.z;
+            v[4 * q + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 3 * K; ++q) v[q] = rec[q];
+    }
     constexpr float C0 = 0.28209479177387814f;
     constexpr float C1 = 0.4886025119029199f;
     constexpr float C20 = 1.0925484305920792f, C21 = -1.0925484305920792f,
@@ -44,7 +64,7 @@ __device__ __forceinline__ void sh_eval(const float* __restrict__ sh, int64_t n,
     const float xy = x * y, yz = y * z, xz = x * z;
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-        auto S = [&](int k) { return sh[(int64_t)(k * 3 + c) * n + i]; };
+        auto S = [&](int k) { return v[k * 3 + c]; };
         float o = C0 * S(0);
         if (DEG >= 1) {
             o = o - C1 * y * S(1) + C1 * z * S(2) - C1 * x * S(3);
@@ -236,16 +256,17 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
         }
         float rgb[3];
         if (DEG < 0) {
-            rgb[0] = s.col[0][i];
-            rgb[1] = s.col[1][i];
-            rgb[2] = s.col[2][i];
+            rgb[0] = s.sh[i * 3 + 0];
+            rgb[1] = s.sh[i * 3 + 1];
+            rgb[2] = s.sh[i * 3 + 2];
         } else {
             const float dx = s.mean[0][i] - p.ccx;
             const float dy = s.mean[1][i] - p.ccy;
             const float dz = s.mean[2][i] - p.ccz;
             const float nrm = sqrtf(dx * dx + dy * dy + dz * dz);
-            sh_eval<(DEG < 0 ? 0 : DEG)>(s.sh, n, i, dx / nrm, dy / nrm, dz / nrm,
-                                         p.sh_clamp_hi, rgb);
+            constexpr int D = DEG < 0 ? 0 : DEG;
+            sh_eval<D>(s.sh + i * (3 * (D + 1) * (D + 1)), dx / nrm, dy / nrm, dz / nrm,
+                       p.sh_clamp_hi, rgb);
         }
         const float op = p.has_opac ? s.opac[i] : 1.0f;
         out.brec[m * 3 + 0] = make_float4(vmx[it], vmy[it], xh, yh);

@@ -49,6 +49,29 @@ def test_project_bitexact(gpu_ctx, ts):
         assert np.array_equal(_bits(g[k]), _bits(o[k])), k
 
 
+@pytest.mark.parametrize("deg", [0, 1, 2, 3])
+@pytest.mark.parametrize("clamp", [True, False])
+def test_project_sh_colour_bitexact(gpu_ctx, deg, clamp):
+    """Colour from SH of every degree inside the fused projection, bit-exact
+    against the oracle's SH evaluation (train_oracle.py:99-122) of the visible
+    Gaussians; the per-Gaussian records have odd lengths (3, 12, 27, 48 floats)."""
+    scene, cam, cov = _scene(20_000, 40 + deg)
+    rng = np.random.default_rng(deg)
+    K = (deg + 1) ** 2
+    sh = rng.standard_normal((scene.n, K, 3)).astype(np.float32) * np.float32(0.4)
+    sh[:, 0, :] = rng.uniform(-0.5, 2.5, (scene.n, 3)).astype(np.float32)
+    view = L.make_view(cam.w2c, cam.K, cam.height, cam.width, tile_size=16, sh_clamp=clamp)
+    g = gpu_ctx.project(scene.means, cov, scene.opacities, sh, view, sh_degree=deg)
+    o = O.project(scene.means, cov, cam.w2c, cam.K, scene.colors, scene.opacities,
+                  cam.height, cam.width)
+    assert np.array_equal(g["valid"], o["valid"])
+    ref = O.sh_rgb(scene.means, sh, deg, cam.w2c, clamp_hi=clamp)[o["valid"]]
+    assert ref.shape[0] > 1000
+    if not clamp:
+        assert (ref > 1.0).any()
+    assert np.array_equal(_bits(g["colors"]), _bits(ref))
+
+
 @pytest.mark.parametrize("ts", [16, 32])
 def test_tile_assign_bitexact(gpu_ctx, ts):
     scene, cam, cov = _scene(30_000, 22)
