@@ -166,7 +166,7 @@ struct gs_ctx {
     DevBuf b_mean, b_cov, b_opac, b_col, b_terms, b_upload;
 
     // frame
-    DevBuf b_rect, b_covc, b_dkey, b_brec, b_src, b_valid;
+    DevBuf b_rc, b_dkey, b_brec, b_src, b_valid;
     DevBuf b_offs, b_bstart, b_pair_tile, b_pair_id, b_ranges, b_out;
     DevBuf b_kalt, b_valt, b_hist, b_state, b_lb, b_cnt;
     DevBuf b_tmp_a, b_tmp_b, b_tmp_c, b_evals;
@@ -176,7 +176,7 @@ struct gs_ctx {
 
     ~gs_ctx() {
         if (st) (void)hipStreamSynchronize(st);
-        for (DevBuf* b : {&b_mean, &b_cov, &b_opac, &b_col, &b_terms, &b_upload, &b_rect, &b_covc,
+        for (DevBuf* b : {&b_mean, &b_cov, &b_opac, &b_col, &b_terms, &b_upload, &b_rc,
                           &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_bstart, &b_pair_tile, &b_pair_id,
                           &b_ranges, &b_out, &b_kalt, &b_valt, &b_hist, &b_state, &b_lb, &b_cnt,
                           &b_tmp_a, &b_tmp_b, &b_tmp_c, &b_evals, &b_frame, &b_phist_proj,
@@ -363,12 +363,11 @@ struct gs_ctx {
         return ms;
     }
 
-    // Project + compaction. Returns M; compact arrays in b_rect/b_covc/b_dkey/b_brec.
+    // Project + compaction. Returns M; compact arrays in b_rc/b_dkey/b_brec.
     int64_t run_project(const gs_view* v, bool want_valid, bool want_src) {
         const int64_t n = sd.n;
         ensure_counters();
-        b_rect.ensure(std::max<int64_t>(n, 1) * 16);
-        b_covc.ensure(std::max<int64_t>(n, 1) * 16);
+        b_rc.ensure(std::max<int64_t>(n, 1) * 32);
         b_dkey.ensure(std::max<int64_t>(n, 1) * 4);
         b_brec.ensure(std::max<int64_t>(n, 1) * 48);
         if (want_src) b_src.ensure(std::max<int64_t>(n, 1) * 4);
@@ -379,7 +378,7 @@ struct gs_ctx {
         HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, parts * 2, st));
         if (n == 0) return 0;
         gs::ProjParams p = proj_params(v);
-        gs::Compact c{b_rect.as<float4>(), b_covc.as<float4>(), b_dkey.as<uint32_t>(),
+        gs::Compact c{b_rc.as<float4>(), b_dkey.as<uint32_t>(),
                       b_brec.as<float4>(), want_src ? b_src.as<uint32_t>() : nullptr};
         HIPCHK(gs::launch_project(sd, p, c, want_valid ? b_valid.as<uint8_t>() : nullptr,
                                   b_lb.as<uint64_t>(), b_cnt.as<uint32_t>() + 0,
@@ -402,7 +401,7 @@ struct gs_ctx {
         for (int attempt = 0; attempt < 2; ++attempt) {
             HIPCHK(gs::launch_fill_u32(b_cnt.as<uint32_t>() + 8, 0u, 8, st));
             HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, rparts * 2, st));
-            HIPCHK(gs::launch_rect_count_scan(rect, cov, order, m, nullptr, tp,
+            HIPCHK(gs::launch_rect_count_scan(rect, cov, 1, order, m, nullptr, tp,
                                               b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(),
                                               (uint32_t)(b_bstart.cap / 4), b_lb.as<uint64_t>(),
                                               b_cnt.as<uint32_t>() + 8, b_cnt.as<uint32_t>() + 9,
@@ -530,8 +529,7 @@ struct gs_ctx {
         L.pparts = gs::project_partitions(N);
         L.rparts = gs::rect_scan_partitions(N);
         L.eparts = gs::emit_partitions(L.pcap);
-        b_rect.ensure((size_t)N * 16);
-        b_covc.ensure((size_t)N * 16);
+        b_rc.ensure((size_t)N * 32);
         b_dkey.ensure((size_t)N * 4);
         b_brec.ensure((size_t)N * 48);
         b_src.ensure((size_t)N * 4);
@@ -571,7 +569,7 @@ struct gs_ctx {
                                         fr + kFrDepthHist, cnt + C_DSORT_TICKETS, sort, st, true,
                                         &kf, &order));
         record(2);
-        HIPCHK(gs::launch_rect_count_scan(b_rect.as<float4>(), b_covc.as<float4>(), order, N,
+        HIPCHK(gs::launch_rect_count_scan(b_rc.as<float4>(), b_rc.as<float4>() + 1, 2, order, N,
                                           cnt + C_M, tp, b_offs.as<uint32_t>(),
                                           b_bstart.as<uint32_t>(), (uint32_t)(L.eparts + 1),
                                           L.lb_rect, cnt + C_RECT_TICKET, cnt + C_PPRE,
@@ -607,7 +605,7 @@ struct gs_ctx {
         HIPCHK(gs::launch_fill_u32(L.fr, 0u, L.fwords, st));
         if (timing) HIPCHK(gs::launch_fill_u32(b_evals.as<uint32_t>(), 0u, 64 * 8 * 2, st));
         gs::ProjParams p = proj_params(v);
-        gs::Compact c{b_rect.as<float4>(), b_covc.as<float4>(), b_dkey.as<uint32_t>(),
+        gs::Compact c{b_rc.as<float4>(), b_dkey.as<uint32_t>(),
                       b_brec.as<float4>(), nullptr};
         HIPCHK(gs::launch_project(sd, p, c, nullptr, L.lb_proj, L.cnt + C_PROJ_TICKET,
                                   L.cnt + C_M, b_phist_proj.as<uint32_t>(), st));
@@ -786,7 +784,7 @@ struct gs_ctx {
         if (timing) HIPCHK(hipEventRecord(tev[0], st));
         HIPCHK(gs::launch_fill_u32(L.fr, 0u, L.fwords, st));
         HIPCHK(gs::launch_fill_u32(t_loss.as<uint32_t>(), 0u, 4, st));
-        gs::Compact cpt{b_rect.as<float4>(), b_covc.as<float4>(), b_dkey.as<uint32_t>(),
+        gs::Compact cpt{b_rc.as<float4>(), b_dkey.as<uint32_t>(),
                         nullptr, b_src.as<uint32_t>()};
         HIPCHK(gs::launch_train_project(tplanes(t_p), tr.cam, cpt, b_brec.as<float4>(),
                                         t_cidx.as<uint32_t>(), t_vis.as<uint8_t>(), L.lb_proj,
@@ -1027,29 +1025,28 @@ int gs_project(gs_ctx* ctx, const gs_scene* scene, const gs_view* view, uint8_t*
         *m_out = M;
         if (valid_mask && n > 0)
             HIPCHK(hipMemcpyAsync(valid_mask, ctx->b_valid.p, (size_t)n, hipMemcpyDeviceToHost, ctx->st));
-        std::vector<float> rect((size_t)M * 4), cov((size_t)M * 4), brec((size_t)M * 12);
+        std::vector<float> rc((size_t)M * 8), brec((size_t)M * 12);
         std::vector<uint32_t> dk((size_t)M);
         if (M > 0) {
-            HIPCHK(hipMemcpyAsync(rect.data(), ctx->b_rect.p, (size_t)M * 16, hipMemcpyDeviceToHost, ctx->st));
-            HIPCHK(hipMemcpyAsync(cov.data(), ctx->b_covc.p, (size_t)M * 16, hipMemcpyDeviceToHost, ctx->st));
+            HIPCHK(hipMemcpyAsync(rc.data(), ctx->b_rc.p, (size_t)M * 32, hipMemcpyDeviceToHost, ctx->st));
             HIPCHK(hipMemcpyAsync(brec.data(), ctx->b_brec.p, (size_t)M * 48, hipMemcpyDeviceToHost, ctx->st));
             HIPCHK(hipMemcpyAsync(dk.data(), ctx->b_dkey.p, (size_t)M * 4, hipMemcpyDeviceToHost, ctx->st));
         }
         ctx->sync();
         for (int64_t m = 0; m < M; ++m) {
             if (means2d) {
-                means2d[m * 2 + 0] = rect[m * 4 + 0];
-                means2d[m * 2 + 1] = rect[m * 4 + 1];
+                means2d[m * 2 + 0] = rc[m * 8 + 0];
+                means2d[m * 2 + 1] = rc[m * 8 + 1];
             }
             if (radii) {
-                radii[m * 2 + 0] = rect[m * 4 + 2];
-                radii[m * 2 + 1] = rect[m * 4 + 3];
+                radii[m * 2 + 0] = rc[m * 8 + 2];
+                radii[m * 2 + 1] = rc[m * 8 + 3];
             }
             if (covs2d) {
-                covs2d[m * 4 + 0] = cov[m * 4 + 0];
-                covs2d[m * 4 + 1] = cov[m * 4 + 1];
-                covs2d[m * 4 + 2] = cov[m * 4 + 1];
-                covs2d[m * 4 + 3] = cov[m * 4 + 2];
+                covs2d[m * 4 + 0] = rc[m * 8 + 4];
+                covs2d[m * 4 + 1] = rc[m * 8 + 5];
+                covs2d[m * 4 + 2] = rc[m * 8 + 5];
+                covs2d[m * 4 + 3] = rc[m * 8 + 6];
             }
             if (depths) std::memcpy(&depths[m], &dk[m], 4);
             if (opac_out) opac_out[m] = brec[m * 12 + 8];

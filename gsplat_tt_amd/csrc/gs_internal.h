@@ -43,8 +43,9 @@ struct ProjParams {
 
 // Compact (visible-only) Gaussian records, index m in [0, M).
 struct Compact {
-    float4* rect;      // px, py, rx, ry
-    float4* cov;       // a, b, c, m2thr
+    // 2 x float4 per Gaussian, adjacent so that one 32-byte read gathers both
+    // in rank order: (px, py, rx, ry) (a, b, c, m2thr)
+    float4* rc;
     uint32_t* dkey;    // fp32 depth bits
     float4* brec;      // 3 x float4 per Gaussian: (mx,my,xh,yh) (ci_a,ci_b,ci_c,lt) (op,r,g,b)
     uint32_t* src;     // source index (optional)
@@ -106,8 +107,8 @@ struct TileParams {
 // capacity) and partitions beyond it exit at once.
 // rect_r / cov_r (optional): rect[order[r]] / cov[order[r]] gathered into
 // rank order (cov_r only with the cull on), the inputs of launch_pair_emit.
-hipError_t launch_rect_count_scan(const float4* rect, const float4* cov, const uint32_t* order,
-                                  int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
+hipError_t launch_rect_count_scan(const float4* rect, const float4* cov, int stride,
+                                  const uint32_t* order, int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
                                   uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
                                   uint32_t* ticket, uint32_t* total_out, float4* rect_r,
                                   float4* cov_r, hipStream_t st);

@@ -239,8 +239,8 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
         const int64_t i = base + it * kProjThreads + tid;
         const uint64_t m = excl + my_off[it] + (uint64_t)__popcll(bal[it] & lt_mask);
         const float a = va[it], b = vb[it], c = vc[it];
-        out.rect[m] = make_float4(vmx[it], vmy[it], vrx[it], vry[it]);
-        out.cov[m] = make_float4(a, b, c, s.m2thr[i]);
+        out.rc[2 * m + 0] = make_float4(vmx[it], vmy[it], vrx[it], vry[it]);
+        out.rc[2 * m + 1] = make_float4(a, b, c, s.m2thr[i]);
         out.dkey[m] = __float_as_uint(vtz[it]);
         // Microblock cull / blend record (cull_and_blend.cpp:723-777).
         const float det = fmax_std(a * c - b * b, 1e-6f);

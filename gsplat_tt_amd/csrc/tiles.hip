@@ -97,6 +97,7 @@ __device__ __forceinline__ bool pair_keep(float px, float py, float4 cv, int til
 // given, the rectangles and conics are also gathered into rank order.
 __global__ __launch_bounds__(kThreads) void k_rect_count_scan(const float4* __restrict__ rect,
                                                               const float4* __restrict__ cov,
+                                                              int stride,
                                                               const uint32_t* __restrict__ order,
                                                               int64_t m_cap,
                                                               const uint32_t* __restrict__ m_dev,
@@ -121,19 +122,38 @@ __global__ __launch_bounds__(kThreads) void k_rect_count_scan(const float4* __re
     const uint32_t nparts = (uint32_t)((m + kCountPart - 1) / kCountPart);
     if (vid >= nparts) return;  // no later partition has work either
     const int64_t base = (int64_t)vid * kCountPart;
+    // loads in stages (all ranks' ids, then all records) so that the four
+    // gathers of a thread are in flight together
+    const bool gather = rect_r != nullptr;
+    const bool want_cov = gather && tp.cull;
+    // (indices past m are clamped to m - 1: unconditional loads, no branches
+    // whose joins would wait for each load in turn)
+    uint32_t gid[kCountItems];
+    float4 rr[kCountItems], cv[kCountItems];
+#pragma unroll
+    for (int it = 0; it < kCountItems; ++it)
+        gid[it] = (uint32_t)min(base + it * kThreads + tid, m - 1);
+    if (order != nullptr) {
+#pragma unroll
+        for (int it = 0; it < kCountItems; ++it) gid[it] = order[gid[it]];
+    }
+#pragma unroll
+    for (int it = 0; it < kCountItems; ++it) rr[it] = rect[(int64_t)gid[it] * stride];
+    if (want_cov) {
+#pragma unroll
+        for (int it = 0; it < kCountItems; ++it) cv[it] = cov[(int64_t)gid[it] * stride];
+    }
     uint32_t incl[kCountItems], cnt[kCountItems];
 #pragma unroll
     for (int it = 0; it < kCountItems; ++it) {
         const int64_t r = base + it * kThreads + tid;
         uint32_t c = 0;
         if (r < m) {
-            const uint32_t g = order ? order[r] : (uint32_t)r;
-            const float4 rr = rect[g];
-            const Rect q = tile_rect(rr, tp);
+            const Rect q = tile_rect(rr[it], tp);
             c = (uint32_t)((q.x1 - q.x0 + 1) * (q.y1 - q.y0 + 1));
-            if (rect_r != nullptr) {
-                rect_r[r] = rr;
-                if (tp.cull) cov_r[r] = cov[g];
+            if (gather) {
+                rect_r[r] = rr[it];
+                if (want_cov) cov_r[r] = cv[it];
             }
         }
         cnt[it] = c;
@@ -482,14 +502,14 @@ hipError_t launch_tile_ranges64(const uint64_t* keys, uint32_t p, uint32_t* rang
 size_t rect_scan_partitions(int64_t m) { return (size_t)((m + kCountPart - 1) / kCountPart); }
 size_t emit_partitions(uint64_t p_pre) { return (size_t)((p_pre + kEmitPart - 1) / kEmitPart); }
 
-hipError_t launch_rect_count_scan(const float4* rect, const float4* cov, const uint32_t* order,
-                                  int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
+hipError_t launch_rect_count_scan(const float4* rect, const float4* cov, int stride,
+                                  const uint32_t* order, int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
                                   uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
                                   uint32_t* ticket, uint32_t* total_out, float4* rect_r,
                                   float4* cov_r, hipStream_t st) {
     if (m <= 0) return hipSuccess;
     const unsigned grid = (unsigned)rect_scan_partitions(m);
-    k_rect_count_scan<<<grid, kThreads, 0, st>>>(rect, cov, order, m, m_dev, tp, offs, bstart,
+    k_rect_count_scan<<<grid, kThreads, 0, st>>>(rect, cov, stride, order, m, m_dev, tp, offs, bstart,
                                                  bstart_cap, lb_state, ticket, total_out, rect_r,
                                                  cov_r);
     return hipGetLastError();

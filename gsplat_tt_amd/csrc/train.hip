@@ -296,8 +296,8 @@ __global__ __launch_bounds__(kTThreads) void k_train_project(
         if (!keep[it]) continue;
         const int64_t i = base + it * kTThreads + tid;
         const uint64_t m = excl + my_off[it] + (uint64_t)__popcll(bal[it] & ltm);
-        out.rect[m] = rect[it];
-        out.cov[m] = cov[it];
+        out.rc[2 * m + 0] = rect[it];
+        out.rc[2 * m + 1] = cov[it];
         out.dkey[m] = __float_as_uint(depth[it]);
         trec[3 * m + 0] = r0[it];
         trec[3 * m + 1] = r1[it];
