@@ -388,10 +388,29 @@ __global__ __launch_bounds__(256) void k_train_fwd(const float4* __restrict__ tr
     }
 }
 
+// Sum over the 64 lanes of a wave (all lanes active), result valid in every
+// lane: DPP moves inside each row of 16 lanes (quad swaps, half-row and row
+// mirrors), then the four row sums read out of lanes 0, 16, 32, 48.
+__device__ __forceinline__ float dpp_add(float v, int ctrl_sel) {
+    int x = __float_as_int(v);
+    switch (ctrl_sel) {
+        case 0: x = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false); break;   // quad_perm 1,0,3,2
+        case 1: x = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false); break;   // quad_perm 2,3,0,1
+        case 2: x = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+        default: x = __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false); break; // row_mirror
+    }
+    return v + __int_as_float(x);
+}
 __device__ __forceinline__ float wave_fsum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, GS_WAVE);
-    return v;
+    v = dpp_add(v, 0);
+    v = dpp_add(v, 1);
+    v = dpp_add(v, 2);
+    v = dpp_add(v, 3);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
 constexpr int kBwdBatch = 128;
