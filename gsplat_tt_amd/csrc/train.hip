@@ -388,29 +388,23 @@ __global__ __launch_bounds__(256) void k_train_fwd(const float4* __restrict__ tr
     }
 }
 
-// Sum over the 64 lanes of a wave (all lanes active), result valid in every
-// lane: DPP moves inside each row of 16 lanes (quad swaps, half-row and row
-// mirrors), then the four row sums read out of lanes 0, 16, 32, 48.
-__device__ __forceinline__ float dpp_add(float v, int ctrl_sel) {
-    int x = __float_as_int(v);
-    switch (ctrl_sel) {
-        case 0: x = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false); break;   // quad_perm 1,0,3,2
-        case 1: x = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false); break;   // quad_perm 2,3,0,1
-        case 2: x = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false); break;  // row_half_mirror
-        default: x = __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false); break; // row_mirror
-    }
+// Sum over the 64 lanes of a wave (all lanes active), result in lane 63: DPP
+// moves inside each row of 16 lanes (quad swaps, half-row and row mirrors
+// leave every lane with its row's sum), then row broadcasts fold row 0 into
+// row 1, row 2 into row 3, and row 1 into row 3.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int x = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false);
     return v + __int_as_float(x);
 }
-__device__ __forceinline__ float wave_fsum(float v) {
-    v = dpp_add(v, 0);
-    v = dpp_add(v, 1);
-    v = dpp_add(v, 2);
-    v = dpp_add(v, 3);
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return (r0 + r1) + (r2 + r3);
+__device__ __forceinline__ float wave_fsum_last(float v) {
+    v = dpp_add<0xB1, 0xF>(v);   // quad_perm 1,0,3,2
+    v = dpp_add<0x4E, 0xF>(v);   // quad_perm 2,3,0,1
+    v = dpp_add<0x141, 0xF>(v);  // row_half_mirror
+    v = dpp_add<0x140, 0xF>(v);  // row_mirror
+    v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
 }
 
 constexpr int kBwdBatch = 128;
@@ -507,8 +501,8 @@ __global__ __launch_bounds__(256) void k_train_bwd(const float4* __restrict__ tr
             const uint64_t any = __ballot(live);
             if (any) {
 #pragma unroll
-                for (int k = 0; k < 9; ++k) v[k] = wave_fsum(v[k]);
-                if (lane == 0) {
+                for (int k = 0; k < 9; ++k) v[k] = wave_fsum_last(v[k]);
+                if (lane == GS_WAVE - 1) {
 #pragma unroll
                     for (int k = 0; k < 9; ++k) s_part[w][j][k] = v[k];
                 }
