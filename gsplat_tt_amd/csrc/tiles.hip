@@ -431,37 +431,56 @@ __global__ __launch_bounds__(256) void k_tile_bounds(const uint32_t* __restrict_
     }
 }
 
-// out[c] += sum of rows [y*kRedRows, ...) of part (rows x cols, cols % 4 == 0),
-// rows bounded by ceil(min(*count_dev, count_cap) / per_row) when count_dev is
-// given. One thread per 4 columns, 16-byte loads, 8 rows in flight.
-constexpr int kRedRows = 32;
-__global__ void k_reduce_rows(const uint32_t* __restrict__ part, int cols, uint32_t rows_cap,
-                              const uint32_t* __restrict__ count_dev, uint32_t count_cap,
-                              uint32_t per_row, uint32_t* __restrict__ out) {
+// out[c] += column sums of part (rows x cols, cols / 4 dividing 1024), rows
+// bounded by ceil(min(*count_dev, count_cap) / per_row) when count_dev is
+// given. A 1024-thread workgroup takes `span` rows: cols / 4 column quads x
+// (4096 / cols) row lanes, 16-byte loads with 8 rows in flight per lane; the
+// row lanes are summed in LDS and each workgroup adds its column sums with one
+// atomic per column (few workgroups, so little contention on the atomics).
+constexpr int kRedThreads = 1024;
+constexpr uint32_t kRedBlocks = 96;  // workgroups for the largest row count
+__global__ __launch_bounds__(kRedThreads) void k_reduce_rows(
+    const uint32_t* __restrict__ part, int cols, uint32_t rows_cap, uint32_t span,
+    const uint32_t* __restrict__ count_dev, uint32_t count_cap, uint32_t per_row,
+    uint32_t* __restrict__ out) {
+    __shared__ uint4 s_acc[kRedThreads];
     uint32_t rows = rows_cap;
     if (count_dev) {
         const uint32_t c = min(*count_dev, count_cap);
         rows = min(rows_cap, (uint32_t)(((uint64_t)c + per_row - 1) / per_row));
     }
-    const int c4 = blockIdx.x * blockDim.x + threadIdx.x;  // column quad
-    const uint32_t r0 = blockIdx.y * (uint32_t)kRedRows;
-    if (c4 * 4 >= cols || r0 >= rows) return;
-    const uint32_t r1 = min(rows, r0 + (uint32_t)kRedRows);
-    const uint4* p = reinterpret_cast<const uint4*>(part) + (size_t)r0 * (cols / 4) + c4;
+    const uint32_t r0 = blockIdx.x * span;
+    if (r0 >= rows) return;  // uniform over the workgroup
+    const int quads = cols / 4;
+    const int lanes = kRedThreads / quads;  // row lanes
+    const int q = threadIdx.x % quads, rl = threadIdx.x / quads;
+    const uint32_t r1 = min(rows, r0 + span);
+    const uint4* p = reinterpret_cast<const uint4*>(part) + (size_t)r0 * quads + q;
     uint4 acc = make_uint4(0, 0, 0, 0);
 #pragma unroll 8
-    for (uint32_t r = r0; r < r1; ++r, p += cols / 4) {
-        const uint4 v = *p;
+    for (uint32_t r = r0 + rl; r < r1; r += lanes) {
+        const uint4 v = p[(size_t)(r - r0) * quads];
         acc.x += v.x;
         acc.y += v.y;
         acc.z += v.z;
         acc.w += v.w;
     }
-    uint32_t* o = out + c4 * 4;
-    if (acc.x) atomicAdd(o + 0, acc.x);
-    if (acc.y) atomicAdd(o + 1, acc.y);
-    if (acc.z) atomicAdd(o + 2, acc.z);
-    if (acc.w) atomicAdd(o + 3, acc.w);
+    s_acc[threadIdx.x] = acc;
+    __syncthreads();
+    if (rl == 0) {
+        for (int l = 1; l < lanes; ++l) {
+            const uint4 v = s_acc[l * quads + q];
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+        }
+        uint32_t* o = out + q * 4;
+        if (acc.x) atomicAdd(o + 0, acc.x);
+        if (acc.y) atomicAdd(o + 1, acc.y);
+        if (acc.z) atomicAdd(o + 2, acc.z);
+        if (acc.w) atomicAdd(o + 3, acc.w);
+    }
 }
 
 // key = (tile << 32) | fp32 depth bits of the pair's Gaussian (sort.cpp:180-205).
@@ -550,12 +569,11 @@ hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,
                               const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
                               uint32_t* out, hipStream_t st) {
     if (rows_cap == 0) return hipSuccess;
-    if (cols % 4 != 0) return hipErrorInvalidValue;
-    const int quads = cols / 4;
-    const int block = std::min(quads, 256);
-    dim3 grid((quads + block - 1) / block, (rows_cap + kRedRows - 1) / kRedRows);
-    k_reduce_rows<<<grid, block, 0, st>>>(part, cols, rows_cap, count_dev, count_cap, per_row,
-                                          out);
+    if (cols <= 0 || cols % 4 != 0 || kRedThreads % (cols / 4) != 0) return hipErrorInvalidValue;
+    const uint32_t span = std::max<uint32_t>(32, (rows_cap + kRedBlocks - 1) / kRedBlocks);
+    const unsigned grid = (rows_cap + span - 1) / span;
+    k_reduce_rows<<<grid, kRedThreads, 0, st>>>(part, cols, rows_cap, span, count_dev,
+                                                count_cap, per_row, out);
     return hipGetLastError();
 }
 
