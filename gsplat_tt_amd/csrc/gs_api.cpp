@@ -426,7 +426,7 @@ struct gs_ctx {
                                     b_bstart.as<uint32_t>(), m, nullptr, p_pre, nullptr, tp,
                                     b_pair_tile.as<uint32_t>(), b_pair_id.as<uint32_t>(), p_pre,
                                     b_lb.as<uint64_t>(), b_cnt.as<uint32_t>() + 10,
-                                    b_cnt.as<uint32_t>() + 11, nullptr, st));
+                                    b_cnt.as<uint32_t>() + 11, nullptr, true, st));
         HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
         sync();
         return h_pin[11];
@@ -579,18 +579,19 @@ struct gs_ctx {
                                     L.pcap, cnt + C_PPRE, tp, b_pair_tile.as<uint32_t>(),
                                     b_pair_id.as<uint32_t>(), L.pcap, L.lb_emit,
                                     cnt + C_EMIT_TICKET, cnt + C_P, b_phist_emit.as<uint32_t>(),
-                                    st));
+                                    false, st));
         HIPCHK(gs::launch_reduce_rows(b_phist_emit.as<uint32_t>(), 512, (uint32_t)L.eparts,
                                       cnt + C_PPRE, L.pcap, gs::kEmitPartition, fr + kFrTileHist,
                                       st));
         record(3);
-        // stable tile sort of the depth-ordered pairs
+        // stable tile sort of the depth-ordered candidate slots; its first pass
+        // drops the culled ones (kPairDrop), so the kept pairs come out compact
         void* tiles_sorted = nullptr;
         uint32_t* ids_sorted = nullptr;
         HIPCHK(gs::radix_sort_pairs_dev(b_pair_tile.p, b_pair_id.as<uint32_t>(), L.pcap,
-                                        cnt + C_P, 4, 0, tile_bits(T), fr + kFrTileHist,
+                                        cnt + C_PPRE, 4, 0, tile_bits(T), fr + kFrTileHist,
                                         cnt + C_TSORT_TICKETS, sort, st, false, &tiles_sorted,
-                                        &ids_sorted));
+                                        &ids_sorted, cnt + C_P));
         HIPCHK(gs::launch_tile_bounds(static_cast<uint32_t*>(tiles_sorted), L.pcap, cnt + C_P,
                                       b_ranges.as<uint32_t>(), T, st));
         return ids_sorted;

@@ -90,10 +90,15 @@ hipError_t radix_sort_pairs(void* keys, uint32_t* vals, int64_t n, int key_bytes
 // (n_dev may be null), `hist` holds the [pass][256] digit histograms of the
 // keys (built by their producer), `tickets` one zeroed word per pass. Every
 // pass runs; the result buffer follows from the pass count alone.
+// n_kept_dev (u32 keys only, optional): the first pass drops every key equal
+// to kPairDrop (its value is not read) and stably compacts the rest; later
+// passes sort min(n_cap, *n_kept_dev) keys, and `hist` counts kept keys only.
+constexpr uint32_t kPairDrop = 0xFFFFFFFFu;
 hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const uint32_t* n_dev,
                                 int key_bytes, int begin_bit, int end_bit, const uint32_t* hist,
                                 uint32_t* tickets, SortTemp& tmp, hipStream_t st, bool vals_iota,
-                                void** keys_final, uint32_t** vals_final);
+                                void** keys_final, uint32_t** vals_final,
+                                const uint32_t* n_kept_dev = nullptr);
 
 // ---- tiles.hip
 struct TileParams {
@@ -107,8 +112,10 @@ struct TileParams {
 // capacity) and partitions beyond it exit at once.
 // rect_r / cov_r (optional): rect[order[r]] / cov[order[r]] gathered into
 // rank order (cov_r only with the cull on), the inputs of launch_pair_emit.
+// stride: element stride of rect / cov in float4 (2 for interleaved records).
 hipError_t launch_rect_count_scan(const float4* rect, const float4* cov, int stride,
-                                  const uint32_t* order, int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
+                                  const uint32_t* order, int64_t m, const uint32_t* m_dev,
+                                  TileParams tp, uint32_t* offs,
                                   uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
                                   uint32_t* ticket, uint32_t* total_out, float4* rect_r,
                                   float4* cov_r, hipStream_t st);
@@ -121,7 +128,7 @@ hipError_t launch_pair_emit(const float4* rect_r, const float4* cov_r, const uin
                             const uint32_t* m_dev, uint32_t p_pre, const uint32_t* p_pre_dev,
                             TileParams tp, uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
                             uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
-                            uint32_t* part_hist, hipStream_t st);
+                            uint32_t* part_hist, bool compact, hipStream_t st);
 hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, const uint32_t* p_dev,
                               uint32_t* ranges, int64_t num_tiles, hipStream_t st);
 // Same ranges by per-tile binary search over the sorted tile keys (reads

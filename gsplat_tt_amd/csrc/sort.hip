@@ -126,7 +126,9 @@ __global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ key
     }
 }
 
-template <typename K, bool IOTA, int THREADS, int ITEMS, bool D32>
+// DROP: keys equal to kPairDrop are left out (not ranked, not written): the
+// pass stably compacts the kept keys while it sorts them.
+template <typename K, bool IOTA, int THREADS, int ITEMS, bool D32, bool DROP>
 __global__ __launch_bounds__(THREADS) void k_onesweep(
     const K* __restrict__ kin, const uint32_t* __restrict__ vin, K* __restrict__ kout,
     uint32_t* __restrict__ vout, int64_t n_cap, const uint32_t* __restrict__ n_dev, int shift,
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     constexpr int WAVES = THREADS / GS_WAVE;
     constexpr int PART = THREADS * ITEMS;
     static_assert(THREADS >= 256, "one thread per digit");
-    __shared__ uint32_t s_vid;
+    __shared__ uint32_t s_vid, s_count;
     __shared__ uint32_t s_wcnt[WAVES][256];
     __shared__ uint32_t s_loff[256];
     __shared__ uint32_t s_gpos[256];
@@ -182,7 +184,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     for (int it = 0; it < ITEMS; ++it) {
         const int64_t idx = wave_base + it * GS_WAVE + lane;
         rank[it] = 0;
-        if (idx < n) {
+        if (idx < n && !(DROP && key[it] == (K)kPairDrop)) {
             const uint32_t d = digit_of(key[it], shift, mask);
             uint64_t peers = __ballot(1);
             for (int b = 0; b < bits; ++b) {
@@ -268,6 +270,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         }
         const uint32_t loff = p1 + i1 - v1;
         s_loff[tid] = loff;
+        if (tid == 255) s_count = p1 + i1;  // keys of this partition (kept ones)
         s_gpos[tid] = (p2 + i2 - v2) + excl - loff;
     }
     __syncthreads();
@@ -275,7 +278,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
         const int64_t idx = wave_base + it * GS_WAVE + lane;
-        if (idx < n) {
+        if (idx < n && !(DROP && key[it] == (K)kPairDrop)) {
             const uint32_t d = digit_of(key[it], shift, mask);
             const uint32_t lp = s_loff[d] + s_wcnt[w][d] + rank[it];
             if (lp < (uint32_t)PART) {
@@ -286,7 +289,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     }
     __syncthreads();
     const int64_t cnt64 = n - part_base;
-    const int count = cnt64 < PART ? (int)cnt64 : PART;
+    const int count = DROP ? (int)min(s_count, (uint32_t)PART) : (cnt64 < PART ? (int)cnt64 : PART);
     for (int j = tid; j < count; j += THREADS) {
         const K k = s_keys[j];
         const uint32_t d = digit_of(k, shift, mask);
@@ -330,7 +333,7 @@ template <typename K>
 hipError_t launch_pass(bool iota, const K* kin, const uint32_t* vin, K* kout, uint32_t* vout,
                        int64_t n_cap, const uint32_t* n_dev, int shift, int bits,
                        const uint32_t* hist_pass, SortTemp& tmp, uint32_t* ticket,
-                       hipStream_t st) {
+                       hipStream_t st, bool drop = false) {
     constexpr int T = SweepCfg<K>::T, I = SweepCfg<K>::I;
     const unsigned grid = (unsigned)((n_cap + T * I - 1) / (T * I));
     const bool d32 = n_cap < ((int64_t)1 << 30);
@@ -339,9 +342,20 @@ hipError_t launch_pass(bool iota, const K* kin, const uint32_t* vin, K* kout, ui
         reinterpret_cast<uint32_t*>(tmp.state), 0u, words);
     const uint32_t epoch = ++tmp.epoch;
 #define GS_OS(IO, DD)                                                                        \
-    k_onesweep<K, IO, T, I, DD><<<grid, T, 0, st>>>(kin, vin, kout, vout, n_cap, n_dev, shift, \
-                                                    bits, hist_pass, tmp.state, ticket, epoch)
-    if (iota) {
+    k_onesweep<K, IO, T, I, DD, false><<<grid, T, 0, st>>>(kin, vin, kout, vout, n_cap, n_dev, \
+                                                           shift, bits, hist_pass, tmp.state,  \
+                                                           ticket, epoch)
+    if (drop) {
+        if (iota || sizeof(K) != 4) return hipErrorInvalidValue;
+        if (d32)
+            k_onesweep<K, false, T, I, true, true><<<grid, T, 0, st>>>(
+                kin, vin, kout, vout, n_cap, n_dev, shift, bits, hist_pass, tmp.state, ticket,
+                epoch);
+        else
+            k_onesweep<K, false, T, I, false, true><<<grid, T, 0, st>>>(
+                kin, vin, kout, vout, n_cap, n_dev, shift, bits, hist_pass, tmp.state, ticket,
+                epoch);
+    } else if (iota) {
         if (d32) GS_OS(true, true); else GS_OS(true, false);
     } else {
         if (d32) GS_OS(false, true); else GS_OS(false, false);
@@ -415,7 +429,7 @@ template <typename K>
 hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t* n_dev,
                          int begin_bit, int end_bit, const uint32_t* hist, uint32_t* tickets,
                          SortTemp& tmp, hipStream_t st, bool vals_iota, K** keys_final,
-                         uint32_t** vals_final) {
+                         uint32_t** vals_final, const uint32_t* n_kept_dev) {
     *keys_final = keys;
     *vals_final = vals;
     if (n_cap <= 0) return hipSuccess;
@@ -429,8 +443,10 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
     for (int p = 0; p < npass; ++p) {
         const int shift = begin_bit + 8 * p;
         const int bits = std::min(8, end_bit - shift);
-        hipError_t e = launch_pass<K>(p == 0 && vals_iota, kin, vin, kalt, valt, n_cap, n_dev,
-                                      shift, bits, hist + p * 256, tmp, tickets + p, st);
+        const bool drop = p == 0 && n_kept_dev != nullptr;
+        const uint32_t* cnt = (p > 0 && n_kept_dev != nullptr) ? n_kept_dev : n_dev;
+        hipError_t e = launch_pass<K>(p == 0 && vals_iota, kin, vin, kalt, valt, n_cap, cnt,
+                                      shift, bits, hist + p * 256, tmp, tickets + p, st, drop);
         if (e != hipSuccess) return e;
         std::swap(kin, kalt);
         std::swap(vin, valt);
@@ -445,20 +461,22 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
 hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const uint32_t* n_dev,
                                 int key_bytes, int begin_bit, int end_bit, const uint32_t* hist,
                                 uint32_t* tickets, SortTemp& tmp, hipStream_t st, bool vals_iota,
-                                void** keys_final, uint32_t** vals_final) {
+                                void** keys_final, uint32_t** vals_final,
+                                const uint32_t* n_kept_dev) {
     if (key_bytes == 4) {
         uint32_t* kf = nullptr;
         hipError_t e = sort_dev_impl<uint32_t>(static_cast<uint32_t*>(keys), vals, n_cap, n_dev,
                                                begin_bit, end_bit, hist, tickets, tmp, st,
-                                               vals_iota, &kf, vals_final);
+                                               vals_iota, &kf, vals_final, n_kept_dev);
         *keys_final = kf;
         return e;
     }
     if (key_bytes == 8) {
+        if (n_kept_dev != nullptr) return hipErrorInvalidValue;
         uint64_t* kf = nullptr;
         hipError_t e = sort_dev_impl<uint64_t>(static_cast<uint64_t*>(keys), vals, n_cap, n_dev,
                                                begin_bit, end_bit, hist, tickets, tmp, st,
-                                               vals_iota, &kf, vals_final);
+                                               vals_iota, &kf, vals_final, nullptr);
         *keys_final = kf;
         return e;
     }

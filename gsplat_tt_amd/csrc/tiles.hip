@@ -199,6 +199,12 @@ __global__ __launch_bounds__(kThreads) void k_rect_count_scan(const float4* __re
 // cull, stable compaction of kept pairs in candidate order. The ranks of a
 // partition are [bstart[vid], bstart[vid+1]]; each candidate finds its rank by
 // an inclusive max-scan over rank heads in LDS.
+// COMPACT: kept pairs are compacted (ticket-ordered partitions, look-back).
+// Otherwise every candidate slot c < cap is written, the tile id of a kept
+// pair or kPairDrop for a culled one (the pair id only for kept ones), and the
+// kept count is added to *total_out: the tile sort's first pass drops the
+// culled slots, so no partition waits on another here.
+template <bool COMPACT>
 __global__ __launch_bounds__(kThreads) void k_pair_emit(
     const float4* __restrict__ rect_r, const float4* __restrict__ cov_r,
     const uint32_t* __restrict__ order, const uint32_t* __restrict__ offs,
@@ -222,14 +228,14 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     __shared__ uint32_t s_th[2][256];
     __shared__ uint64_t s_excl;
     const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
-    if (tid == 0) s_vid = atomicAdd(ticket, 1u);
+    if (COMPACT && tid == 0) s_vid = atomicAdd(ticket, 1u);
     for (int i = tid; i < kEmitPart; i += kThreads) s_own[i] = 0;
     if (part_hist != nullptr) {
         s_th[0][tid] = 0;
         s_th[1][tid] = 0;
     }
     __syncthreads();
-    const uint32_t vid = s_vid;
+    const uint32_t vid = COMPACT ? s_vid : blockIdx.x;
     const int64_t m = m_dev ? min(m_cap, (int64_t)*m_dev) : m_cap;
     const uint32_t p_pre = p_pre_dev ? min(p_pre_cap, *p_pre_dev) : p_pre_cap;
     const uint32_t nparts = (uint32_t)(((uint64_t)p_pre + kEmitPart - 1) / kEmitPart);
@@ -307,7 +313,9 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
         ty[it] = (int)((xy[it] >> 16) + row);
         tx[it] = (int)((xy[it] & 0xFFFFu) + col);
         tile[it] = (uint32_t)(ty[it] * tp.tiles_x + tx[it]);
-        keep[it] = c < c1;
+        // without compaction a slot past the capacity is not written, so it
+        // must not be counted either (the frame is re-run with more room)
+        keep[it] = c < c1 && (COMPACT || c < cap);
     }
     if (tp.cull) {
         if (nr <= kRankCache) {
@@ -349,6 +357,25 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     if (part_hist != nullptr) {
         part_hist[(size_t)vid * 512 + tid] = s_th[0][tid];
         part_hist[(size_t)vid * 512 + 256 + tid] = s_th[1][tid];
+    }
+    if (!COMPACT) {
+#pragma unroll
+        for (int it = 0; it < kEmitItems; ++it) {
+            const uint64_t c = c0 + it * kThreads + tid;
+            if (c < c1 && c < cap) {
+                pair_tile[c] = keep[it] ? tile[it] : kPairDrop;
+                if (keep[it]) pair_id[c] = gid[it];
+            }
+        }
+        if (tid == 0) {
+            uint32_t kept = 0;
+#pragma unroll
+            for (int it = 0; it < kEmitItems; ++it)
+#pragma unroll
+                for (int ww = 0; ww < kWaves; ++ww) kept += s_cnt[it][ww];
+            if (kept) atomicAdd(total_out, kept);
+        }
+        return;
     }
     uint32_t total = 0, my_off[kEmitItems];
 #pragma unroll
@@ -539,12 +566,18 @@ hipError_t launch_pair_emit(const float4* rect_r, const float4* cov_r, const uin
                             const uint32_t* m_dev, uint32_t p_pre, const uint32_t* p_pre_dev,
                             TileParams tp, uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
                             uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
-                            uint32_t* part_hist, hipStream_t st) {
+                            uint32_t* part_hist, bool compact, hipStream_t st) {
     if (p_pre == 0 || m <= 0) return hipSuccess;
     const unsigned grid = (unsigned)emit_partitions(p_pre);
-    k_pair_emit<<<grid, kThreads, 0, st>>>(rect_r, cov_r, order, offs, bstart, m, m_dev, p_pre,
-                                           p_pre_dev, tp, pair_tile, pair_id, cap, lb_state,
-                                           ticket, total_out, part_hist);
+    if (compact)
+        k_pair_emit<true><<<grid, kThreads, 0, st>>>(rect_r, cov_r, order, offs, bstart, m, m_dev,
+                                                     p_pre, p_pre_dev, tp, pair_tile, pair_id,
+                                                     cap, lb_state, ticket, total_out, part_hist);
+    else
+        k_pair_emit<false><<<grid, kThreads, 0, st>>>(rect_r, cov_r, order, offs, bstart, m,
+                                                      m_dev, p_pre, p_pre_dev, tp, pair_tile,
+                                                      pair_id, cap, lb_state, ticket, total_out,
+                                                      part_hist);
     return hipGetLastError();
 }
 

@@ -139,6 +139,39 @@ def test_render_frame(gpu_ctx, ts, H, W):
     assert p >= 55.0
 
 
+def test_render_pair_capacity_retry():
+    """A fresh context starts with room for max(2^20, 4N) candidate pairs; 4200
+    large Gaussians make 1.3M pairs, so the first frame overflows, is detected
+    after the fact and re-run with a larger capacity. Both that frame and the
+    next (no overflow) must equal the oracle's."""
+    rng = np.random.default_rng(31)
+    n = 4200
+    means = np.stack([rng.uniform(-1.5, 1.5, n), rng.uniform(-1.1, 1.1, n),
+                      rng.uniform(3.0, 6.0, n)], 1).astype(np.float32)
+    scales = np.exp(rng.normal(np.log(0.4), 0.25, (n, 3))).astype(np.float32)
+    q = rng.standard_normal((n, 4))
+    quats = (q / np.linalg.norm(q, axis=1, keepdims=True)).astype(np.float32)
+    opac = rng.uniform(0.05, 0.35, n).astype(np.float32)
+    rgb = rng.uniform(0, 1, (n, 3)).astype(np.float32)
+    cov = O.cov3d(scales, quats)
+    K = scenes.intrinsics(500, 500, 320, 240)
+    w2c = np.eye(4, dtype=np.float32)
+    img_o, st_o, _ = O.render_full(means, cov, opac, rgb, w2c, K, 480, 640, tile_size=16)
+    ctx = L.Context(0)
+    try:
+        ctx.set_scene(means, cov, opac, rgb)
+        view = L.make_view(w2c, K, 480, 640, tile_size=16, output="f32")
+        for frame in range(2):
+            img, st = ctx.render(view)
+            print("capacity frame", frame, st["num_entries"], st["pairs_pre"])
+            assert st["pairs_pre"] > (1 << 20)
+            assert st["num_visible"] == st_o["num_visible"]
+            assert st["num_entries"] == st_o["num_entries"]
+            assert np.abs(img - img_o).max() <= 1e-5
+    finally:
+        ctx.close()
+
+
 def test_render_edge_cases(gpu_ctx):
     scene, cam, cov = _scene(2_000, 26)
     # everything behind the camera -> M == 0 -> black image
