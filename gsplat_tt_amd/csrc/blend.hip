@@ -201,8 +201,31 @@ __device__ __forceinline__ void blend_band(const Band& g, const float4* __restri
             const float mx = e0.x, my = e0.y, op = e0.z;
             const float A = e1.x, B = e1.y, C = e1.z;
             const bool run = (mine >> j) & 1u;
-            if (run) {
-                if (INTERIOR || g.full) {
+            if (INTERIOR) {
+                // both halves evaluate the entry and a lane whose half does not
+                // keep it adds nothing (at = 0 leaves T and the colour exactly
+                // as they are): no divergent branch per entry
+                const float px_base = g.pxs - mx;
+                const float dx = px_base + g.offx;
+                const float dx_sq = dx * dx;
+                const float dy = g.pyc - my;
+                const float y_term = C * dy * dy;
+                const float xy_coef = B * dy;
+                float pwr = __builtin_fmaf(xy_coef, dx, y_term);
+                pwr = __builtin_fmaf(A, dx_sq, pwr);
+                pwr = (pwr < 0.0f) ? pwr : 0.0f;
+                pwr = (pwr > -30.0f) ? pwr : -30.0f;
+                const float gw = exp4(pwr);
+                float al = op * gw;
+                al = (al < 0.99f) ? al : 0.99f;
+                const float at = run ? al * T : 0.0f;
+                cr = __builtin_fmaf(at, e2.x, cr);
+                cg = __builtin_fmaf(at, e2.y, cg);
+                cb = __builtin_fmaf(at, e2.z, cb);
+                T = T - at;
+                cnt += run ? 1u : 0u;
+            } else if (run) {
+                if (g.full) {
                     const float px_base = g.pxs - mx;
                     const float dx = px_base + g.offx;
                     const float dx_sq = dx * dx;
