@@ -193,6 +193,70 @@ __device__ __forceinline__ void blend_band(const Band& g, const float4* __restri
         }
         __syncthreads();  // one wave per workgroup: orders the LDS writes and reads
         uint32_t uni = mA | mB;
+        if (INTERIOR) {
+            // two union entries per step: their alpha chains are independent
+            // (only T and the colour are carried from one to the next), so the
+            // two evaluations interleave; each entry keeps its own early-out test
+            auto alpha_of = [&](int j) {
+                const float4 e0 = s_rec[j].p0, e1 = s_rec[j].p1;
+                const float px_base = g.pxs - e0.x;
+                const float dx = px_base + g.offx;
+                const float dx_sq = dx * dx;
+                const float dy = g.pyc - e0.y;
+                const float y_term = e1.z * dy * dy;
+                const float xy_coef = e1.y * dy;
+                float pwr = __builtin_fmaf(xy_coef, dx, y_term);
+                pwr = __builtin_fmaf(e1.x, dx_sq, pwr);
+                pwr = (pwr < 0.0f) ? pwr : 0.0f;
+                pwr = (pwr > -30.0f) ? pwr : -30.0f;
+                const float gw = exp4(pwr);
+                float al = e0.z * gw;
+                return (al < 0.99f) ? al : 0.99f;
+            };
+            bool all_done = false;
+            auto apply = [&](int j, float al) {
+                const float4 e2 = s_rec[j].p2;
+                const bool run = (mine >> j) & 1u;
+                // a lane whose half does not keep the entry adds nothing
+                const float at = run ? al * T : 0.0f;
+                cr = __builtin_fmaf(at, e2.x, cr);
+                cg = __builtin_fmaf(at, e2.y, cg);
+                cb = __builtin_fmaf(at, e2.z, cb);
+                T = T - at;
+                cnt += run ? 1u : 0u;
+                // early-out test every 4 kept entries (cull_and_blend.cpp:578-616)
+                const uint64_t chkm = __ballot(run && (cnt & 3u) == 0u);
+                if (chkm != 0) {
+                    const uint64_t live = __ballot(!(T < bp.thr));
+                    const bool deadA = (uint32_t)chkm != 0u && (uint32_t)live == 0u;
+                    const bool deadB = (uint32_t)(chkm >> 32) != 0u && (uint32_t)(live >> 32) == 0u;
+                    if (deadA) doneA = true;
+                    if (deadB) doneB = true;
+                    const uint32_t keepA = doneA ? 0u : mA, keepB = doneB ? 0u : mB;
+                    uni &= keepA | keepB;
+                    mine = h ? keepB : keepA;
+                    all_done = doneA && doneB;
+                }
+            };
+            while (uni) {
+                const int j1 = __builtin_ctz(uni);
+                uni &= uni - 1;
+                const bool two = uni != 0u;
+                const int j2 = two ? __builtin_ctz(uni) : j1;
+                if (two) uni &= uni - 1;
+                n_iter += two ? 2u : 1u;
+                const float al1 = alpha_of(j1);
+                const float al2 = alpha_of(j2);
+                apply(j1, al1);
+                if (all_done) return;
+                // the test after the first entry may have retired a half: the
+                // second entry then adds nothing for it (mine is updated)
+                if (two) {
+                    apply(j2, al2);
+                    if (all_done) return;
+                }
+            }
+        } else {
         while (uni) {
             const int j = __builtin_ctz(uni);
             uni &= uni - 1;
@@ -277,6 +341,7 @@ __device__ __forceinline__ void blend_band(const Band& g, const float4* __restri
                 mine = h ? keepB : keepA;
                 if (doneA && doneB) return;
             }
+        }
         }
         __syncthreads();  // the next batch overwrites the staged records
     }
