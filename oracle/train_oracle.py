@@ -13,6 +13,11 @@ out analytically:
   * L1 gradient: train_loss.py:166-171 (mean |x - y| over 3HW, sign(0) = 0; the
     reference's device step also scales it by 1 - lambda_dssim = 0.8, here a
     `scale` argument);
+  * full 3DGS loss (1 - lambda) L1 + lambda (1 - SSIM): train_oracle.py:253-279
+    (11-tap Gaussian window, sigma 1.5, zero padding, C1 = 0.01^2,
+    C2 = 0.03^2, mean over 3HW) with the analytic image gradient of
+    train_loss.py:5-19 (fused-SSIM form: three filtered maps forward, three
+    backward);
   * blend backward: the reverse recursion over each pixel's live pairs;
   * projection backward: conic -> cov2d -> (J, cov3d) -> means / log-scales /
     quaternions, opacity logit, SH coefficients and the SH view direction;
@@ -20,8 +25,9 @@ out analytically:
     with step + 1 for every row).
 
 Pinned against the reference's dumps (tests/golden/t0_sh{0,3}_64x64_n50.npz:
-forward arrays, 2D gradients, parameter gradients, fp32 Adam outputs) and against
-central finite differences (tests/test_train_oracle.py).
+forward arrays, the full loss and its image gradient, 2D gradients, parameter
+gradients, fp32 Adam outputs) and against central finite differences
+(tests/test_train_oracle.py).
 """
 from __future__ import annotations
 
@@ -211,6 +217,60 @@ def l1_loss_grad(image, target, scale=1.0):
 
 
 # ------------------------------------------------------------------ backward
+SSIM_WIN, SSIM_SIGMA = 11, 1.5
+SSIM_C1, SSIM_C2 = 0.01 ** 2, 0.03 ** 2
+
+
+def gauss_window(size=SSIM_WIN, sigma=SSIM_SIGMA):
+    """Normalised 1D Gaussian taps (train_oracle.py:240-243)."""
+    x = np.arange(size, dtype=np.float64) - size // 2
+    g = np.exp(-(x * x) / (2.0 * sigma * sigma))
+    return g / g.sum()
+
+
+def gauss_filter(z, size=SSIM_WIN, sigma=SSIM_SIGMA):
+    """Separable Gaussian filter of (H, W, ...) arrays with zero padding: the
+    banded-matrix form G_h @ z @ G_w^T of train_oracle.py:246-266."""
+    g = gauss_window(size, sigma)
+    r = size // 2
+    z = np.asarray(z, np.float64)
+    H, W = z.shape[:2]
+    zp = np.zeros((H + 2 * r, W) + z.shape[2:])
+    zp[r:r + H] = z
+    t = sum(g[k] * zp[k:k + H] for k in range(size))
+    tp = np.zeros((H, W + 2 * r) + z.shape[2:])
+    tp[:, r:r + W] = t
+    return sum(g[k] * tp[:, k:k + W] for k in range(size))
+
+
+def ssim_loss_grad(image, target, lambda_dssim=0.2):
+    """(loss, l1, ssim, dL/dimage) of loss = (1 - lambda) mean|x - y| +
+    lambda (1 - SSIM(x, y)) (train_oracle.py:269-279), fp64; the gradient is the
+    analytic fused-SSIM form (train_loss.py:5-19): with S = A B / (C D),
+    dL/dx = (1 - lambda) sign(x - y)/n + G*(w dS/dmu_x) + 2 x G*(w dS/dE_xx)
+    + y G*(w dS/dE_xy), w = -lambda / n, n = 3HW (G is symmetric)."""
+    x = np.asarray(image, np.float64)
+    y = np.asarray(target, np.float64)
+    n = float(x.size)
+    mu_x, mu_y = gauss_filter(x), gauss_filter(y)
+    e_xx, e_yy, e_xy = gauss_filter(x * x), gauss_filter(y * y), gauss_filter(x * y)
+    A = 2.0 * mu_x * mu_y + SSIM_C1
+    B = 2.0 * (e_xy - mu_x * mu_y) + SSIM_C2
+    C = mu_x * mu_x + mu_y * mu_y + SSIM_C1
+    D = (e_xx - mu_x * mu_x) + (e_yy - mu_y * mu_y) + SSIM_C2
+    S = (A * B) / (C * D)
+    w = -lambda_dssim / n
+    d_mu = w * S * (2.0 * mu_y / A - 2.0 * mu_y / B - 2.0 * mu_x / C + 2.0 * mu_x / D)
+    d_xx = -w * S / D
+    d_xy = 2.0 * w * S / B
+    grad = gauss_filter(d_mu) + 2.0 * x * gauss_filter(d_xx) + y * gauss_filter(d_xy)
+    grad = grad + (1.0 - lambda_dssim) * np.sign(x - y) / n
+    l1 = float(np.abs(x - y).sum() / n)
+    ssim = float(S.sum() / n)
+    loss = (1.0 - lambda_dssim) * l1 + lambda_dssim * (1.0 - ssim)
+    return loss, l1, ssim, grad
+
+
 def blend_backward(pr, order, live, final_T, dL_dimage, H, W, cfg: Cfg):
     """dL/d(means2d, conic, opacity, colors) of the blend with the forward's
     decisions (live pairs, alpha clamp) held fixed, by the reverse recursion per

@@ -150,3 +150,38 @@ def test_gradients_vs_finite_differences(deg):
             assert abs(fd - an) <= 1e-5 * scale + 1e-9, (name, idx, fd, an)
             checked += 1
     assert checked > 40
+
+
+@pytest.mark.parametrize("name", golden_io.TRAIN_CASES)
+def test_ssim_loss_matches_dump(name):
+    """The dumps' `loss` and `dL_dimage` are the reference's full 3DGS loss
+    0.8 L1 + 0.2 (1 - SSIM) and its fp64 autograd image gradient."""
+    g = golden_io.load(name)
+    loss, l1, ssim, grad = TO.ssim_loss_grad(g["image"], g["target"], 0.2)
+    assert abs(loss - float(g["loss"])) <= 1e-12
+    assert rel_err(grad, g["dL_dimage"]) < 1e-10
+    assert 0.0 < ssim < 1.0 and l1 > 0.0
+
+
+def test_ssim_identity_and_finite_differences():
+    rng = np.random.default_rng(3)
+    x = rng.uniform(0, 1, (9, 13, 3))
+    # identical images: SSIM = 1 exactly at every pixel, a maximum (zero gradient)
+    loss, l1, ssim, grad = TO.ssim_loss_grad(x, x, 0.2)
+    assert abs(ssim - 1.0) < 1e-12 and l1 == 0.0 and abs(loss) < 1e-12
+    assert np.abs(grad).max() < 1e-12
+    # pure SSIM term (lambda = 1, no L1 kink) against central differences
+    y = np.clip(x + rng.normal(0, 0.1, x.shape), 0, 1)
+    _, _, _, g = TO.ssim_loss_grad(x, y, 1.0)
+    eps = 1e-6
+    for idx in rng.choice(x.size, 25, replace=False):
+        xp = x.copy().reshape(-1)
+        xp[idx] += eps
+        xm = x.copy().reshape(-1)
+        xm[idx] -= eps
+        fd = (TO.ssim_loss_grad(xp.reshape(x.shape), y, 1.0)[0] -
+              TO.ssim_loss_grad(xm.reshape(x.shape), y, 1.0)[0]) / (2 * eps)
+        assert abs(fd - g.reshape(-1)[idx]) <= 1e-7 * np.abs(g).max() + 1e-12
+    # the window is the reference's normalised 11-tap Gaussian (sigma 1.5)
+    w = TO.gauss_window()
+    assert w.shape == (11,) and abs(w.sum() - 1.0) < 1e-15 and np.argmax(w) == 5
