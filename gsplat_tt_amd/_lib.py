@@ -26,6 +26,7 @@ EXPORTED = (
     "gs_train_init", "gs_train_read", "gs_train_write", "gs_train_set_step",
     "gs_train_set_visible", "gs_train_forward", "gs_train_backward", "gs_train_adam",
     "gs_train_step",
+    "gs_train_loss",
 )
 TRAIN_PARAMS = ("means", "log_scales", "quats", "opacity_logits", "sh")
 
@@ -70,7 +71,7 @@ class GsTrainCfg(ctypes.Structure):
     _fields_ = [("near_plane", ctypes.c_float), ("lowpass", ctypes.c_float),
                 ("alpha_max", ctypes.c_float), ("alpha_min", ctypes.c_float),
                 ("t_min", ctypes.c_float), ("background", ctypes.c_float * 3),
-                ("loss_scale", ctypes.c_float),
+                ("loss_scale", ctypes.c_float), ("lambda_dssim", ctypes.c_float),
                 ("lr_means", ctypes.c_double), ("lr_log_scales", ctypes.c_double),
                 ("lr_quats", ctypes.c_double), ("lr_opacity", ctypes.c_double),
                 ("lr_sh_dc", ctypes.c_double), ("lr_sh_rest", ctypes.c_double),
@@ -81,7 +82,8 @@ class GsTrainStats(ctypes.Structure):
     _fields_ = [("num_blendable", ctypes.c_int64), ("num_entries", ctypes.c_int64),
                 ("step", ctypes.c_int64), ("loss", ctypes.c_double),
                 ("ms_forward", ctypes.c_float), ("ms_backward", ctypes.c_float),
-                ("ms_adam", ctypes.c_float), ("ms_total", ctypes.c_float)]
+                ("ms_adam", ctypes.c_float), ("ms_total", ctypes.c_float),
+                ("l1", ctypes.c_double), ("ssim", ctypes.c_double)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
@@ -94,9 +96,10 @@ class GsTrainProj(ctypes.Structure):
 
 def make_train_cfg(near=0.2, lowpass=0.3, alpha_max=0.99, alpha_min=1.0 / 255.0, t_min=1e-4,
                    background=(0.0, 0.0, 0.0), loss_scale=1.0, lr=None, betas=(0.9, 0.999),
-                   eps=1e-15) -> GsTrainCfg:
+                   eps=1e-15, lambda_dssim=0.0) -> GsTrainCfg:
     """Training configuration: gsplat/train_oracle.py RenderConfig (:63-71) and the
-    3DGS learning rates of DEFAULT_LR (:421-423)."""
+    3DGS learning rates of DEFAULT_LR (:421-423). lambda_dssim = 0: L1 loss;
+    0.2: the full 3DGS loss 0.8 L1 + 0.2 (1 - SSIM) (train_oracle.py:276-279)."""
     lr = dict({"means": 1.6e-4, "log_scales": 5e-3, "quats": 1e-3, "opacity_logits": 0.05,
                "sh_dc": 2.5e-3, "sh_rest": 2.5e-3 / 20.0}, **(lr or {}))
     c = GsTrainCfg()
@@ -105,6 +108,7 @@ def make_train_cfg(near=0.2, lowpass=0.3, alpha_max=0.99, alpha_min=1.0 / 255.0,
     for i in range(3):
         c.background[i] = float(background[i])
     c.loss_scale = float(loss_scale)
+    c.lambda_dssim = float(lambda_dssim)
     c.lr_means, c.lr_log_scales, c.lr_quats = lr["means"], lr["log_scales"], lr["quats"]
     c.lr_opacity, c.lr_sh_dc, c.lr_sh_rest = lr["opacity_logits"], lr["sh_dc"], lr["sh_rest"]
     c.beta1, c.beta2, c.eps = float(betas[0]), float(betas[1]), float(eps)
@@ -233,6 +237,20 @@ class Context:
         st = GsStats()
         _check(self._L.gs_render(self._c, ctypes.byref(view), _ptr(out), 0, ctypes.byref(st)))
         return out, st.as_dict()
+
+    def train_loss(self, image, target, lambda_dssim=0.2, loss_scale=1.0):
+        """(loss, l1, ssim, dL/dimage) of an (H,W,3) image against a target on the
+        GPU: loss_scale ((1 - lambda) L1 + lambda (1 - SSIM))."""
+        image, target = _f32(image), _f32(target)
+        if image.shape != target.shape or image.ndim != 3 or image.shape[2] != 3:
+            raise ValueError("image and target must both be (H, W, 3)")
+        H, W = image.shape[:2]
+        grad = np.empty_like(image)
+        out = (ctypes.c_double * 3)()
+        _check(self._L.gs_train_loss(self._c, _ptr(image), _ptr(target), int(H), int(W),
+                                     ctypes.c_float(lambda_dssim), ctypes.c_float(loss_scale),
+                                     _ptr(grad), out))
+        return out[0], out[1], out[2], grad
 
     def render_dev(self, view: GsView, dev_out_ptr: int):
         st = GsStats()

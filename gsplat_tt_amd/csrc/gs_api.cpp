@@ -190,7 +190,7 @@ struct gs_ctx {
         for (auto& e : tev)
             if (e) (void)hipEventDestroy(e);
         for (DevBuf* b : {&t_p, &t_m, &t_v, &t_g, &t_cidx, &t_vis, &t_grad2d, &t_img, &t_T, &t_stop,
-                          &t_dimg, &t_tgt, &t_loss, &t_dbg})
+                          &t_dimg, &t_tgt, &t_loss, &t_dbg, &t_ssim})
             b->release();
         if (st) (void)hipStreamDestroy(st);
     }
@@ -638,10 +638,10 @@ struct gs_ctx {
         gs::TrainCam cam{};
         uint32_t M = 0, P = 0;
         uint32_t* ids = nullptr;  // tile-sorted compact ids of the last forward
-        double loss = 0.0;
+        double loss = 0.0, l1 = 0.0, ssim = 0.0;
     } tr;
     DevBuf t_p, t_m, t_v, t_g, t_cidx, t_vis, t_grad2d, t_img, t_T, t_stop, t_dimg, t_tgt,
-        t_loss, t_dbg;
+        t_loss, t_dbg, t_ssim;
     std::vector<float> t_host;
     hipEvent_t tev[6] = {};
 
@@ -759,6 +759,29 @@ struct gs_ctx {
         REQUIRE(c->alpha_min > 0.0f && c->alpha_max >= c->alpha_min && c->alpha_max < 1.0f,
                 "train: need 0 < alpha_min <= alpha_max < 1");
         REQUIRE(c->t_min > 0.0f, "train: t_min must be > 0");
+        REQUIRE(c->lambda_dssim >= 0.0f && c->lambda_dssim <= 1.0f,
+                "train: lambda_dssim must be in [0, 1]");
+    }
+
+    // SSIM part of the full loss on device images: adds its gradient to dimage
+    // (which holds the L1 part) and its S sum to *ssim_sum.
+    void enqueue_ssim(const float* image, const float* target, int H, int W, float lambda,
+                      float loss_scale, float* dimage, double* ssim_sum) {
+        const size_t px = (size_t)H * W;
+        t_ssim.ensure(px * 36);
+        gs::SsimParams sp{};
+        sp.width = W;
+        sp.height = H;
+        double g[11], gs = 0.0;
+        for (int k = 0; k < 11; ++k) gs += (g[k] = std::exp(-(double)((k - 5) * (k - 5)) / 4.5));
+        for (int k = 0; k < 11; ++k) sp.g[k] = (float)(g[k] / gs);
+        sp.w = (float)(-(double)lambda * (double)loss_scale / (3.0 * (double)px));
+        sp.image = image;
+        sp.target = target;
+        sp.maps = t_ssim.as<float>();
+        sp.dimage = dimage;
+        sp.ssim_sum = ssim_sum;
+        HIPCHK(gs::launch_ssim(sp, st));
     }
 
     // Enqueues projection, tiles and the forward (+ L1 with a device target).
@@ -809,9 +832,13 @@ struct gs_ctx {
         fp.stop = t_stop.as<uint32_t>();
         fp.target = tgt_dev;
         fp.dimage = t_dimg.as<float>();
-        fp.grad_scale = (float)((double)c->loss_scale / (3.0 * (double)px));
+        fp.grad_scale = (float)((double)c->loss_scale * (1.0 - (double)c->lambda_dssim) /
+                                (3.0 * (double)px));
         fp.loss = reinterpret_cast<double*>(t_loss.p);
         HIPCHK(gs::launch_train_fwd(b_brec.as<float4>(), tr.ids, b_ranges.as<uint32_t>(), fp, st));
+        if (tgt_dev != nullptr && c->lambda_dssim > 0.0f)
+            enqueue_ssim(t_img.as<float>(), tgt_dev, H, W, c->lambda_dssim, c->loss_scale,
+                         t_dimg.as<float>(), reinterpret_cast<double*>(t_loss.p) + 1);
         if (timing) HIPCHK(hipEventRecord(tev[1], st));
     }
 
@@ -836,7 +863,7 @@ struct gs_ctx {
         for (int attempt = 0;; ++attempt) {
             train_forward_enqueue(v, c, tgt, dbg);
             HIPCHK(hipMemcpyAsync(h_pin, b_frame.p, 64 * 4, hipMemcpyDeviceToHost, st));
-            HIPCHK(hipMemcpyAsync(h_pin + 64, t_loss.p, 8, hipMemcpyDeviceToHost, st));
+            HIPCHK(hipMemcpyAsync(h_pin + 64, t_loss.p, 16, hipMemcpyDeviceToHost, st));
             sync();
             const uint32_t p_pre = h_pin[C_PPRE];
             if (p_pre == 0xFFFFFFFFu)
@@ -847,9 +874,13 @@ struct gs_ctx {
         }
         tr.M = h_pin[C_M];
         tr.P = h_pin[C_P];
-        double lsum;
-        std::memcpy(&lsum, h_pin + 64, 8);
-        tr.loss = tgt ? (double)c->loss_scale * lsum / (3.0 * (double)px) : 0.0;
+        double sums[2];
+        std::memcpy(sums, h_pin + 64, 16);
+        const double lam = c->lambda_dssim;
+        tr.l1 = tgt ? sums[0] / (3.0 * (double)px) : 0.0;
+        tr.ssim = (tgt && lam > 0.0) ? sums[1] / (3.0 * (double)px) : 0.0;
+        tr.loss = tgt ? (double)c->loss_scale * ((1.0 - lam) * tr.l1 + lam * (1.0 - tr.ssim))
+                      : 0.0;
         tr.fwd_valid = true;
         tr.has_dimage = tgt != nullptr;
     }
@@ -916,6 +947,8 @@ struct gs_ctx {
         o.num_entries = tr.P;
         o.step = tr.step;
         o.loss = tr.loss;
+        o.l1 = tr.l1;
+        o.ssim = tr.ssim;
         if (timing) {
             float ms = 0.0f;
             if (fwd && hipEventElapsedTime(&ms, tev[0], tev[1]) == hipSuccess) o.ms_forward = ms;
@@ -1422,6 +1455,47 @@ int gs_train_step(gs_ctx* ctx, const gs_view* view, const gs_train_cfg* cfg, con
         ctx->tr.fwd_valid = false;
         ctx->tr.grads_valid = false;
         ctx->train_stats(stats, true, true, true, t0);
+    });
+}
+
+int gs_train_loss(gs_ctx* ctx, const float* image, const float* target, int height, int width,
+                  float lambda_dssim, float loss_scale, float* dimage, double* loss3) {
+    return guard([&] {
+        REQUIRE(ctx && image && target && dimage, "null argument");
+        REQUIRE(height > 0 && width > 0 && (int64_t)height * width <= ((int64_t)1 << 28),
+                "train_loss: bad image size");
+        REQUIRE(lambda_dssim >= 0.0f && lambda_dssim <= 1.0f,
+                "train_loss: lambda_dssim must be in [0, 1]");
+        HIPCHK(hipSetDevice(ctx->device));
+        const size_t px = (size_t)height * width;
+        ctx->t_img.ensure(px * 12);
+        ctx->t_tgt.ensure(px * 12);
+        ctx->t_dimg.ensure(px * 12);
+        ctx->t_loss.ensure(16);
+        hipStream_t st = ctx->st;
+        HIPCHK(hipMemcpyAsync(ctx->t_img.p, image, px * 12, hipMemcpyHostToDevice, st));
+        HIPCHK(hipMemcpyAsync(ctx->t_tgt.p, target, px * 12, hipMemcpyHostToDevice, st));
+        HIPCHK(gs::launch_fill_u32(ctx->t_loss.as<uint32_t>(), 0u, 4, st));
+        double* sums = reinterpret_cast<double*>(ctx->t_loss.p);
+        const float scale = (float)((double)loss_scale * (1.0 - (double)lambda_dssim) /
+                                    (3.0 * (double)px));
+        HIPCHK(gs::launch_l1(ctx->t_img.as<float>(), ctx->t_tgt.as<float>(), (int64_t)px * 3,
+                             scale, ctx->t_dimg.as<float>(), sums, st));
+        if (lambda_dssim > 0.0f)
+            ctx->enqueue_ssim(ctx->t_img.as<float>(), ctx->t_tgt.as<float>(), height, width,
+                              lambda_dssim, loss_scale, ctx->t_dimg.as<float>(), sums + 1);
+        double h[2];
+        HIPCHK(hipMemcpyAsync(dimage, ctx->t_dimg.p, px * 12, hipMemcpyDeviceToHost, st));
+        HIPCHK(hipMemcpyAsync(h, sums, 16, hipMemcpyDeviceToHost, st));
+        ctx->sync();
+        ctx->tr.fwd_valid = false;  // t_dimg / t_img no longer hold a training forward
+        if (loss3) {
+            const double n = 3.0 * (double)px, lam = lambda_dssim;
+            const double l1 = h[0] / n, ssim = lam > 0.0 ? h[1] / n : 0.0;
+            loss3[0] = (double)loss_scale * ((1.0 - lam) * l1 + lam * (1.0 - ssim));
+            loss3[1] = l1;
+            loss3[2] = ssim;
+        }
     });
 }
 

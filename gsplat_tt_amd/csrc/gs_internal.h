@@ -211,6 +211,22 @@ struct TrainFwdParams {
     double* loss;          // accumulates sum |image - target|
 };
 
+// Full 3DGS loss terms (1 - lambda) L1 + lambda (1 - SSIM) on an (H,W,3) image.
+struct SsimParams {
+    int width, height;
+    float g[11];           // normalised Gaussian taps (sigma 1.5)
+    float w;               // -lambda * loss_scale / (3HW): scale of the SSIM terms
+    const float* image;    // (H,W,3)
+    const float* target;   // (H,W,3)
+    float* maps;           // 3 x (H,W,3): w dS/dmu_x, w dS/dE_xx, w dS/dE_xy
+    float* dimage;         // (H,W,3): the SSIM gradient is added
+    double* ssim_sum;      // accumulates sum of S over the 3HW values
+};
+hipError_t launch_ssim(const SsimParams& sp, hipStream_t st);
+// dimage = scale * sign(image - target); *l1_sum += sum |image - target|.
+hipError_t launch_l1(const float* image, const float* target, int64_t count, float scale,
+                     float* dimage, double* l1_sum, hipStream_t st);
+
 struct TrainBwdParams {
     int tiles_x, tiles_y, width, height;
     float alpha_max, alpha_min;

@@ -388,6 +388,179 @@ __global__ __launch_bounds__(256) void k_train_fwd(const float4* __restrict__ tr
     }
 }
 
+// ---------------------------------------------------------------------------
+// Full 3DGS loss (train_oracle.py:253-279): SSIM with an 11-tap Gaussian window
+// (sigma 1.5), zero padding, S = A B / (C D); the image gradient in the
+// fused-SSIM form of train_loss.py:5-19. One workgroup per 16x16 tile and
+// channel loop; a 26x26 halo in LDS, row pass then column pass.
+// ---------------------------------------------------------------------------
+constexpr int kSsimT = 16, kSsimR = 5, kSsimE = kSsimT + 2 * kSsimR;
+
+// Forward: mu_x, mu_y, E_xx, E_yy, E_xy -> S and the three per-pixel terms
+// w dS/dmu_x, w dS/dE_xx, w dS/dE_xy (zero outside the image), sum of S.
+__global__ __launch_bounds__(256) void k_ssim_fwd(SsimParams sp) {
+    __shared__ float s_x[kSsimE][kSsimE + 1], s_y[kSsimE][kSsimE + 1];
+    __shared__ float s_h[5][kSsimE][kSsimT + 1];
+    __shared__ double s_sum[4];
+    const int tid = threadIdx.x;
+    const int tiles_x = (sp.width + kSsimT - 1) / kSsimT;
+    const int tx = blockIdx.x % tiles_x, ty = blockIdx.x / tiles_x;
+    const int x0 = tx * kSsimT - kSsimR, y0 = ty * kSsimT - kSsimR;
+    const int lx = tid & 15, ly = tid >> 4;
+    const int px = tx * kSsimT + lx, py = ty * kSsimT + ly;
+    const bool inside = px < sp.width && py < sp.height;
+    const size_t npx = (size_t)sp.width * sp.height;
+    double ssum = 0.0;
+    for (int ch = 0; ch < 3; ++ch) {
+        for (int i = tid; i < kSsimE * kSsimE; i += 256) {
+            const int r = i / kSsimE, c = i % kSsimE;
+            const int gx = x0 + c, gy = y0 + r;
+            float xv = 0.0f, yv = 0.0f;
+            if (gx >= 0 && gx < sp.width && gy >= 0 && gy < sp.height) {
+                const size_t q = ((size_t)gy * sp.width + gx) * 3 + ch;
+                xv = sp.image[q];
+                yv = sp.target[q];
+            }
+            s_x[r][c] = xv;
+            s_y[r][c] = yv;
+        }
+        __syncthreads();
+        // row pass over all 26 halo rows, 16 output columns
+        for (int i = tid; i < kSsimE * kSsimT; i += 256) {
+            const int r = i / kSsimT, c = i % kSsimT;
+            float hx = 0.0f, hy = 0.0f, hxx = 0.0f, hyy = 0.0f, hxy = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 11; ++k) {
+                const float xv = s_x[r][c + k], yv = s_y[r][c + k], g = sp.g[k];
+                hx += g * xv;
+                hy += g * yv;
+                hxx += g * (xv * xv);
+                hyy += g * (yv * yv);
+                hxy += g * (xv * yv);
+            }
+            s_h[0][r][c] = hx;
+            s_h[1][r][c] = hy;
+            s_h[2][r][c] = hxx;
+            s_h[3][r][c] = hyy;
+            s_h[4][r][c] = hxy;
+        }
+        __syncthreads();
+        float mu_x = 0.0f, mu_y = 0.0f, e_xx = 0.0f, e_yy = 0.0f, e_xy = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 11; ++k) {
+            const float g = sp.g[k];
+            mu_x += g * s_h[0][ly + k][lx];
+            mu_y += g * s_h[1][ly + k][lx];
+            e_xx += g * s_h[2][ly + k][lx];
+            e_yy += g * s_h[3][ly + k][lx];
+            e_xy += g * s_h[4][ly + k][lx];
+        }
+        if (inside) {
+            const float c1 = 0.01f * 0.01f, c2 = 0.03f * 0.03f;
+            const float mxy = mu_x * mu_y;
+            const float A = 2.0f * mxy + c1;
+            const float B = 2.0f * (e_xy - mxy) + c2;
+            const float C = mu_x * mu_x + mu_y * mu_y + c1;
+            const float D = (e_xx - mu_x * mu_x) + (e_yy - mu_y * mu_y) + c2;
+            const float S = (A * B) / (C * D);
+            const float Sw = S * sp.w;
+            const float d_mu = Sw * (2.0f * mu_y / A - 2.0f * mu_y / B - 2.0f * mu_x / C +
+                                     2.0f * mu_x / D);
+            const size_t q = ((size_t)py * sp.width + px) * 3 + ch;
+            sp.maps[q] = d_mu;
+            sp.maps[3 * npx + q] = -Sw / D;
+            sp.maps[6 * npx + q] = 2.0f * Sw / B;
+            ssum += (double)S;
+        }
+        __syncthreads();  // the next channel overwrites the LDS planes
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ssum += __shfl_xor(ssum, o, GS_WAVE);
+    if (lane_id() == 0) s_sum[tid / GS_WAVE] = ssum;
+    __syncthreads();
+    if (tid == 0) atomicAdd(sp.ssim_sum, (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]));
+}
+
+// Backward: dimage += G*(w dS/dmu_x) + 2 x G*(w dS/dE_xx) + y G*(w dS/dE_xy)
+// (G symmetric, so its adjoint is the same zero-padded filter).
+__global__ __launch_bounds__(256) void k_ssim_bwd(SsimParams sp) {
+    __shared__ float s_m[3][kSsimE][kSsimE + 1];
+    __shared__ float s_h[3][kSsimE][kSsimT + 1];
+    const int tid = threadIdx.x;
+    const int tiles_x = (sp.width + kSsimT - 1) / kSsimT;
+    const int tx = blockIdx.x % tiles_x, ty = blockIdx.x / tiles_x;
+    const int x0 = tx * kSsimT - kSsimR, y0 = ty * kSsimT - kSsimR;
+    const int lx = tid & 15, ly = tid >> 4;
+    const int px = tx * kSsimT + lx, py = ty * kSsimT + ly;
+    const bool inside = px < sp.width && py < sp.height;
+    const size_t npx = (size_t)sp.width * sp.height;
+    for (int ch = 0; ch < 3; ++ch) {
+        for (int i = tid; i < kSsimE * kSsimE; i += 256) {
+            const int r = i / kSsimE, c = i % kSsimE;
+            const int gx = x0 + c, gy = y0 + r;
+            float a = 0.0f, b = 0.0f, d = 0.0f;
+            if (gx >= 0 && gx < sp.width && gy >= 0 && gy < sp.height) {
+                const size_t q = ((size_t)gy * sp.width + gx) * 3 + ch;
+                a = sp.maps[q];
+                b = sp.maps[3 * npx + q];
+                d = sp.maps[6 * npx + q];
+            }
+            s_m[0][r][c] = a;
+            s_m[1][r][c] = b;
+            s_m[2][r][c] = d;
+        }
+        __syncthreads();
+        for (int i = tid; i < kSsimE * kSsimT; i += 256) {
+            const int r = i / kSsimT, c = i % kSsimT;
+            float h0 = 0.0f, h1 = 0.0f, h2 = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 11; ++k) {
+                const float g = sp.g[k];
+                h0 += g * s_m[0][r][c + k];
+                h1 += g * s_m[1][r][c + k];
+                h2 += g * s_m[2][r][c + k];
+            }
+            s_h[0][r][c] = h0;
+            s_h[1][r][c] = h1;
+            s_h[2][r][c] = h2;
+        }
+        __syncthreads();
+        if (inside) {
+            float P = 0.0f, Q = 0.0f, R = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 11; ++k) {
+                const float g = sp.g[k];
+                P += g * s_h[0][ly + k][lx];
+                Q += g * s_h[1][ly + k][lx];
+                R += g * s_h[2][ly + k][lx];
+            }
+            const size_t q = ((size_t)py * sp.width + px) * 3 + ch;
+            sp.dimage[q] += P + 2.0f * sp.image[q] * Q + sp.target[q] * R;
+        }
+        __syncthreads();
+    }
+}
+
+// dimage = scale * sign(image - target), sum |image - target| (stage path).
+__global__ __launch_bounds__(256) void k_l1(const float* __restrict__ image,
+                                            const float* __restrict__ target, int64_t count,
+                                            float scale, float* __restrict__ dimage,
+                                            double* l1_sum) {
+    __shared__ double s_sum[4];
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    double a = 0.0;
+    if (i < count) {
+        const float d = image[i] - target[i];
+        dimage[i] = (d > 0.0f ? 1.0f : (d < 0.0f ? -1.0f : 0.0f)) * scale;
+        a = (double)fabsf(d);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o, GS_WAVE);
+    if (lane_id() == 0) s_sum[threadIdx.x / GS_WAVE] = a;
+    __syncthreads();
+    if (threadIdx.x == 0) atomicAdd(l1_sum, (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]));
+}
+
 // Sum over the 64 lanes of a wave (all lanes active), result in lane 63: DPP
 // moves inside each row of 16 lanes (quad swaps, half-row and row mirrors
 // leave every lane with its row's sum), then row broadcasts fold row 0 into
@@ -736,6 +909,25 @@ hipError_t launch_train_fwd(const float4* trec, const uint32_t* sid, const uint3
     const int tiles = fp.tiles_x * fp.tiles_y;
     if (tiles <= 0) return hipSuccess;
     k_train_fwd<<<tiles, 256, 0, st>>>(trec, sid, ranges, fp);
+    return hipGetLastError();
+}
+
+hipError_t launch_ssim(const SsimParams& sp, hipStream_t st) {
+    if (sp.width <= 0 || sp.height <= 0) return hipSuccess;
+    const unsigned tiles = (unsigned)(((sp.width + kSsimT - 1) / kSsimT) *
+                                      ((sp.height + kSsimT - 1) / kSsimT));
+    k_ssim_fwd<<<tiles, 256, 0, st>>>(sp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    k_ssim_bwd<<<tiles, 256, 0, st>>>(sp);
+    return hipGetLastError();
+}
+
+hipError_t launch_l1(const float* image, const float* target, int64_t count, float scale,
+                     float* dimage, double* l1_sum, hipStream_t st) {
+    if (count <= 0) return hipSuccess;
+    k_l1<<<(unsigned)((count + 255) / 256), 256, 0, st>>>(image, target, count, scale, dimage,
+                                                          l1_sum);
     return hipGetLastError();
 }
 

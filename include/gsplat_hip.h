@@ -165,7 +165,11 @@ typedef struct gs_train_cfg {
     float alpha_min;        /* 1/255: pairs below are skipped */
     float t_min;            /* 1e-4: a pixel stops before T (1 - alpha) drops below */
     float background[3];
-    float loss_scale;       /* dL/dimage = loss_scale * sign(image - target) / (3HW) */
+    float loss_scale;       /* scale of the whole loss (1: the reference's) */
+    float lambda_dssim;     /* 0: loss = loss_scale * mean |image - target| (L1);
+                             * > 0: loss_scale * ((1 - l) L1 + l (1 - SSIM)), the full
+                             * 3DGS loss at l = 0.2 (train_oracle.py:253-279: 11-tap
+                             * Gaussian window, sigma 1.5, zero padding) */
     /* Adam hyper-parameters in double, as the reference forms its fp32 step sizes
      * (float(lr / (1 - beta1^t)), float(1 - beta1), ...) from Python floats. */
     double lr_means, lr_log_scales, lr_quats, lr_opacity, lr_sh_dc, lr_sh_rest;
@@ -176,11 +180,13 @@ typedef struct gs_train_stats {
     int64_t num_blendable;  /* Gaussians that reach alpha_min somewhere (M) */
     int64_t num_entries;    /* tile-Gaussian pairs after the cull (P) */
     int64_t step;           /* Adam steps taken so far */
-    double loss;            /* loss_scale * mean |image - target| (with a target) */
+    double loss;            /* the loss of cfg (with a target) */
     float ms_forward;       /* device time: projection + tiles + forward + L1 */
     float ms_backward;      /* blend backward + projection backward */
     float ms_adam;
     float ms_total;         /* host wall clock of the call */
+    double l1;              /* mean |image - target| */
+    double ssim;            /* mean SSIM (computed when lambda_dssim > 0) */
 } gs_train_stats;
 
 /* Gaussian-indexed projection values of the last forward (parity tests). */
@@ -223,6 +229,14 @@ int gs_train_adam(gs_ctx* ctx, const gs_train_cfg* cfg, gs_train_stats* stats);
  * target_on_device) + backward + sparse Adam, one host synchronisation. */
 int gs_train_step(gs_ctx* ctx, const gs_view* view, const gs_train_cfg* cfg,
                   const float* target, int target_on_device, gs_train_stats* stats);
+
+/* Loss and image gradient of an (H,W,3) image against a target, both host
+ * arrays: loss_scale ((1 - lambda_dssim) L1 + lambda_dssim (1 - SSIM)) and
+ * dL/dimage (H,W,3), the device form of the reference's
+ * gsplat/train_loss.py:115-153 loss_and_grad_device (fp32). loss3 (optional)
+ * receives {loss, mean L1, mean SSIM}. */
+int gs_train_loss(gs_ctx* ctx, const float* image, const float* target, int height, int width,
+                  float lambda_dssim, float loss_scale, float* dimage, double* loss3);
 
 /* ---- device memory helpers (for callers without a GPU framework) ------ */
 int gs_dev_alloc(gs_ctx* ctx, int64_t bytes, void** ptr);

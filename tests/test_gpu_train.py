@@ -122,3 +122,74 @@ def test_train_steps_match_oracle(gpu_ctx):
         moved = np.abs(p_o[k] - params[k]).max()
         print(k, "max diff", d, "moved", moved)
         assert d <= 1e-2 * max(moved, 1e-12) + 1e-6, k
+
+
+@pytest.mark.parametrize("name", golden_io.TRAIN_CASES)
+def test_train_loss_ssim_matches_dump(gpu_ctx, name):
+    """gs_train_loss with lambda 0.2 is the reference's full loss: its value and
+    dL/dimage against the dump (fp64 autograd of 0.8 L1 + 0.2 (1 - SSIM)), on the
+    dump's image rounded to fp32 (the oracle re-evaluated on those inputs pins
+    the rounding part)."""
+    print("train loss ssim", name, flush=True)
+    g = golden_io.load(name)
+    img, tgt = g["image"].astype(np.float32), g["target"].astype(np.float32)
+    loss, l1, ssim, grad = gpu_ctx.train_loss(img, tgt, 0.2)
+    lo, l1o, so, go = TO.ssim_loss_grad(img, tgt, 0.2)
+    print(f"loss gpu {loss:.9f} oracle {lo:.9f} dump {float(g['loss']):.9f}; "
+          f"grad rel {rel_err(grad, go):.3g}")
+    assert abs(loss - lo) <= 1e-6 * lo and abs(l1 - l1o) <= 1e-6 * l1o
+    assert abs(ssim - so) <= 1e-6
+    assert abs(lo - float(g["loss"])) <= 1e-6 * lo  # fp32 rounding of the inputs only
+    assert rel_err(grad, go) < 1e-3
+    assert rel_err(grad, g["dL_dimage"]) < 1e-2  # the reference's device-backward gate
+
+
+def test_train_loss_ssim_full_size(gpu_ctx):
+    """1280x720 image against a noisy, blurred-edge target: device loss terms and
+    gradient against the fp64 oracle; lambda 0 gives the plain L1 gradient."""
+    print("train loss ssim 1280x720", flush=True)
+    rng = np.random.default_rng(9)
+    H, W = 720, 1280
+    tgt = rng.uniform(0, 1, (H, W, 3)).astype(np.float32)
+    img = np.clip(tgt + rng.normal(0, 0.05, tgt.shape), 0, 1).astype(np.float32)
+    img[100:300, 200:600] = 0.5  # a flat patch: low-variance SSIM terms
+    loss, l1, ssim, grad = gpu_ctx.train_loss(img, tgt, 0.2)
+    lo, l1o, so, go = TO.ssim_loss_grad(img, tgt, 0.2)
+    e = rel_err(grad, go)
+    print(f"loss gpu {loss:.9f} oracle {lo:.9f} ssim {ssim:.7f}/{so:.7f} grad rel {e:.3g}")
+    assert abs(loss - lo) <= 1e-6 * lo and abs(ssim - so) <= 1e-6
+    assert e < 1e-3
+    l0, l10, s0, g0 = gpu_ctx.train_loss(img, tgt, 0.0, loss_scale=2.0)
+    d = img.astype(np.float64) - tgt
+    assert s0 == 0.0 and abs(l0 - 2.0 * np.abs(d).mean()) <= 1e-6 * l0
+    assert np.array_equal(g0, (np.sign(d) * (2.0 / d.size)).astype(np.float32))
+
+
+def test_train_step_ssim_loss_matches_oracle(gpu_ctx):
+    """One whole step with the full 3DGS loss (lambda 0.2) of a C5-shaped scene
+    against the oracle's forward, SSIM loss gradient, backward and Adam."""
+    print("train step ssim c5-shaped", flush=True)
+    params, tparams, w2c, K, H, W = _c5_small(seed=57)
+    cfg_o = TO.Cfg(sh_degree=1)
+    cfg = L.make_train_cfg(lambda_dssim=0.2)
+    view = L.make_view(w2c, K, H, W, tile_size=16)
+    _, target, _, _, _ = TO.forward(tparams, w2c, K, H, W, cfg_o)
+    target = target.astype(np.float32)
+    tr = L.Trainer(gpu_ctx, params, 1)
+    st = tr.step(view, cfg, target)
+    p_o = {k: v.astype(np.float32) for k, v in params.items()}
+    pr, img, fT, order, live = TO.forward(p_o, w2c, K, H, W, cfg_o)
+    loss, l1, ssim, dimg = TO.ssim_loss_grad(img, target, 0.2)
+    g2 = TO.blend_backward(pr, order, live, fT, dimg, H, W, cfg_o)
+    grads = TO.projection_backward(pr, g2, cfg_o)
+    zeros = {k: np.zeros_like(v) for k, v in p_o.items()}
+    out = TO.sparse_adam(p_o, grads, zeros, dict(zeros), 0, pr["visible"])
+    print(f"loss gpu {st['loss']:.7f} oracle {loss:.7f}; ssim {st['ssim']:.7f}/{ssim:.7f}")
+    assert abs(st["loss"] - loss) <= 1e-4 * loss
+    assert abs(st["ssim"] - ssim) <= 1e-5 and abs(st["l1"] - l1) <= 1e-4 * l1
+    p = tr.read(0)
+    for k in TO.PARAM_NAMES:
+        d = np.abs(p[k] - out[k][0]).max()
+        moved = np.abs(out[k][0] - params[k]).max()
+        print(k, "max diff", d, "moved", moved)
+        assert d <= 1e-2 * max(moved, 1e-12) + 1e-6, k
