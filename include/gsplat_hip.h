@@ -233,7 +233,7 @@ int gs_train_step(gs_ctx* ctx, const gs_view* view, const gs_train_cfg* cfg,
 /* Loss and image gradient of an (H,W,3) image against a target, both host
  * arrays: loss_scale ((1 - lambda_dssim) L1 + lambda_dssim (1 - SSIM)) and
  * dL/dimage (H,W,3), the device form of the reference's
- * gsplat/train_loss.py:115-153 loss_and_grad_device (fp32). loss3 (optional)
+ * gsplat/train_loss.py:126-163 loss_and_grad_device (fp32). loss3 (optional)
  * receives {loss, mean L1, mean SSIM}. */
 int gs_train_loss(gs_ctx* ctx, const float* image, const float* target, int height, int width,
                   float lambda_dssim, float loss_scale, float* dimage, double* loss3);
