@@ -203,3 +203,43 @@ def test_sort_u64(gpu_ctx):
         ko, vo, passes = gpu_ctx.sort_pairs_u64(keys, vals, 0, 38)
         order = np.argsort(keys, kind="stable")
         assert np.array_equal(ko, keys[order]) and np.array_equal(vo, vals[order]), n
+
+
+def test_render_opacity_prune_is_exact(gpu_ctx):
+    """Dropping the Gaussians below min_opacity at load leaves the frame bit for
+    bit unchanged (the projection drops them and compacts in source order)."""
+    from gsplat_tt_amd import prep
+    scene, cam, cov = _scene(30_000, 71)
+    op = scene.opacities.copy()
+    op[::3] = 0.002  # a third of the scene below 1/255
+    view = L.make_view(cam.w2c, cam.K, cam.height, cam.width, tile_size=16, output="f32")
+    gpu_ctx.set_scene(scene.means, cov, op, scene.colors)
+    img_a, st_a = gpu_ctx.render(view)
+    pr = prep.opacity_prune({"means": scene.means, "cov": cov, "opacities": op,
+                             "colors": scene.colors})
+    assert pr["means"].shape[0] == 20_000
+    gpu_ctx.set_scene(pr["means"], pr["cov"], pr["opacities"], pr["colors"])
+    img_b, st_b = gpu_ctx.render(view)
+    assert st_a["num_visible"] == st_b["num_visible"]
+    assert st_a["num_entries"] == st_b["num_entries"]
+    assert np.array_equal(_bits(img_a), _bits(img_b))
+
+
+def test_render_morton_reordered_scene(gpu_ctx):
+    """A Morton-reordered scene renders as the oracle renders the same reordered
+    scene (counts bit-exact, image within the f32 bar)."""
+    from gsplat_tt_amd import prep
+    scene, cam, cov = _scene(40_000, 72)
+    arrays, order = prep.morton_reorder({"means": scene.means, "cov": cov,
+                                         "opacities": scene.opacities,
+                                         "colors": scene.colors})
+    assert not np.array_equal(order, np.arange(order.size))
+    img_o, st_o, _ = O.render_full(arrays["means"], arrays["cov"], arrays["opacities"],
+                                   arrays["colors"], cam.w2c, cam.K, cam.height, cam.width,
+                                   tile_size=16)
+    gpu_ctx.set_scene(arrays["means"], arrays["cov"], arrays["opacities"], arrays["colors"])
+    img, st = gpu_ctx.render(L.make_view(cam.w2c, cam.K, cam.height, cam.width, tile_size=16,
+                                         output="f32"))
+    assert st["num_visible"] == st_o["num_visible"]
+    assert st["num_entries"] == st_o["num_entries"]
+    assert np.abs(img - img_o).max() <= 1e-5
