@@ -52,6 +52,10 @@ def parse():
 
 
 def bench_frames(args):
+    """The orbit: `warmup` untimed frames, then `steps` frames timed as one camera
+    path through gs_render_batch (two frames in flight on two streams), with the
+    per-stage hipEvents off; then 16 frames one at a time with the events on,
+    for the per-stage times and the blend diagnostics."""
     from gsplat_tt_amd import _lib as L
     from gsplat_tt_amd import scenes
 
@@ -59,27 +63,32 @@ def bench_frames(args):
     scene, cams = scenes.config3(n=args.n, views=args.views)
     cov = scenes.cov3d(scene.scales, scene.quats)
     log(f"scene generated in {time.time() - t:.1f}s (N={scene.n})")
-    ctx = L.Context(0, timing=True)
+    ctx = L.Context(0, timing=False)
     cus, _ = ctx.device_info()
     t = time.time()
     ctx.set_scene(scene.means, cov, scene.opacities, scene.sh, sh_degree=3)
     log(f"scene resident in HBM in {time.time() - t:.1f}s ({cus} CUs)")
     H, W = cams[0].height, cams[0].width
-    out = ctx.dev_alloc(H * W * 3 * 2)
+    outs = [ctx.dev_alloc(H * W * 3 * 2) for _ in range(2)]
     views = [L.make_view(c.w2c, c.K, H, W, tile_size=16, output="bf16") for c in cams]
 
-    for i in range(args.warmup):
-        ctx.render_dev(views[i % len(views)], out)
-    ctx._L.gs_sync(ctx.handle)
+    def path(first, count):
+        return [views[(first + i) % len(views)] for i in range(count)]
+
+    if args.warmup > 0:
+        ctx.render_batch(path(0, args.warmup), [outs[i % 2] for i in range(args.warmup)])
     log(f"warmup {args.warmup} frames done")
-    stats = []
+    seq = path(args.warmup, args.steps)
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        stats.append(ctx.render_dev(views[i % len(views)], out))
+    ctx.render_batch(seq, [outs[i % 2] for i in range(args.steps)])
     ctx._L.gs_sync(ctx.handle)
     dt = time.perf_counter() - t0
-    ctx.dev_free(out)
     log(f"timed {args.steps} frames in {dt:.3f}s")
+    _check = L._check
+    _check(ctx._L.gs_set_timing(ctx.handle, 1))
+    stats = [ctx.render_dev(views[i % len(views)], outs[0]) for i in range(16)]
+    for o in outs:
+        ctx.dev_free(o)
     return ctx, scene, cov, cams, stats, dt
 
 
@@ -313,7 +322,9 @@ def main():
         "config": {"workload": "forward render, 6M Gaussians (slab+shell), SH degree 3, "
                                "1237x822, 16x16 tiles, 64-view orbit r=4m h=1m fx=fy=1100, "
                                "bf16 out", "global_batch": 1, "seq_len": 0,
-                   "parallelism": "single GPU", "n_gaussians": scene.n, "views": len(cams)},
+                   "parallelism": "single GPU", "n_gaussians": scene.n, "views": len(cams),
+                   "frames_in_flight": 2,
+                   "stage_times": "16 frames one at a time with per-stage hipEvents"},
         "stages": st,
         "roofline": roof,
     }

@@ -27,6 +27,7 @@ EXPORTED = (
     "gs_train_set_visible", "gs_train_forward", "gs_train_backward", "gs_train_adam",
     "gs_train_step",
     "gs_train_loss",
+    "gs_render_batch",
 )
 TRAIN_PARAMS = ("means", "log_scales", "quats", "opacity_logits", "sh")
 
@@ -251,6 +252,20 @@ class Context:
                                      ctypes.c_float(lambda_dssim), ctypes.c_float(loss_scale),
                                      _ptr(grad), out))
         return out[0], out[1], out[2], grad
+
+    def render_batch(self, views, outs, out_on_device=True):
+        """Views rendered with two frames in flight; outs: device pointers (or host
+        arrays when out_on_device is False), one per view. Returns their stats."""
+        n = len(views)
+        varr = (GsView * n)(*views)
+        if out_on_device:
+            ptrs = (ctypes.c_void_p * n)(*[ctypes.c_void_p(int(p)) for p in outs])
+        else:
+            ptrs = (ctypes.c_void_p * n)(*[o.ctypes.data_as(ctypes.c_void_p) for o in outs])
+        sts = (GsStats * n)()
+        _check(self._L.gs_render_batch(self._c, varr, ctypes.c_int(n), ptrs,
+                                       ctypes.c_int(1 if out_on_device else 0), sts))
+        return [st.as_dict() for st in sts]
 
     def render_dev(self, view: GsView, dev_out_ptr: int):
         st = GsStats()

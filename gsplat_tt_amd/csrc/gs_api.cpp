@@ -175,6 +175,7 @@ struct gs_ctx {
     gs::SortTemp sort;
 
     ~gs_ctx() {
+        delete peer;
         if (st) (void)hipStreamSynchronize(st);
         for (DevBuf* b : {&b_mean, &b_cov, &b_opac, &b_col, &b_terms, &b_upload, &b_rc,
                           &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_bstart, &b_pair_tile, &b_pair_id,
@@ -450,66 +451,163 @@ struct gs_ctx {
     // by the kernels from the counters; grids are sized for capacities (the
     // scene size, the pair capacity) and partitions beyond the real count exit
     // at once. If the candidates overflow the pair capacity the frame is run
-    // again with a larger one.
+    // again with a larger one. render_begin enqueues the frame and returns;
+    // render_end waits for it (and re-runs it after an overflow).
+    struct Pending {
+        bool active = false, empty = false;
+        gs_view v{};
+        void* out = nullptr;
+        void* dout = nullptr;
+        bool out_dev = false;
+        size_t bytes = 0;
+        int64_t T = 0;
+        int tiles_x = 0, tiles_y = 0, attempt = 0;
+        gs_stats* stats = nullptr;
+        std::chrono::steady_clock::time_point t0;
+    } pend;
+    gs_ctx* peer = nullptr;  // second frame slot of gs_render_batch (shares the scene)
+
     void render(const gs_view* v, void* out, bool out_dev, gs_stats* stats) {
-        const auto t0 = std::chrono::steady_clock::now();
+        render_begin(v, out, out_dev, stats, false);
+        render_end();
+    }
+
+    // shared_terms: the opacity terms of the scene descriptor are another
+    // context's (the batch's first slot computed them for this view's floors).
+    void render_begin(const gs_view* v, void* out, bool out_dev, gs_stats* stats,
+                      bool shared_terms) {
+        if (pend.active) {  // an earlier frame that was never completed
+            sync();
+            pend.active = false;
+        }
+        pend = Pending{};
+        pend.t0 = std::chrono::steady_clock::now();
         tr.fwd_valid = false;  // the frame buffers are about to be reused
         check_view(v);
         REQUIRE(out != nullptr, "render: null output");
-        ensure_terms(v);
+        if (!shared_terms) ensure_terms(v);
         if (timing)
             for (auto& e : ev)
                 if (!e) HIPCHK(hipEventCreate(&e));
         const int H = v->image_height, W = v->image_width, ts = v->tile_size;
-        const int tiles_x = (W + ts - 1) / ts, tiles_y = (H + ts - 1) / ts;
-        const int64_t T = (int64_t)tiles_x * tiles_y;
+        pend.v = *v;
+        pend.tiles_x = (W + ts - 1) / ts;
+        pend.tiles_y = (H + ts - 1) / ts;
+        pend.T = (int64_t)pend.tiles_x * pend.tiles_y;
         const size_t px = (size_t)H * W * 3;
         const size_t ebytes = v->out_format == GS_OUT_F32 ? 4 : (v->out_format == GS_OUT_BF16 ? 2 : 1);
-        void* dout = out;
+        pend.bytes = px * ebytes;
+        pend.out = out;
+        pend.out_dev = out_dev;
+        pend.dout = out;
         if (!out_dev) {
-            b_out.ensure(px * ebytes);
-            dout = b_out.p;
+            b_out.ensure(pend.bytes);
+            pend.dout = b_out.p;
         }
-        gs_stats s{};
-        const int64_t N = sd.n;
+        pend.stats = stats;
+        pend.active = true;
         ensure_counters();
-        if (N == 0) {
-            HIPCHK(gs::launch_fill_u32(static_cast<uint32_t*>(dout), 0u, px * ebytes / 4, st));
-            if ((px * ebytes) % 4)
-                HIPCHK(hipMemsetAsync(static_cast<char*>(dout) + px * ebytes / 4 * 4, 0,
-                                      (px * ebytes) % 4, st));
-            finish(out, dout, out_dev, px * ebytes, stats, s, t0);
+        if (sd.n == 0) {
+            pend.empty = true;
+            HIPCHK(gs::launch_fill_u32(static_cast<uint32_t*>(pend.dout), 0u, pend.bytes / 4, st));
+            if (pend.bytes % 4)
+                HIPCHK(hipMemsetAsync(static_cast<char*>(pend.dout) + pend.bytes / 4 * 4, 0,
+                                      pend.bytes % 4, st));
+            if (!out_dev) HIPCHK(hipMemcpyAsync(out, pend.dout, pend.bytes, hipMemcpyDeviceToHost, st));
             return;
         }
-        if (pair_cap == 0) pair_cap = std::max<uint64_t>(1u << 20, (uint64_t)N * 4);
-        for (int attempt = 0;; ++attempt) {
-            frame(v, dout, T, tiles_x, tiles_y);
-            if (!out_dev) HIPCHK(hipMemcpyAsync(out, dout, px * ebytes, hipMemcpyDeviceToHost, st));
-            HIPCHK(hipMemcpyAsync(h_pin, b_frame.p, 64 * 4, hipMemcpyDeviceToHost, st));
-            if (timing)
-                HIPCHK(hipMemcpyAsync(h_evals.data(), b_evals.p, 64 * 8 * 8, hipMemcpyDeviceToHost, st));
+        if (pair_cap == 0) pair_cap = std::max<uint64_t>(1u << 20, (uint64_t)sd.n * 4);
+        enqueue_attempt();
+    }
+
+    void enqueue_attempt() {
+        frame(&pend.v, pend.dout, pend.T, pend.tiles_x, pend.tiles_y);
+        if (!pend.out_dev)
+            HIPCHK(hipMemcpyAsync(pend.out, pend.dout, pend.bytes, hipMemcpyDeviceToHost, st));
+        HIPCHK(hipMemcpyAsync(h_pin, b_frame.p, 64 * 4, hipMemcpyDeviceToHost, st));
+        if (timing)
+            HIPCHK(hipMemcpyAsync(h_evals.data(), b_evals.p, 64 * 8 * 8, hipMemcpyDeviceToHost, st));
+    }
+
+    void render_end() {
+        REQUIRE(pend.active, "render: no frame in flight");
+        gs_stats s{};
+        for (;;) {
             sync();
+            if (pend.empty) break;
             const uint32_t p_pre = h_pin[C_PPRE];
-            if (p_pre == 0xFFFFFFFFu)
+            if (p_pre == 0xFFFFFFFFu) {
+                pend.active = false;
                 throw GsError(GS_E_CAPACITY, "render: more than 2^32-1 candidate pairs");
+            }
             if (p_pre <= pair_cap) break;
-            REQUIRE(attempt == 0, "render: pair capacity did not converge");
+            if (pend.attempt != 0) {
+                pend.active = false;
+                throw GsError(GS_E_INVALID, "render: pair capacity did not converge");
+            }
+            ++pend.attempt;
             pair_cap = std::min<uint64_t>(0xFFFFFFFFull, (uint64_t)p_pre + p_pre / 8 + 4096);
+            enqueue_attempt();
         }
-        s.num_visible = h_pin[C_M];
-        s.pairs_pre = h_pin[C_PPRE];
-        s.num_entries = h_pin[C_P];
-        if (timing) {
-            s.ms_project = elapsed(0, 1);
-            s.ms_depth_sort = elapsed(1, 2);
-            s.ms_tile_assign = elapsed(2, 3);
-            s.ms_tile_sort = elapsed(3, 4);
-            s.ms_blend = elapsed(4, 5);
-            blend_diag(s);
+        pend.active = false;
+        if (!pend.empty) {
+            s.num_visible = h_pin[C_M];
+            s.pairs_pre = h_pin[C_PPRE];
+            s.num_entries = h_pin[C_P];
+            if (timing) {
+                s.ms_project = elapsed(0, 1);
+                s.ms_depth_sort = elapsed(1, 2);
+                s.ms_tile_assign = elapsed(2, 3);
+                s.ms_tile_sort = elapsed(3, 4);
+                s.ms_blend = elapsed(4, 5);
+                blend_diag(s);
+            }
         }
-        s.ms_total = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() - t0)
-                         .count();
-        if (stats) *stats = s;
+        s.ms_total = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() -
+                                                               pend.t0).count();
+        if (pend.stats) *pend.stats = s;
+    }
+
+    // Renders views[0..n) keeping two frames in flight on two streams (this
+    // context and its peer, which shares the scene and has its own frame
+    // buffers): frame i+1 is enqueued before frame i is waited for, so one
+    // frame's tail stages overlap the next frame's head stages.
+    void render_batch(const gs_view* views, int n, void* const* outs, bool out_dev,
+                      gs_stats* stats) {
+        REQUIRE(views != nullptr && outs != nullptr && n >= 0, "render_batch: bad arguments");
+        if (n == 0) return;
+        for (int i = 0; i < n; ++i) {
+            check_view(&views[i]);
+            REQUIRE(views[i].contrib_floor == views[0].contrib_floor &&
+                        views[i].mb_contrib_floor == views[0].mb_contrib_floor &&
+                        views[i].k_cap == views[0].k_cap,
+                    "render_batch: every view must share the floors and k_cap");
+        }
+        ensure_terms(&views[0]);
+        if (peer == nullptr) {
+            auto* p = new gs_ctx();
+            p->device = device;
+            p->num_cus = num_cus;
+            hipError_t e = hipStreamCreateWithFlags(&p->st, hipStreamNonBlocking);
+            if (e != hipSuccess) {
+                delete p;
+                throw GsError(GS_E_DEVICE, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+            }
+            peer = p;
+        }
+        peer->timing = timing;
+        peer->sd = sd;  // scene planes and opacity terms of this context
+        peer->has_opac = has_opac;
+        peer->skey.valid = true;
+        peer->pair_cap = std::max(peer->pair_cap, pair_cap);
+        gs_ctx* slot[2] = {this, peer};
+        for (int i = 0; i < n; ++i) {
+            gs_ctx* c = slot[i & 1];
+            if (i >= 2) c->render_end();  // frame i-2 used this slot
+            c->render_begin(&views[i], outs[i], out_dev, stats ? &stats[i] : nullptr, true);
+        }
+        if (n >= 2) slot[(n - 2) & 1]->render_end();
+        slot[(n - 1) & 1]->render_end();
     }
 
     // Enqueues one frame (project -> depth sort -> tile assign -> tile sort ->
@@ -973,14 +1071,6 @@ struct gs_ctx {
         s.blend_max_iters = (int64_t)e[4];
     }
 
-    void finish(void* out, void* dout, bool out_dev, size_t bytes, gs_stats* stats, gs_stats s,
-                std::chrono::steady_clock::time_point t0) {
-        if (!out_dev) HIPCHK(hipMemcpyAsync(out, dout, bytes, hipMemcpyDeviceToHost, st));
-        sync();
-        s.ms_total = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() - t0)
-                         .count();
-        if (stats) *stats = s;
-    }
 };
 
 extern "C" {
@@ -1042,6 +1132,15 @@ int gs_render(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device, gs
         REQUIRE(ctx, "null ctx");
         HIPCHK(hipSetDevice(ctx->device));
         ctx->render(view, out, out_on_device != 0, stats);
+    });
+}
+
+int gs_render_batch(gs_ctx* ctx, const gs_view* views, int n, void* const* outs,
+                    int out_on_device, gs_stats* stats) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->render_batch(views, n, outs, out_on_device != 0, stats);
     });
 }
 

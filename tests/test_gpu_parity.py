@@ -243,3 +243,63 @@ def test_render_morton_reordered_scene(gpu_ctx):
     assert st["num_visible"] == st_o["num_visible"]
     assert st["num_entries"] == st_o["num_entries"]
     assert np.abs(img - img_o).max() <= 1e-5
+
+
+def test_render_batch_matches_single_frames(gpu_ctx):
+    """Two frames in flight (gs_render_batch) give each view the image and
+    counts of its own gs_render, for device and host outputs."""
+    scene, cams = scenes.config3(seed=73, n=60_000, views=8)
+    cov = O.cov3d(scene.scales, scene.quats)
+    gpu_ctx.set_scene(scene.means, cov, scene.opacities, scene.sh, sh_degree=3)
+    H, W = cams[0].height, cams[0].width
+    views = [L.make_view(c.w2c, c.K, H, W, tile_size=16, output="bf16") for c in cams]
+    single = [gpu_ctx.render(v) for v in views]
+    outs = [np.empty((H, W, 3), np.uint16) for _ in views]
+    stats = gpu_ctx.render_batch(views, outs, out_on_device=False)
+    for (img, st), out, sb in zip(single, outs, stats):
+        assert np.array_equal(img, out)
+        assert (st["num_visible"], st["num_entries"]) == (sb["num_visible"], sb["num_entries"])
+    ptrs = [gpu_ctx.dev_alloc(H * W * 6) for _ in range(3)]
+    try:
+        stats = gpu_ctx.render_batch(views[:3], ptrs)
+        for (img, st), p, sb in zip(single[:3], ptrs, stats):
+            got = np.empty((H, W, 3), np.uint16)
+            gpu_ctx.d2h(got, p)
+            assert np.array_equal(img, got) and st["num_entries"] == sb["num_entries"]
+    finally:
+        for p in ptrs:
+            gpu_ctx.dev_free(p)
+
+
+def test_render_batch_capacity_retry():
+    """A batch on a fresh context whose first frames overflow the pair capacity
+    in both slots: every frame is re-run and equals the oracle's."""
+    rng = np.random.default_rng(31)
+    n = 4200
+    means = np.stack([rng.uniform(-1.5, 1.5, n), rng.uniform(-1.1, 1.1, n),
+                      rng.uniform(3.0, 6.0, n)], 1).astype(np.float32)
+    scales = np.exp(rng.normal(np.log(0.4), 0.25, (n, 3))).astype(np.float32)
+    q = rng.standard_normal((n, 4))
+    quats = (q / np.linalg.norm(q, axis=1, keepdims=True)).astype(np.float32)
+    opac = rng.uniform(0.05, 0.35, n).astype(np.float32)
+    rgb = rng.uniform(0, 1, (n, 3)).astype(np.float32)
+    cov = O.cov3d(scales, quats)
+    K = scenes.intrinsics(500, 500, 320, 240)
+    w2cs = []
+    for k in range(3):
+        w2c = np.eye(4, dtype=np.float32)
+        w2c[0, 3] = 0.05 * k
+        w2cs.append(w2c)
+    ctx = L.Context(0)
+    try:
+        ctx.set_scene(means, cov, opac, rgb)
+        views = [L.make_view(w, K, 480, 640, tile_size=16, output="f32") for w in w2cs]
+        outs = [np.empty((480, 640, 3), np.float32) for _ in views]
+        stats = ctx.render_batch(views, outs, out_on_device=False)
+        for w2c, img, st in zip(w2cs, outs, stats):
+            ref, st_o, _ = O.render_full(means, cov, opac, rgb, w2c, K, 480, 640, tile_size=16)
+            assert st["pairs_pre"] > (1 << 20)
+            assert st["num_entries"] == st_o["num_entries"]
+            assert np.abs(img - ref).max() <= 1e-5
+    finally:
+        ctx.close()
