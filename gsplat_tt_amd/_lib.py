@@ -28,6 +28,7 @@ EXPORTED = (
     "gs_train_step",
     "gs_train_loss",
     "gs_render_batch",
+    "gs_render_next",
 )
 TRAIN_PARAMS = ("means", "log_scales", "quats", "opacity_logits", "sh")
 
@@ -252,6 +253,18 @@ class Context:
                                      ctypes.c_float(lambda_dssim), ctypes.c_float(loss_scale),
                                      _ptr(grad), out))
         return out[0], out[1], out[2], grad
+
+    def render_next(self, view: GsView, next_view: GsView | None = None, out=None):
+        """render() of `view` that also enqueues `next_view`'s frame on the second
+        slot; a following render_next(next_view, ...) completes it."""
+        H, W = view.image_height, view.image_width
+        if out is None:
+            out = np.empty((H, W, 3), _OUT_DTYPE[view.out_format])
+        st = GsStats()
+        _check(self._L.gs_render_next(self._c, ctypes.byref(view), _ptr(out), 0,
+                                      ctypes.byref(next_view) if next_view is not None else None,
+                                      ctypes.byref(st)))
+        return out, st.as_dict()
 
     def render_batch(self, views, outs, out_on_device=True):
         """Views rendered with two frames in flight; outs: device pointers (or host

@@ -181,7 +181,7 @@ struct gs_ctx {
                           &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_bstart, &b_pair_tile, &b_pair_id,
                           &b_ranges, &b_out, &b_kalt, &b_valt, &b_hist, &b_state, &b_lb, &b_cnt,
                           &b_tmp_a, &b_tmp_b, &b_tmp_c, &b_evals, &b_frame, &b_phist_proj,
-                          &b_phist_emit, &b_rect_r, &b_cov_r})
+                          &b_phist_emit, &b_rect_r, &b_cov_r, &b_spec})
             b->release();
         if (h_pin) (void)hipHostFree(h_pin);
         for (auto& e : ev)
@@ -209,6 +209,7 @@ struct gs_ctx {
             skey.opac == s->opacities && skey.col == s->colors && skey.n == s->n &&
             skey.stride == s->cov3d_stride && skey.deg == s->sh_degree && skey.ver == s->version)
             return;
+        drain_spec();  // an announced frame reads the buffers about to change
         const int64_t n = s->n;
         sync();
         const int K = s->sh_degree < 0 ? 1 : (s->sh_degree + 1) * (s->sh_degree + 1);
@@ -468,6 +469,7 @@ struct gs_ctx {
     gs_ctx* peer = nullptr;  // second frame slot of gs_render_batch (shares the scene)
 
     void render(const gs_view* v, void* out, bool out_dev, gs_stats* stats) {
+        drain_spec();
         render_begin(v, out, out_dev, stats, false);
         render_end();
     }
@@ -568,22 +570,9 @@ struct gs_ctx {
         if (pend.stats) *pend.stats = s;
     }
 
-    // Renders views[0..n) keeping two frames in flight on two streams (this
-    // context and its peer, which shares the scene and has its own frame
-    // buffers): frame i+1 is enqueued before frame i is waited for, so one
-    // frame's tail stages overlap the next frame's head stages.
-    void render_batch(const gs_view* views, int n, void* const* outs, bool out_dev,
-                      gs_stats* stats) {
-        REQUIRE(views != nullptr && outs != nullptr && n >= 0, "render_batch: bad arguments");
-        if (n == 0) return;
-        for (int i = 0; i < n; ++i) {
-            check_view(&views[i]);
-            REQUIRE(views[i].contrib_floor == views[0].contrib_floor &&
-                        views[i].mb_contrib_floor == views[0].mb_contrib_floor &&
-                        views[i].k_cap == views[0].k_cap,
-                    "render_batch: every view must share the floors and k_cap");
-        }
-        ensure_terms(&views[0]);
+    // The second frame slot: its own stream and frame buffers, this context's
+    // scene planes and opacity terms (refreshed at every use).
+    void ensure_peer() {
         if (peer == nullptr) {
             auto* p = new gs_ctx();
             p->device = device;
@@ -596,10 +585,89 @@ struct gs_ctx {
             peer = p;
         }
         peer->timing = timing;
-        peer->sd = sd;  // scene planes and opacity terms of this context
+        peer->sd = sd;
         peer->has_opac = has_opac;
         peer->skey.valid = true;
         peer->pair_cap = std::max(peer->pair_cap, pair_cap);
+    }
+
+    // Cross-view pipelining for render_view(..., next_extrinsics): the next
+    // view's whole frame is enqueued on the other slot, into that slot's own
+    // output buffer, before the current view is waited for; the next call
+    // takes it when its view equals the announced one and the scene is the
+    // same (render/host/render.cpp:316-322, 439-492). Any other entry point
+    // first completes and drops such a frame (drain_spec).
+    gs_ctx* spec_slot = nullptr;  // the slot holding the announced frame
+    gs_view spec_view{};
+    uint64_t spec_gen = 0;
+    DevBuf b_spec;                // output of an announced frame (per slot)
+    gs_stats spec_st{};
+
+    void drain_spec() {
+        if (spec_slot == nullptr) return;
+        gs_ctx* s = spec_slot;
+        spec_slot = nullptr;
+        s->render_end();
+    }
+
+    void render_next(const gs_view* v, void* out, bool out_dev, const gs_view* next,
+                     gs_stats* stats) {
+        check_view(v);
+        REQUIRE(out != nullptr, "render: null output");
+        if (next) check_view(next);
+        ensure_peer();
+        gs_ctx* cur;
+        const bool hit = spec_slot != nullptr && spec_gen == scene_gen &&
+                         std::memcmp(&spec_view, v, sizeof(gs_view)) == 0;
+        if (hit) {
+            cur = spec_slot;  // this view's frame is already in flight there
+            spec_slot = nullptr;
+        } else {
+            drain_spec();
+            cur = this;
+            cur->render_begin(v, out, out_dev, stats, false);
+            peer->sd = sd;  // terms for v's floors
+        }
+        // announce the next view on the other slot (same floors: shared terms)
+        if (next != nullptr && next->contrib_floor == v->contrib_floor &&
+            next->mb_contrib_floor == v->mb_contrib_floor && next->k_cap == v->k_cap) {
+            gs_ctx* other = cur == this ? peer : this;
+            const size_t eb = next->out_format == GS_OUT_F32 ? 4 : (next->out_format == GS_OUT_BF16 ? 2 : 1);
+            other->b_spec.ensure((size_t)next->image_height * next->image_width * 3 * eb);
+            other->render_begin(next, other->b_spec.p, true, &other->spec_st, true);
+            spec_slot = other;
+            spec_view = *next;
+            spec_gen = scene_gen;
+        }
+        cur->render_end();
+        if (hit) {
+            const size_t eb = v->out_format == GS_OUT_F32 ? 4 : (v->out_format == GS_OUT_BF16 ? 2 : 1);
+            const size_t bytes = (size_t)v->image_height * v->image_width * 3 * eb;
+            HIPCHK(hipMemcpyAsync(out, cur->b_spec.p, bytes,
+                                  out_dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, cur->st));
+            cur->sync();
+            if (stats) *stats = cur->spec_st;
+        }
+    }
+
+    // Renders views[0..n) keeping two frames in flight on two streams (this
+    // context and its peer, which shares the scene and has its own frame
+    // buffers): frame i+1 is enqueued before frame i is waited for, so one
+    // frame's tail stages overlap the next frame's head stages.
+    void render_batch(const gs_view* views, int n, void* const* outs, bool out_dev,
+                      gs_stats* stats) {
+        REQUIRE(views != nullptr && outs != nullptr && n >= 0, "render_batch: bad arguments");
+        drain_spec();
+        if (n == 0) return;
+        for (int i = 0; i < n; ++i) {
+            check_view(&views[i]);
+            REQUIRE(views[i].contrib_floor == views[0].contrib_floor &&
+                        views[i].mb_contrib_floor == views[0].mb_contrib_floor &&
+                        views[i].k_cap == views[0].k_cap,
+                    "render_batch: every view must share the floors and k_cap");
+        }
+        ensure_terms(&views[0]);
+        ensure_peer();
         gs_ctx* slot[2] = {this, peer};
         for (int i = 0; i < n; ++i) {
             gs_ctx* c = slot[i & 1];
@@ -1123,7 +1191,7 @@ int gs_scene_set(gs_ctx* ctx, const gs_scene* scene) {
     return guard([&] {
         REQUIRE(ctx, "null ctx");
         HIPCHK(hipSetDevice(ctx->device));
-        ctx->set_scene(scene);
+        ctx->set_scene(scene);  // completes an announced frame only if the scene changes
     });
 }
 
@@ -1131,7 +1199,17 @@ int gs_render(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device, gs
     return guard([&] {
         REQUIRE(ctx, "null ctx");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         ctx->render(view, out, out_on_device != 0, stats);
+    });
+}
+
+int gs_render_next(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device,
+                   const gs_view* next_view, gs_stats* stats) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->render_next(view, out, out_on_device != 0, next_view, stats);
     });
 }
 
@@ -1140,6 +1218,7 @@ int gs_render_batch(gs_ctx* ctx, const gs_view* views, int n, void* const* outs,
     return guard([&] {
         REQUIRE(ctx, "null ctx");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         ctx->render_batch(views, n, outs, out_on_device != 0, stats);
     });
 }
@@ -1150,6 +1229,7 @@ int gs_project(gs_ctx* ctx, const gs_scene* scene, const gs_view* view, uint8_t*
     return guard([&] {
         REQUIRE(ctx && m_out, "null argument");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         ctx->set_scene(scene);
         ctx->check_view(view);
         ctx->ensure_terms(view);
@@ -1202,6 +1282,7 @@ int gs_tile_assign(gs_ctx* ctx, const float* means2d, const float* radii, int64_
         REQUIRE(image_height > 0 && image_width > 0 && tile_size > 0, "bad image/tile size");
         REQUIRE(m == 0 || (means2d && radii), "null means2d/radii");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         const bool cull = covs2d != nullptr && opac != nullptr;
         *p_out = 0;
         if (p_pre_out) *p_pre_out = 0;
@@ -1255,6 +1336,7 @@ int gs_sort_and_bin(gs_ctx* ctx, const int64_t* gids, const int64_t* tids, const
         REQUIRE(tiles_x > 0 && tiles_y > 0, "bad tile grid");
         REQUIRE(p >= 0 && p < ((int64_t)1 << 32) - 1, "p out of range");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         const int64_t T = (int64_t)tiles_x * tiles_y;
         REQUIRE(T < ((int64_t)1 << 31), "too many tiles");
         std::vector<uint32_t> g((size_t)p), t((size_t)p);
@@ -1309,6 +1391,7 @@ int gs_cull_and_blend(gs_ctx* ctx, const float* means2d, const float* covs2d,
         REQUIRE(ctx && view && image_out && tile_ranges, "null argument");
         REQUIRE(m >= 0 && m < ((int64_t)1 << 31) && p >= 0 && p < ((int64_t)1 << 32), "size out of range");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         ctx->check_view(view);
         const int H = view->image_height, W = view->image_width, ts = view->tile_size;
         const int tiles_x = (W + ts - 1) / ts, tiles_y = (H + ts - 1) / ts;
@@ -1367,6 +1450,7 @@ int gs_sort_pairs_u64_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n
         REQUIRE(n >= 0 && n < ((int64_t)1 << 32) - 1, "n out of range");
         REQUIRE(0 <= begin_bit && begin_bit < end_bit && end_bit <= 64, "bad bit range");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         ctx->ensure_counters();
         ctx->ensure_sort(n, 8);
         ctx->sync();
@@ -1401,6 +1485,7 @@ int gs_train_init(gs_ctx* ctx, const gs_train_arrays* params, int64_t n, int sh_
     return guard([&] {
         REQUIRE(ctx, "null ctx");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         ctx->train_init(params, n, sh_degree);
     });
 }
@@ -1410,6 +1495,7 @@ int gs_train_read(gs_ctx* ctx, int which, gs_train_arrays* out) {
         REQUIRE(ctx && ctx->tr.ready, "train: gs_train_init first");
         REQUIRE(which >= 0 && which <= 3, "train: which must be 0..3");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         DevBuf* b[4] = {&ctx->t_p, &ctx->t_m, &ctx->t_v, &ctx->t_g};
         ctx->train_download(*b[which], out);
     });
@@ -1420,6 +1506,7 @@ int gs_train_write(gs_ctx* ctx, int which, const gs_train_arrays* in) {
         REQUIRE(ctx && ctx->tr.ready, "train: gs_train_init first");
         REQUIRE(which >= 0 && which <= 3, "train: which must be 0..3");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         DevBuf* b[4] = {&ctx->t_p, &ctx->t_m, &ctx->t_v, &ctx->t_g};
         ctx->sync();
         ctx->train_upload(*b[which], in);
@@ -1441,6 +1528,7 @@ int gs_train_set_visible(gs_ctx* ctx, const uint8_t* visible) {
         REQUIRE(ctx && ctx->tr.ready, "train: gs_train_init first");
         REQUIRE(visible != nullptr || ctx->tr.n == 0, "train: null mask");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         if (ctx->tr.n > 0)
             HIPCHK(hipMemcpyAsync(ctx->t_vis.p, visible, (size_t)ctx->tr.n, hipMemcpyHostToDevice,
                                   ctx->st));
@@ -1455,6 +1543,7 @@ int gs_train_forward(gs_ctx* ctx, const gs_view* view, const gs_train_cfg* cfg,
         const auto t0 = std::chrono::steady_clock::now();
         REQUIRE(ctx, "null ctx");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         ctx->train_check(view, cfg);
         const int64_t n = ctx->tr.n;
         gs::TrainDebug dbg{};
@@ -1498,6 +1587,7 @@ int gs_train_backward(gs_ctx* ctx, const gs_train_cfg* cfg, const float* dimage,
         REQUIRE(dimage != nullptr || ctx->tr.has_dimage,
                 "train: no dL/dimage (forward without a target and none given)");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         const size_t px = (size_t)ctx->tr.H * ctx->tr.W;
         if (dimage)
             HIPCHK(hipMemcpyAsync(ctx->t_dimg.p, dimage, px * 12, hipMemcpyHostToDevice, ctx->st));
@@ -1531,6 +1621,7 @@ int gs_train_adam(gs_ctx* ctx, const gs_train_cfg* cfg, gs_train_stats* stats) {
         REQUIRE(cfg != nullptr, "train: null cfg");
         REQUIRE(ctx->tr.grads_valid, "train: no gradients (run gs_train_backward first)");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         ctx->train_adam_enqueue(cfg);
         ctx->sync();
         ctx->tr.fwd_valid = false;  // parameters changed
@@ -1546,6 +1637,7 @@ int gs_train_step(gs_ctx* ctx, const gs_view* view, const gs_train_cfg* cfg, con
         REQUIRE(ctx, "null ctx");
         REQUIRE(target != nullptr, "train: null target");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         ctx->train_check(view, cfg);
         ctx->train_forward(view, cfg, target, target_on_device != 0, gs::TrainDebug{});
         ctx->train_backward_enqueue(cfg);
@@ -1566,6 +1658,7 @@ int gs_train_loss(gs_ctx* ctx, const float* image, const float* target, int heig
         REQUIRE(lambda_dssim >= 0.0f && lambda_dssim <= 1.0f,
                 "train_loss: lambda_dssim must be in [0, 1]");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         const size_t px = (size_t)height * width;
         ctx->t_img.ensure(px * 12);
         ctx->t_tgt.ensure(px * 12);
@@ -1602,6 +1695,7 @@ int gs_dev_alloc(gs_ctx* ctx, int64_t bytes, void** ptr) {
     return guard([&] {
         REQUIRE(ctx && ptr && bytes >= 0, "bad argument");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         HIPCHK(hipMalloc(ptr, (size_t)std::max<int64_t>(bytes, 1)));
     });
 }
@@ -1610,6 +1704,7 @@ int gs_dev_free(gs_ctx* ctx, void* ptr) {
     return guard([&] {
         REQUIRE(ctx, "null ctx");
         HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
         ctx->sync();
         if (ptr) HIPCHK(hipFree(ptr));
     });

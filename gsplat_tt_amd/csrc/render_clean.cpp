@@ -81,8 +81,9 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
     }
     if (extrinsics.size() != 16) throw std::invalid_argument("extrinsics must be 4x4");
     if (intrinsics.size() != 9) throw std::invalid_argument("intrinsics must be 3x3");
+    farr ne;
     if (!next_extrinsics.is_none()) {
-        auto ne = farr::ensure(next_extrinsics);
+        ne = farr::ensure(next_extrinsics);
         if (!ne || ne.size() != 16)
             throw std::invalid_argument("render_view: next_extrinsics must be 16 floats (4x4)");
     }
@@ -130,7 +131,14 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
         gs_ctx* c = ctx_locked();
         sc.version = g_scene_version;
         check(gs_scene_set(c, &sc));
-        check(gs_render(c, &v, out, 0, &st));
+        if (ne) {
+            // the next view: this call's parameters at the announced pose
+            gs_view nv = v;
+            std::memcpy(nv.extrinsics, ne.data(), sizeof(nv.extrinsics));
+            check(gs_render_next(c, &v, out, 0, &nv, &st));
+        } else {
+            check(gs_render_next(c, &v, out, 0, nullptr, &st));
+        }
         g_t.views++;
         g_t.project += st.ms_project;
         g_t.depth_sort += st.ms_depth_sort;

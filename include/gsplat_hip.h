@@ -107,6 +107,14 @@ int gs_render(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device, gs
  * share contrib_floor, mb_contrib_floor and k_cap. */
 int gs_render_batch(gs_ctx* ctx, const gs_view* views, int n, void* const* outs,
                     int out_on_device, gs_stats* stats);
+/* gs_render of `view`, and - with next_view - the next view's frame enqueued on
+ * the context's second slot before this one is waited for (render/host/
+ * render.cpp:316-322, the next_extrinsics argument of render_view): the next
+ * call whose view equals next_view (and whose scene is unchanged) completes
+ * that frame instead of starting one. Any other call first completes and
+ * drops an announced frame. */
+int gs_render_next(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device,
+                   const gs_view* next_view, gs_stats* stats);
 
 /* ---- stages on host arrays (parity entry points) ----------------------
  * gs_project: project_full_fused, src/gsplat_cpu/project.cpp:484-798.

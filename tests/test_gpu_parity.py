@@ -303,3 +303,51 @@ def test_render_batch_capacity_retry():
             assert np.abs(img - ref).max() <= 1e-5
     finally:
         ctx.close()
+
+
+def test_render_next_pipelines_exactly(gpu_ctx):
+    """gs_render_next with the next view announced: every frame equals its own
+    gs_render, also when the announced view is not the one asked for next, and
+    when the scene changes in between."""
+    scene, cams = scenes.config3(seed=74, n=50_000, views=6)
+    cov = O.cov3d(scene.scales, scene.quats)
+    gpu_ctx.set_scene(scene.means, cov, scene.opacities, scene.sh, sh_degree=3)
+    H, W = cams[0].height, cams[0].width
+    views = [L.make_view(c.w2c, c.K, H, W, tile_size=16, output="bf16") for c in cams]
+    single = [gpu_ctx.render(v) for v in views]
+    for i, v in enumerate(views):
+        nxt = views[i + 1] if i + 1 < len(views) else None
+        img, st = gpu_ctx.render_next(v, nxt)
+        assert np.array_equal(img, single[i][0]), i
+        assert st["num_entries"] == single[i][1]["num_entries"], i
+    # announced 1, asked for 3: the announced frame is dropped
+    gpu_ctx.render_next(views[0], views[1])
+    img, st = gpu_ctx.render_next(views[3], views[4])
+    assert np.array_equal(img, single[3][0])
+    # the scene changes while view 4 is announced
+    op2 = scene.opacities * np.float32(0.5)
+    gpu_ctx.set_scene(scene.means, cov, op2, scene.sh, sh_degree=3)
+    img, st = gpu_ctx.render_next(views[4], None)
+    ref, _ = gpu_ctx.render(views[4])
+    assert np.array_equal(img, ref) and not np.array_equal(img, single[4][0])
+
+
+def test_render_clean_next_extrinsics():
+    """render_view(..., next_extrinsics=...) renders exactly what render_view
+    renders without it, view after view."""
+    import gsplat_tt_amd
+    rc = gsplat_tt_amd.render_clean_module()
+    scene, cams = scenes.config3(seed=75, n=40_000, views=4)
+    cov = O.cov3d(scene.scales, scene.quats)
+    args = dict(image_height=cams[0].height, image_width=cams[0].width, tile_size=16,
+                min_opacity=1.0 / 255.0, contrib_floor=1.0 / 16384.0,
+                mb_contrib_floor=1.0 / 16384.0, cull_disabled=False,
+                transmittance_threshold=1.0 / 255.0, max_radius=0, k_cap=3.0,
+                use_isoellipse=False)
+    plain = [rc.render_view(scene.means, cov, scene.opacities, scene.sh, c.w2c, c.K,
+                            **args)[0] for c in cams]
+    for i, c in enumerate(cams):
+        nxt = cams[i + 1].w2c if i + 1 < len(cams) else None
+        img, st = rc.render_view(scene.means, cov, scene.opacities, scene.sh, c.w2c, c.K,
+                                 next_extrinsics=nxt, **args)
+        assert np.array_equal(img, plain[i]), i
