@@ -25,6 +25,8 @@ FP32_PEAK_TFLOPS = 157.3     # MI355X FP32 vector peak
 # per pixel x Gaussian evaluation: dx, dy (2 sub), quadratic form (3 mul + 2 FMA),
 # clamp, exp, alpha (mul + min), alpha*T, 3 colour FMA, T update; FMA = 2 flops
 BLEND_FLOPS_PER_EVAL = 20
+# frame slots of gs_render_batch; one output buffer per slot
+FRAMES_IN_FLIGHT = 3
 
 
 def log(msg):
@@ -53,7 +55,7 @@ def parse():
 
 def bench_frames(args):
     """The orbit: `warmup` untimed frames, then `steps` frames timed as one camera
-    path through gs_render_batch (two frames in flight on two streams), with the
+    path through gs_render_batch (three frames in flight on three streams), with the
     per-stage hipEvents off; then 16 frames one at a time with the events on,
     for the per-stage times and the blend diagnostics."""
     from gsplat_tt_amd import _lib as L
@@ -69,18 +71,18 @@ def bench_frames(args):
     ctx.set_scene(scene.means, cov, scene.opacities, scene.sh, sh_degree=3)
     log(f"scene resident in HBM in {time.time() - t:.1f}s ({cus} CUs)")
     H, W = cams[0].height, cams[0].width
-    outs = [ctx.dev_alloc(H * W * 3 * 2) for _ in range(2)]
+    outs = [ctx.dev_alloc(H * W * 3 * 2) for _ in range(FRAMES_IN_FLIGHT)]
     views = [L.make_view(c.w2c, c.K, H, W, tile_size=16, output="bf16") for c in cams]
 
     def path(first, count):
         return [views[(first + i) % len(views)] for i in range(count)]
 
     if args.warmup > 0:
-        ctx.render_batch(path(0, args.warmup), [outs[i % 2] for i in range(args.warmup)])
+        ctx.render_batch(path(0, args.warmup), [outs[i % FRAMES_IN_FLIGHT] for i in range(args.warmup)])
     log(f"warmup {args.warmup} frames done")
     seq = path(args.warmup, args.steps)
     t0 = time.perf_counter()
-    ctx.render_batch(seq, [outs[i % 2] for i in range(args.steps)])
+    ctx.render_batch(seq, [outs[i % FRAMES_IN_FLIGHT] for i in range(args.steps)])
     ctx._L.gs_sync(ctx.handle)
     dt = time.perf_counter() - t0
     log(f"timed {args.steps} frames in {dt:.3f}s")
@@ -323,7 +325,7 @@ def main():
                                "1237x822, 16x16 tiles, 64-view orbit r=4m h=1m fx=fy=1100, "
                                "bf16 out", "global_batch": 1, "seq_len": 0,
                    "parallelism": "single GPU", "n_gaussians": scene.n, "views": len(cams),
-                   "frames_in_flight": 2,
+                   "frames_in_flight": FRAMES_IN_FLIGHT,
                    "stage_times": "16 frames one at a time with per-stage hipEvents"},
         "stages": st,
         "roofline": roof,

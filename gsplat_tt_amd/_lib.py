@@ -267,7 +267,7 @@ class Context:
         return out, st.as_dict()
 
     def render_batch(self, views, outs, out_on_device=True):
-        """Views rendered with two frames in flight; outs: device pointers (or host
+        """Views rendered with up to three frames in flight; outs: device pointers (or host
         arrays when out_on_device is False), one per view. Returns their stats."""
         n = len(views)
         varr = (GsView * n)(*views)

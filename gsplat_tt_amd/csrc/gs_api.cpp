@@ -175,7 +175,7 @@ struct gs_ctx {
     gs::SortTemp sort;
 
     ~gs_ctx() {
-        delete peer;
+        for (gs_ctx* p : peers) delete p;
         if (st) (void)hipStreamSynchronize(st);
         for (DevBuf* b : {&b_mean, &b_cov, &b_opac, &b_col, &b_terms, &b_upload, &b_rc,
                           &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_bstart, &b_pair_tile, &b_pair_id,
@@ -466,7 +466,9 @@ struct gs_ctx {
         gs_stats* stats = nullptr;
         std::chrono::steady_clock::time_point t0;
     } pend;
-    gs_ctx* peer = nullptr;  // second frame slot of gs_render_batch (shares the scene)
+    // further frame slots (peer contexts sharing the scene): slot 0 is this one
+    std::vector<gs_ctx*> peers;
+    static constexpr int kFramesInFlight = 3;  // slots of gs_render_batch
 
     void render(const gs_view* v, void* out, bool out_dev, gs_stats* stats) {
         drain_spec();
@@ -570,10 +572,10 @@ struct gs_ctx {
         if (pend.stats) *pend.stats = s;
     }
 
-    // The second frame slot: its own stream and frame buffers, this context's
-    // scene planes and opacity terms (refreshed at every use).
-    void ensure_peer() {
-        if (peer == nullptr) {
+    // Frame slots 1..count-1: each its own stream and frame buffers, with this
+    // context's scene planes and opacity terms (refreshed at every use).
+    void ensure_peers(int count) {
+        while ((int)peers.size() < count - 1) {
             auto* p = new gs_ctx();
             p->device = device;
             p->num_cus = num_cus;
@@ -582,14 +584,17 @@ struct gs_ctx {
                 delete p;
                 throw GsError(GS_E_DEVICE, std::string("hipStreamCreate: ") + hipGetErrorString(e));
             }
-            peer = p;
+            peers.push_back(p);
         }
-        peer->timing = timing;
-        peer->sd = sd;
-        peer->has_opac = has_opac;
-        peer->skey.valid = true;
-        peer->pair_cap = std::max(peer->pair_cap, pair_cap);
+        for (gs_ctx* p : peers) {
+            p->timing = timing;
+            p->sd = sd;
+            p->has_opac = has_opac;
+            p->skey.valid = true;
+            p->pair_cap = std::max(p->pair_cap, pair_cap);
+        }
     }
+    gs_ctx* slot(int k) { return k == 0 ? this : peers[k - 1]; }
 
     // Cross-view pipelining for render_view(..., next_extrinsics): the next
     // view's whole frame is enqueued on the other slot, into that slot's own
@@ -615,7 +620,8 @@ struct gs_ctx {
         check_view(v);
         REQUIRE(out != nullptr, "render: null output");
         if (next) check_view(next);
-        ensure_peer();
+        ensure_peers(2);
+        gs_ctx* peer = peers[0];
         gs_ctx* cur;
         const bool hit = spec_slot != nullptr && spec_gen == scene_gen &&
                          std::memcmp(&spec_view, v, sizeof(gs_view)) == 0;
@@ -650,10 +656,11 @@ struct gs_ctx {
         }
     }
 
-    // Renders views[0..n) keeping two frames in flight on two streams (this
-    // context and its peer, which shares the scene and has its own frame
-    // buffers): frame i+1 is enqueued before frame i is waited for, so one
-    // frame's tail stages overlap the next frame's head stages.
+    // Renders views[0..n) keeping kFramesInFlight frames in flight, one per
+    // slot (this context and its peers, which share the scene and have their
+    // own streams and frame buffers): frame i+1.. are enqueued before frame i
+    // is waited for, so one frame's memory-bound stages run beside another's
+    // VALU-bound blend.
     void render_batch(const gs_view* views, int n, void* const* outs, bool out_dev,
                       gs_stats* stats) {
         REQUIRE(views != nullptr && outs != nullptr && n >= 0, "render_batch: bad arguments");
@@ -667,15 +674,14 @@ struct gs_ctx {
                     "render_batch: every view must share the floors and k_cap");
         }
         ensure_terms(&views[0]);
-        ensure_peer();
-        gs_ctx* slot[2] = {this, peer};
+        const int S = std::min(n, kFramesInFlight);
+        ensure_peers(S);
         for (int i = 0; i < n; ++i) {
-            gs_ctx* c = slot[i & 1];
-            if (i >= 2) c->render_end();  // frame i-2 used this slot
+            gs_ctx* c = slot(i % S);
+            if (i >= S) c->render_end();  // frame i-S used this slot
             c->render_begin(&views[i], outs[i], out_dev, stats ? &stats[i] : nullptr, true);
         }
-        if (n >= 2) slot[(n - 2) & 1]->render_end();
-        slot[(n - 1) & 1]->render_end();
+        for (int i = std::max(0, n - S); i < n; ++i) slot(i % S)->render_end();
     }
 
     // Enqueues one frame (project -> depth sort -> tile assign -> tile sort ->

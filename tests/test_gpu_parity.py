@@ -246,7 +246,7 @@ def test_render_morton_reordered_scene(gpu_ctx):
 
 
 def test_render_batch_matches_single_frames(gpu_ctx):
-    """Two frames in flight (gs_render_batch) give each view the image and
+    """Frames in flight (gs_render_batch) give each view the image and
     counts of its own gs_render, for device and host outputs."""
     scene, cams = scenes.config3(seed=73, n=60_000, views=8)
     cov = O.cov3d(scene.scales, scene.quats)
@@ -273,7 +273,7 @@ def test_render_batch_matches_single_frames(gpu_ctx):
 
 def test_render_batch_capacity_retry():
     """A batch on a fresh context whose first frames overflow the pair capacity
-    in both slots: every frame is re-run and equals the oracle's."""
+    in every slot: every frame is re-run and equals the oracle's."""
     rng = np.random.default_rng(31)
     n = 4200
     means = np.stack([rng.uniform(-1.5, 1.5, n), rng.uniform(-1.1, 1.1, n),
