@@ -164,6 +164,33 @@ def copy_calibration(nbytes):
     print(json.dumps({"copy_calibration_bytes": nbytes, "dispatches": 5}), flush=True)
 
 
+def bench_host_out(ctx, cams, frames):
+    """The orbit with images delivered to host memory (PCIe-inclusive, the
+    render_view path): u8 images into the pinned output ring with the next view
+    announced (gs_render_out_ring), and, for comparison, copied into a fresh
+    pageable numpy array per frame (gs_render_next). Not the headline value."""
+    from gsplat_tt_amd import _lib as L
+
+    L._check(ctx._L.gs_set_timing(ctx.handle, 0))
+    H, W = cams[0].height, cams[0].width
+    views = [L.make_view(c.w2c, c.K, H, W, tile_size=16, output="u8") for c in cams]
+    res = {"format": "u8", "frames": frames}
+    for name in ("ring", "pageable"):
+        for rep in range(2):  # the first pass warms the ring's pinned buffers
+            t0 = time.perf_counter()
+            for i in range(frames):
+                nxt = views[(i + 1) % len(views)] if i + 1 < frames else None
+                if name == "ring":
+                    img, _ = ctx.render_ring(views[i % len(views)], nxt)
+                else:
+                    img, _ = ctx.render_next(views[i % len(views)], nxt)
+                del img
+            dt = time.perf_counter() - t0
+        res[f"{name}_frames_per_s"] = round(frames / dt, 1)
+    L._check(ctx._L.gs_set_timing(ctx.handle, 1))  # the sort and training report stage times
+    return res
+
+
 def bench_sort(ctx, n):
     from gsplat_tt_amd import scenes
 
@@ -330,6 +357,8 @@ def main():
         "stages": st,
         "roofline": roof,
     }
+    res["host_out"] = bench_host_out(ctx, cams, min(args.steps, 64))
+    log(f"host_out: {res['host_out']}")
     if not args.no_sort:
         res["sort"] = bench_sort(ctx, args.sort_keys)
         log(f"sort: {res['sort']}")

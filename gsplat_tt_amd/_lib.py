@@ -29,6 +29,7 @@ EXPORTED = (
     "gs_train_loss",
     "gs_render_batch",
     "gs_render_next",
+    "gs_render_out_ring", "gs_out_release", "gs_out_ring_config", "gs_out_ring_info",
 )
 TRAIN_PARAMS = ("means", "log_scales", "quats", "opacity_logits", "sh")
 
@@ -62,6 +63,11 @@ class GsStats(ctypes.Structure):
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+class GsOutImage(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("bytes", ctypes.c_int64), ("pitch", ctypes.c_int64),
+                ("lease", ctypes.c_uint64)]
 
 
 class GsTrainArrays(ctypes.Structure):
@@ -129,6 +135,7 @@ def load_library():
         L = ctypes.CDLL(LIB_PATH)
         L.gs_last_error.restype = ctypes.c_char_p
         L.gs_destroy.restype = None
+        L.gs_out_release.argtypes = [ctypes.c_uint64]
         for name in EXPORTED:
             getattr(L, name)  # every declared symbol must resolve
         _LIB = L
@@ -176,6 +183,22 @@ def make_view(extrinsics, intrinsics, H, W, tile_size=16, min_opacity=1.0 / 255.
 
 
 _OUT_DTYPE = {0: np.uint8, 1: np.uint16, 2: np.float32}
+
+
+class _LeasedImage:
+    """The base object of an array over a ring image: releases the lease when
+    the last array over it is gone."""
+
+    def __init__(self, lib, img, shape, dtype):
+        self._lib = lib
+        self._lease = int(img.lease)
+        self.__array_interface__ = {"shape": shape, "typestr": np.dtype(dtype).str,
+                                    "data": (int(img.data), False), "version": 3}
+
+    def __del__(self):
+        if self._lease:
+            self._lib.gs_out_release(ctypes.c_uint64(self._lease))
+            self._lease = 0
 
 
 class Context:
@@ -265,6 +288,29 @@ class Context:
                                       ctypes.byref(next_view) if next_view is not None else None,
                                       ctypes.byref(st)))
         return out, st.as_dict()
+
+    def render_ring(self, view: GsView, next_view: GsView | None = None):
+        """render_next() whose image is a pinned buffer of the context's output
+        ring, returned without a host copy: an (H,W,3) array that holds the
+        buffer's lease until the array (and every view of it) is gone."""
+        img, st = GsOutImage(), GsStats()
+        _check(self._L.gs_render_out_ring(self._c, ctypes.byref(view),
+                                          ctypes.byref(next_view) if next_view is not None
+                                          else None, ctypes.byref(img), ctypes.byref(st)))
+        shape = (view.image_height, view.image_width, 3)
+        return np.asarray(_LeasedImage(self._L, img, shape, _OUT_DTYPE[view.out_format])), \
+            st.as_dict()
+
+    def out_ring_config(self, cap: int):
+        _check(self._L.gs_out_ring_config(self._c, ctypes.c_int(cap)))
+
+    def out_ring_info(self):
+        """(slots, slots whose image is held, slots made, slots replaced)."""
+        size, held = ctypes.c_int(), ctypes.c_int()
+        grows, replaced = ctypes.c_int64(), ctypes.c_int64()
+        _check(self._L.gs_out_ring_info(self._c, ctypes.byref(size), ctypes.byref(held),
+                                        ctypes.byref(grows), ctypes.byref(replaced)))
+        return size.value, held.value, grows.value, replaced.value
 
     def render_batch(self, views, outs, out_on_device=True):
         """Views rendered with up to three frames in flight; outs: device pointers (or host

@@ -18,6 +18,7 @@
 #include <climits>
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <thread>
@@ -25,6 +26,7 @@
 
 #include "../../include/gsplat_hip.h"
 #include "gs_internal.h"
+#include "out_ring.h"
 
 namespace {
 
@@ -184,6 +186,7 @@ struct gs_ctx {
                           &b_phist_emit, &b_rect_r, &b_cov_r, &b_spec})
             b->release();
         if (h_pin) (void)hipHostFree(h_pin);
+        ring.reset();  // held images stay valid until their leases are released
         for (auto& e : ev)
             if (e) (void)hipEventDestroy(e);
         for (auto& e : sort_ev)
@@ -607,6 +610,38 @@ struct gs_ctx {
     uint64_t spec_gen = 0;
     DevBuf b_spec;                // output of an announced frame (per slot)
     gs_stats spec_st{};
+
+    // Zero-copy output (render/host/out_ring.h, render.cpp:598-612): the frame's
+    // image is copied by DMA into a pinned buffer of the ring and handed over
+    // with a lease; the ring never rewrites a held buffer.
+    std::unique_ptr<gs::OutRing> ring;
+    size_t ring_cap = 4;
+    static void* pinned_alloc(size_t bytes) {
+        void* p = nullptr;
+        return hipHostMalloc(&p, bytes) == hipSuccess ? p : nullptr;
+    }
+    static void pinned_free(void* p) { (void)hipHostFree(p); }
+
+    void render_out_ring(const gs_view* v, const gs_view* next, gs_out_image* img,
+                         gs_stats* stats) {
+        REQUIRE(img != nullptr, "render_out_ring: null image");
+        check_view(v);
+        if (!ring) ring.reset(new gs::OutRing(pinned_alloc, pinned_free, ring_cap));
+        const size_t eb = v->out_format == GS_OUT_F32 ? 4 : (v->out_format == GS_OUT_BF16 ? 2 : 1);
+        const size_t pitch = (size_t)v->image_width * 3 * eb;
+        const size_t bytes = pitch * v->image_height;
+        gs::PinnedImage* im = nullptr;
+        try {
+            im = ring->acquire(bytes);
+        } catch (const std::bad_alloc&) {
+            throw GsError(GS_E_DEVICE, "render_out_ring: pinned host allocation failed");
+        }
+        render_next(v, im->p, false, next, stats);
+        img->data = im->p;
+        img->bytes = (int64_t)bytes;
+        img->pitch = (int64_t)pitch;
+        img->lease = gs::LeaseTable::get().lease(im);
+    }
 
     void drain_spec() {
         if (spec_slot == nullptr) return;
@@ -1216,6 +1251,41 @@ int gs_render_next(gs_ctx* ctx, const gs_view* view, void* out, int out_on_devic
         REQUIRE(ctx, "null ctx");
         HIPCHK(hipSetDevice(ctx->device));
         ctx->render_next(view, out, out_on_device != 0, next_view, stats);
+    });
+}
+
+int gs_render_out_ring(gs_ctx* ctx, const gs_view* view, const gs_view* next_view,
+                       gs_out_image* image, gs_stats* stats) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->render_out_ring(view, next_view, image, stats);
+    });
+}
+
+int gs_out_release(uint64_t lease) {
+    return guard([&] {
+        REQUIRE(gs::LeaseTable::get().release(lease), "gs_out_release: unknown or released lease");
+    });
+}
+
+int gs_out_ring_config(gs_ctx* ctx, int cap) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        REQUIRE(cap >= 1, "gs_out_ring_config: cap must be at least 1");
+        ctx->ring_cap = (size_t)cap;
+        if (ctx->ring) ctx->ring->set_cap((size_t)cap);
+    });
+}
+
+int gs_out_ring_info(gs_ctx* ctx, int* size, int* held, int64_t* grows, int64_t* replaced) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        const gs::OutRing* r = ctx->ring.get();
+        if (size) *size = r ? (int)r->size() : 0;
+        if (held) *held = r ? (int)r->held() : 0;
+        if (grows) *grows = r ? (int64_t)r->grows() : 0;
+        if (replaced) *replaced = r ? (int64_t)r->replaced() : 0;
     });
 }
 

@@ -10,14 +10,24 @@
 // Extensions, all keyword-only with defaults that keep the reference's
 // behaviour: `output` ("u8" default, "bf16" as uint16 bits, "f32") and SH
 // colours (colors of shape (N, K, 3), K = (d+1)^2, evaluated on the GPU).
+//
+// Zero-copy output, on by default as in the reference (render.cpp:334-340,
+// 598-612; env_config.h:251-277): the returned image is a pinned buffer of the
+// context's output ring, and the array keeps that buffer's lease, so the ring
+// never writes it again while Python holds the image or any view of it.
+// GSPLAT_TT_OUT_ZEROCOPY=0 (or GSPLAT_TT_OUT_PINNED=0) returns a fresh array
+// instead; GSPLAT_TT_OUT_ZEROCOPY_SLOTS (default 4, at least 1) caps the ring.
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 
+#include <algorithm>
 #include <chrono>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "gsplat_hip.h"
 
@@ -50,6 +60,21 @@ gs_ctx* ctx_locked() {
 }
 
 using farr = py::array_t<float, py::array::c_style | py::array::forcecast>;
+
+unsigned env_uint(const char* name, unsigned dflt) {
+    const char* v = std::getenv(name);
+    if (v == nullptr || *v == 0) return dflt;
+    char* end = nullptr;
+    const unsigned long x = std::strtoul(v, &end, 10);
+    return (end != nullptr && *end == 0) ? (unsigned)x : dflt;
+}
+bool out_zerocopy() {
+    return env_uint("GSPLAT_TT_OUT_ZEROCOPY", 1u) != 0u && env_uint("GSPLAT_TT_OUT_PINNED", 1u) != 0u;
+}
+int out_zerocopy_slots() {
+    const unsigned n = env_uint("GSPLAT_TT_OUT_ZEROCOPY_SLOTS", 4u);
+    return n < 1u ? 1 : (int)std::min(n, 1024u);
+}
 
 py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr extrinsics,
                       farr intrinsics, int image_height, int image_width, int tile_size,
@@ -119,11 +144,16 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
     v.sh_clamp_hi = sh_clamp ? 1 : 0;
     if (image_height <= 0 || image_width <= 0) throw std::invalid_argument("image size must be positive");
 
+    const bool zerocopy = out_zerocopy();
+    const int slots = out_zerocopy_slots();
     py::array image;
-    if (fmt == GS_OUT_U8) image = py::array_t<uint8_t>({image_height, image_width, 3});
-    else if (fmt == GS_OUT_BF16) image = py::array_t<uint16_t>({image_height, image_width, 3});
-    else image = py::array_t<float>({image_height, image_width, 3});
-    void* out = image.mutable_data();
+    if (!zerocopy) {
+        if (fmt == GS_OUT_U8) image = py::array_t<uint8_t>({image_height, image_width, 3});
+        else if (fmt == GS_OUT_BF16) image = py::array_t<uint16_t>({image_height, image_width, 3});
+        else image = py::array_t<float>({image_height, image_width, 3});
+    }
+    void* out = zerocopy ? nullptr : image.mutable_data();
+    gs_out_image ring_img{};
     gs_stats st{};
     {
         py::gil_scoped_release nogil;
@@ -131,13 +161,14 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
         gs_ctx* c = ctx_locked();
         sc.version = g_scene_version;
         check(gs_scene_set(c, &sc));
-        if (ne) {
-            // the next view: this call's parameters at the announced pose
-            gs_view nv = v;
-            std::memcpy(nv.extrinsics, ne.data(), sizeof(nv.extrinsics));
-            check(gs_render_next(c, &v, out, 0, &nv, &st));
+        // the next view: this call's parameters at the announced pose
+        gs_view nv = v;
+        if (ne) std::memcpy(nv.extrinsics, ne.data(), sizeof(nv.extrinsics));
+        if (zerocopy) {
+            check(gs_out_ring_config(c, slots));
+            check(gs_render_out_ring(c, &v, ne ? &nv : nullptr, &ring_img, &st));
         } else {
-            check(gs_render_next(c, &v, out, 0, nullptr, &st));
+            check(gs_render_next(c, &v, out, 0, ne ? &nv : nullptr, &st));
         }
         g_t.views++;
         g_t.project += st.ms_project;
@@ -146,6 +177,22 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
         g_t.tile_sort += st.ms_tile_sort;
         g_t.blend += st.ms_blend;
         g_t.view_total += st.ms_total;
+    }
+    if (zerocopy) {
+        // the array's base holds the lease: released when the image is collected
+        auto* lease = new uint64_t(ring_img.lease);
+        py::capsule keep(lease, [](void* p) {
+            auto* l = static_cast<uint64_t*>(p);
+            (void)gs_out_release(*l);
+            delete l;
+        });
+        const py::ssize_t eb = fmt == GS_OUT_F32 ? 4 : (fmt == GS_OUT_BF16 ? 2 : 1);
+        const std::vector<py::ssize_t> shape{image_height, image_width, 3};
+        const std::vector<py::ssize_t> strides{(py::ssize_t)ring_img.pitch, 3 * eb, eb};
+        const py::dtype dt = fmt == GS_OUT_U8 ? py::dtype::of<uint8_t>()
+                             : fmt == GS_OUT_BF16 ? py::dtype::of<uint16_t>()
+                                                  : py::dtype::of<float>();
+        image = py::array(dt, shape, strides, ring_img.data, keep);
     }
     py::dict stats;
     stats["num_visible"] = st.num_visible;

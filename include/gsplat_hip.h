@@ -116,6 +116,29 @@ int gs_render_batch(gs_ctx* ctx, const gs_view* views, int n, void* const* outs,
 int gs_render_next(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device,
                    const gs_view* next_view, gs_stats* stats);
 
+/* ---- zero-copy output ring (render/host/out_ring.h; render/host/render.cpp:
+ * 334-340,598-612, GSPLAT_TT_OUT_ZEROCOPY) ------------------------------
+ * gs_render_out_ring is gs_render_next whose image lands (by DMA from HBM) in
+ * a pinned host buffer of the context's ring; the caller gets that buffer, no
+ * host copy, and a lease. The ring never writes a buffer whose lease is held:
+ * it takes the first free slot after the last one written, else grows up to
+ * its cap, else gives the slot after the last one written a new buffer (the
+ * held one stays valid until released). gs_out_release ends a lease; it may be
+ * called from any thread and after gs_destroy (the buffer is then freed). */
+typedef struct gs_out_image {
+    const void* data;   /* (H, W, 3) of the view's out_format, pinned host memory */
+    int64_t bytes;
+    int64_t pitch;      /* bytes per image row: W * 3 * element size */
+    uint64_t lease;     /* nonzero; pass to gs_out_release when done with data */
+} gs_out_image;
+int gs_render_out_ring(gs_ctx* ctx, const gs_view* view, const gs_view* next_view,
+                       gs_out_image* image, gs_stats* stats);
+int gs_out_release(uint64_t lease);
+/* most buffers the ring keeps (default 4, GSPLAT_TT_OUT_ZEROCOPY_SLOTS of
+ * render/host/env_config.h:272-277); a smaller cap lets go of surplus slots */
+int gs_out_ring_config(gs_ctx* ctx, int cap);
+int gs_out_ring_info(gs_ctx* ctx, int* size, int* held, int64_t* grows, int64_t* replaced);
+
 /* ---- stages on host arrays (parity entry points) ----------------------
  * gs_project: project_full_fused, src/gsplat_cpu/project.cpp:484-798.
  * Outputs sized for n; *m_out = M. colors_out is (M,3) RGB (SH evaluated). */
