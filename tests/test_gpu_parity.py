@@ -205,6 +205,39 @@ def test_sort_u64(gpu_ctx):
         assert np.array_equal(ko, keys[order]) and np.array_equal(vo, vals[order]), n
 
 
+def test_sort_u64_partitions_and_skipped_passes(gpu_ctx):
+    """64-bit sorts spanning several counting workgroups (64 partitions each),
+    with constant digits (their passes skipped: the first pass then counts from
+    the keys), all keys equal (no pass), and full 64-bit keys (8 passes)."""
+    rng = np.random.default_rng(11)
+    n = 1_000_003
+    z = np.minimum(rng.zipf(1.1, n), 5000).astype(np.uint64) - np.uint64(1)
+    d = np.exp(rng.uniform(np.log(0.2), np.log(100.0), n)).astype(np.float32)
+    keys = (z << np.uint64(32)) | d.view(np.uint32).astype(np.uint64)
+    vals = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+    cases = [(keys, 45, None),
+             ((keys >> np.uint64(16)) << np.uint64(16), 45, 4),   # bytes 0, 1 constant
+             (np.full(200_000, 0x1234_5678_9ABC_DEF0, np.uint64), 64, 0),
+             (rng.integers(0, 2**63, 500_000, dtype=np.uint64) * np.uint64(2) + np.uint64(1), 64, 8)]
+    for k, end_bit, want_passes in cases:
+        v = vals[: k.shape[0]]
+        ko, vo, passes = gpu_ctx.sort_pairs_u64(k, v, 0, end_bit)
+        order = np.argsort(k, kind="stable")
+        assert np.array_equal(ko, k[order]) and np.array_equal(vo, v[order]), (k.shape, end_bit)
+        if want_passes is not None:
+            assert passes == want_passes
+
+
+def test_sort_u64_config4_20m(gpu_ctx):
+    """The standalone sort's key distribution (Zipf 1.1 tiles over 5000, log-uniform
+    depths) at 20M keys: exact against numpy's stable sort."""
+    keys, vals = scenes.config4_keys(n=20_000_000)
+    ko, vo, passes = gpu_ctx.sort_pairs_u64(keys, vals, 0, 45)
+    order = np.argsort(keys, kind="stable")
+    assert passes == 6
+    assert np.array_equal(ko, keys[order]) and np.array_equal(vo, vals[order])
+
+
 def test_render_opacity_prune_is_exact(gpu_ctx):
     """Dropping the Gaussians below min_opacity at load leaves the frame bit for
     bit unchanged (the projection drops them and compacts in source order)."""
