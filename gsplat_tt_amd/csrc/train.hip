@@ -341,7 +341,7 @@ __global__ __launch_bounds__(256) void k_train_fwd(const float4* __restrict__ tr
                 const float4 r0 = s0[j], r1 = s1[j];
                 const float dx = pxc - r0.x, dy = pyc - r0.y;
                 const float power = -0.5f * (r1.x * dx * dx + 2.0f * r1.y * dx * dy + r1.z * dy * dy);
-                const float raw = r0.z * expf(power < 0.0f ? power : 0.0f);
+                const float raw = r0.z * __expf(power < 0.0f ? power : 0.0f);
                 const float alpha = raw > fp.alpha_max ? fp.alpha_max : raw;
                 if (alpha < fp.alpha_min) continue;
                 const float tn = T * (1.0f - alpha);
@@ -561,22 +561,20 @@ __global__ __launch_bounds__(256) void k_l1(const float* __restrict__ image,
     if (threadIdx.x == 0) atomicAdd(l1_sum, (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]));
 }
 
-// Sum over the 64 lanes of a wave (all lanes active), result in lane 63: DPP
-// moves inside each row of 16 lanes (quad swaps, half-row and row mirrors
-// leave every lane with its row's sum), then row broadcasts fold row 0 into
-// row 1, row 2 into row 3, and row 1 into row 3.
+// v plus the value a DPP move brings into the lane (all lanes active).
 template <int CTRL, int ROWS>
 __device__ __forceinline__ float dpp_add(float v) {
     const int x = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false);
     return v + __int_as_float(x);
 }
-__device__ __forceinline__ float wave_fsum_last(float v) {
+
+// Sum over each row of 16 lanes, left in every lane of the row (quad swaps,
+// half-row and row mirrors).
+__device__ __forceinline__ float row_fsum(float v) {
     v = dpp_add<0xB1, 0xF>(v);   // quad_perm 1,0,3,2
     v = dpp_add<0x4E, 0xF>(v);   // quad_perm 2,3,0,1
     v = dpp_add<0x141, 0xF>(v);  // row_half_mirror
     v = dpp_add<0x140, 0xF>(v);  // row_mirror
-    v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
-    v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
     return v;
 }
 
@@ -587,14 +585,17 @@ constexpr int kBwdBatch = 128;
 // behind_i = alpha_{i+1} c_{i+1} + (1 - alpha_{i+1}) behind_{i+1},
 // dL/dalpha_i = T_i (c_i - behind_i) . g - T_final bg . g / (1 - alpha_i).
 // The nine per-pair sums (dmx dmy dA dB dC dop dr dg db) are reduced over each
-// wave, staged in LDS, summed over the tile's four waves and added to the
-// Gaussian's accumulator with one atomic per term.
+// 16-lane row of a wave and added into four LDS accumulators (one per row
+// position, shared by the tile's four waves); their sum goes to the Gaussian's
+// accumulator with one global atomic per term. 1/(1 - alpha) is one reciprocal
+// estimate, exp the hardware exponential (the forward uses the same one, so both
+// see the same alpha).
 __global__ __launch_bounds__(256) void k_train_bwd(const float4* __restrict__ trec,
                                                    const uint32_t* __restrict__ sid,
                                                    const uint32_t* __restrict__ ranges,
                                                    TrainBwdParams bp) {
     __shared__ float4 s0[kBwdBatch], s1[kBwdBatch], s2[kBwdBatch];
-    __shared__ float s_part[4][kBwdBatch][9];
+    __shared__ float s_acc[4][kBwdBatch][9];
     __shared__ uint32_t s_has[4][kBwdBatch];
     __shared__ uint32_t s_nmax;
     const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
@@ -630,6 +631,7 @@ __global__ __launch_bounds__(256) void k_train_bwd(const float4* __restrict__ tr
             s1[tid] = trec[3 * (size_t)gi + 1];
             s2[tid] = trec[3 * (size_t)gi + 2];
         }
+        for (int i = tid; i < 4 * kBwdBatch * 9; i += 256) (&s_acc[0][0][0])[i] = 0.0f;
         __syncthreads();
         for (int32_t j = nb - 1; j >= 0; --j) {
             const uint32_t e = (uint32_t)(lo + j);
@@ -642,7 +644,7 @@ __global__ __launch_bounds__(256) void k_train_bwd(const float4* __restrict__ tr
                 const float dx = pxc - r0.x, dy = pyc - r0.y;
                 const float power =
                     -0.5f * (r1.x * dx * dx + 2.0f * r1.y * dx * dy + r1.z * dy * dy);
-                const float wgt = expf(power < 0.0f ? power : 0.0f);
+                const float wgt = __expf(power < 0.0f ? power : 0.0f);
                 const float raw = r0.z * wgt;
                 const bool clamp = raw > bp.alpha_max;
                 const float alpha = clamp ? bp.alpha_max : raw;
@@ -650,9 +652,10 @@ __global__ __launch_bounds__(256) void k_train_bwd(const float4* __restrict__ tr
                     live = true;
                     const float4 c = s2[j];
                     const float om = 1.0f - alpha;
-                    T = T / om;
+                    const float rom = __builtin_amdgcn_rcpf(om);
+                    T = T * rom;
                     const float dalpha =
-                        T * ((c.x - b0) * g0 + (c.y - b1) * g1 + (c.z - b2) * g2) - tbg / om;
+                        T * ((c.x - b0) * g0 + (c.y - b1) * g1 + (c.z - b2) * g2) - tbg * rom;
                     const float at = alpha * T;
                     v[6] = at * g0;
                     v[7] = at * g1;
@@ -674,28 +677,22 @@ __global__ __launch_bounds__(256) void k_train_bwd(const float4* __restrict__ tr
             const uint64_t any = __ballot(live);
             if (any) {
 #pragma unroll
-                for (int k = 0; k < 9; ++k) v[k] = wave_fsum_last(v[k]);
-                if (lane == GS_WAVE - 1) {
+                for (int k = 0; k < 9; ++k) v[k] = row_fsum(v[k]);
+                if ((lane & 15) == 0) {
 #pragma unroll
-                    for (int k = 0; k < 9; ++k) s_part[w][j][k] = v[k];
+                    for (int k = 0; k < 9; ++k) atomicAdd(&s_acc[lane >> 4][j][k], v[k]);
                 }
             }
             if (lane == 0) s_has[w][j] = any ? 1u : 0u;
         }
         __syncthreads();
         if (tid < nb) {
-            float acc[9];
-#pragma unroll
-            for (int k = 0; k < 9; ++k) acc[k] = 0.0f;
-            bool has = false;
-#pragma unroll
-            for (int ww = 0; ww < 4; ++ww) {
-                if (!s_has[ww][tid]) continue;
-                has = true;
-#pragma unroll
-                for (int k = 0; k < 9; ++k) acc[k] += s_part[ww][tid][k];
-            }
+            const bool has = (s_has[0][tid] | s_has[1][tid] | s_has[2][tid] | s_has[3][tid]) != 0u;
             if (has) {
+                float acc[9];
+#pragma unroll
+                for (int k = 0; k < 9; ++k)
+                    acc[k] = (s_acc[0][tid][k] + s_acc[1][tid][k]) + (s_acc[2][tid][k] + s_acc[3][tid][k]);
                 const uint32_t gi = sid[start + lo + tid];
                 float* dst = bp.grad2d + 9 * (size_t)gi;
 #pragma unroll
