@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--train-steps", type=int, default=20)
     ap.add_argument("--train-n", type=int, default=1_000_000)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-morton", action="store_true",
+                    help="skip the Morton-ordered orbit with the chunk frustum skip")
     ap.add_argument("--cpu-frames", type=int, default=10)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -162,6 +164,41 @@ def copy_calibration(nbytes):
     ctx.dev_free(b)
     ctx.close()
     print(json.dumps({"copy_calibration_bytes": nbytes, "dispatches": 5}), flush=True)
+
+
+def bench_morton(scene, cov, cams, steps, warmup):
+    """The same orbit on the scene in Morton order with the chunk frustum skip
+    on (render/run.py:1011-1057 + render/host/chunk_cull.h): a secondary figure,
+    not the headline value (the headline scene is in its generated order)."""
+    from gsplat_tt_amd import _lib as L
+    from gsplat_tt_amd import prep
+
+    t = time.time()
+    a, _ = prep.morton_reorder({"means": scene.means, "cov": cov,
+                                "opacities": scene.opacities, "sh": scene.sh})
+    reorder_s = time.time() - t
+    ctx = L.Context(0, timing=False)
+    try:
+        ctx.set_chunk_cull(True)
+        ctx.set_scene(a["means"], a["cov"], a["opacities"], a["sh"], sh_degree=3)
+        H, W = cams[0].height, cams[0].width
+        outs = [ctx.dev_alloc(H * W * 3 * 2) for _ in range(FRAMES_IN_FLIGHT)]
+        views = [L.make_view(c.w2c, c.K, H, W, tile_size=16, output="bf16") for c in cams]
+        seq = [views[i % len(views)] for i in range(warmup + steps)]
+        ctx.render_batch(seq[:warmup], [outs[i % FRAMES_IN_FLIGHT] for i in range(warmup)])
+        t0 = time.perf_counter()
+        sts = ctx.render_batch(seq[warmup:], [outs[i % FRAMES_IN_FLIGHT] for i in range(steps)])
+        ctx._L.gs_sync(ctx.handle)
+        dt = time.perf_counter() - t0
+        for o in outs:
+            ctx.dev_free(o)
+    finally:
+        ctx.close()
+    nparts = (scene.n + 1023) // 1024
+    return {"frames_per_s": round(steps / dt, 1), "partitions": nparts,
+            "partitions_skipped_avg": round(float(np.mean([s["chunks_skipped"] for s in sts])), 1),
+            "num_visible_avg": round(float(np.mean([s["num_visible"] for s in sts])), 1),
+            "reorder_s": round(reorder_s, 2)}
 
 
 def bench_host_out(ctx, cams, frames):
@@ -359,6 +396,9 @@ def main():
     }
     res["host_out"] = bench_host_out(ctx, cams, min(args.steps, 64))
     log(f"host_out: {res['host_out']}")
+    if not args.no_morton:
+        res["morton_chunk_cull"] = bench_morton(scene, cov, cams, args.steps, args.warmup)
+        log(f"morton_chunk_cull: {res['morton_chunk_cull']}")
     if not args.no_sort:
         res["sort"] = bench_sort(ctx, args.sort_keys)
         log(f"sort: {res['sort']}")

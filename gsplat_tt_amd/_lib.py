@@ -30,6 +30,7 @@ EXPORTED = (
     "gs_render_batch",
     "gs_render_next",
     "gs_render_out_ring", "gs_out_release", "gs_out_ring_config", "gs_out_ring_info",
+    "gs_set_chunk_cull",
 )
 TRAIN_PARAMS = ("means", "log_scales", "quats", "opacity_logits", "sh")
 
@@ -59,7 +60,8 @@ class GsStats(ctypes.Structure):
                 ("ms_tile_sort", ctypes.c_float), ("ms_blend", ctypes.c_float),
                 ("ms_total", ctypes.c_float), ("blend_evals", ctypes.c_int64),
                 ("blend_batches", ctypes.c_int64), ("blend_iters", ctypes.c_int64),
-                ("blend_kept", ctypes.c_int64), ("blend_max_iters", ctypes.c_int64)]
+                ("blend_kept", ctypes.c_int64), ("blend_max_iters", ctypes.c_int64),
+                ("chunks_skipped", ctypes.c_int64)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
@@ -300,6 +302,10 @@ class Context:
         shape = (view.image_height, view.image_width, 3)
         return np.asarray(_LeasedImage(self._L, img, shape, _OUT_DTYPE[view.out_format])), \
             st.as_dict()
+
+    def set_chunk_cull(self, on: bool = True, k: float = 1.5):
+        """Chunk frustum skip for the frames of this context (render/host/chunk_cull.h)."""
+        _check(self._L.gs_set_chunk_cull(self._c, ctypes.c_int(1 if on else 0), ctypes.c_double(k)))
 
     def out_ring_config(self, cap: int):
         _check(self._L.gs_out_ring_config(self._c, ctypes.c_int(cap)))

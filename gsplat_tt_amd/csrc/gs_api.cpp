@@ -183,7 +183,7 @@ struct gs_ctx {
                           &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_bstart, &b_pair_tile, &b_pair_id,
                           &b_ranges, &b_out, &b_kalt, &b_valt, &b_hist, &b_state, &b_lb, &b_cnt,
                           &b_tmp_a, &b_tmp_b, &b_tmp_c, &b_evals, &b_frame, &b_phist_proj,
-                          &b_phist_emit, &b_rect_r, &b_cov_r, &b_spec})
+                          &b_phist_emit, &b_rect_r, &b_cov_r, &b_spec, &b_chunk_box, &b_skip})
             b->release();
         if (h_pin) (void)hipHostFree(h_pin);
         ring.reset();  // held images stay valid until their leases are released
@@ -268,6 +268,32 @@ struct gs_ctx {
         skey.valid = true;
         ++scene_gen;
         tkey.valid = false;
+        if (chunk_on) build_chunk_boxes();
+    }
+
+    // Chunk frustum skip (render/host/chunk_cull.h, GSPLAT_TT_CHUNK_CULL): boxes
+    // per projection partition, built once per scene; each frame flags the
+    // partitions that cannot reach the image and the projection skips them. The
+    // frame is unchanged by it; it pays off on spatially ordered scenes (Morton
+    // order), whose partitions are compact.
+    bool chunk_on = false;
+    double chunk_k = 1.5;
+    DevBuf b_chunk_box, b_skip;
+    void build_chunk_boxes() {
+        sd.chunk_box = nullptr;
+        sd.chunk_k = chunk_k;
+        if (!chunk_on || !skey.valid || sd.n <= 0) return;
+        b_chunk_box.ensure(gs::chunk_box_doubles(sd.n) * 8);
+        HIPCHK(gs::launch_chunk_boxes(sd, chunk_k, b_chunk_box.as<double>(), st));
+        sync();
+        sd.chunk_box = b_chunk_box.as<double>();
+    }
+    void set_chunk_cull(bool on, double k) {
+        REQUIRE(std::isfinite(k) && k >= 0.0, "chunk cull: k must be finite and >= 0");
+        drain_spec();
+        chunk_on = on;
+        chunk_k = k > 0.0 ? k : 1.5;
+        build_chunk_boxes();
     }
 
     void ensure_terms(const gs_view* v) {
@@ -444,7 +470,7 @@ struct gs_ctx {
     static constexpr size_t kFrTileHist = 64 + 1024;  // [2][256] tile-id digits
     static constexpr size_t kFrLb = 2048;       // look-back states (u64 each)
     enum : int {
-        C_PROJ_TICKET = 0, C_M = 1, C_RECT_TICKET = 8, C_PPRE = 9, C_EMIT_TICKET = 10, C_P = 11,
+        C_PROJ_TICKET = 0, C_M = 1, C_SKIPPED = 2, C_RECT_TICKET = 8, C_PPRE = 9, C_EMIT_TICKET = 10, C_P = 11,
         C_DSORT_TICKETS = 16, C_TSORT_TICKETS = 24
     };
     uint64_t pair_cap = 0;  // candidate-pair capacity of the frame buffers
@@ -561,6 +587,7 @@ struct gs_ctx {
             s.num_visible = h_pin[C_M];
             s.pairs_pre = h_pin[C_PPRE];
             s.num_entries = h_pin[C_P];
+            s.chunks_skipped = h_pin[C_SKIPPED];
             if (timing) {
                 s.ms_project = elapsed(0, 1);
                 s.ms_depth_sort = elapsed(1, 2);
@@ -813,6 +840,13 @@ struct gs_ctx {
         HIPCHK(gs::launch_fill_u32(L.fr, 0u, L.fwords, st));
         if (timing) HIPCHK(gs::launch_fill_u32(b_evals.as<uint32_t>(), 0u, 64 * 8 * 2, st));
         gs::ProjParams p = proj_params(v);
+        // the boxes bound three standard deviations: no skipping for wider k
+        if (sd.chunk_box != nullptr && v->k_cap <= 3.0f) {
+            b_skip.ensure(gs::project_partitions(N));
+            HIPCHK(gs::launch_chunk_cull(sd.chunk_box, N, p, sd.chunk_k, b_skip.as<uint8_t>(),
+                                         L.cnt + C_SKIPPED, st));
+            p.skip = b_skip.as<uint8_t>();
+        }
         gs::Compact c{b_rc.as<float4>(), b_dkey.as<uint32_t>(),
                       b_brec.as<float4>(), nullptr};
         HIPCHK(gs::launch_project(sd, p, c, nullptr, L.lb_proj, L.cnt + C_PROJ_TICKET,
@@ -1251,6 +1285,14 @@ int gs_render_next(gs_ctx* ctx, const gs_view* view, void* out, int out_on_devic
         REQUIRE(ctx, "null ctx");
         HIPCHK(hipSetDevice(ctx->device));
         ctx->render_next(view, out, out_on_device != 0, next_view, stats);
+    });
+}
+
+int gs_set_chunk_cull(gs_ctx* ctx, int on, double k) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->set_chunk_cull(on != 0, k);
     });
 }
 

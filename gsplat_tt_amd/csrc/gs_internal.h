@@ -25,6 +25,10 @@ struct SceneDev {
     float* kfac = nullptr;     // min(sqrt(2 ln max(op/floor,1)), k_cap)
     float* m2thr = nullptr;    // -2 ln(floor/op) or -1 (drop) [tile cull]
     float* lthr = nullptr;     // ln(mb_floor/op) or 0 (drop)  [microblock cull]
+    // chunk frustum skip: per projection partition boxes (chunk_box_doubles(n)),
+    // nullptr when off; chunk_k = the box's multiple of rho
+    const double* chunk_box = nullptr;
+    double chunk_k = 1.5;
 };
 
 struct ProjParams {
@@ -39,6 +43,9 @@ struct ProjParams {
     int has_opac;
     int sh_clamp_hi;
     int write_src;             // also write compact->source index
+    // per projection partition: nonzero = no Gaussian of it can reach the image
+    // (its loads are skipped); nullptr = no partition is skipped
+    const uint8_t* skip;
 };
 
 // Compact (visible-only) Gaussian records, index m in [0, M).
@@ -57,6 +64,14 @@ struct Compact {
 hipError_t launch_project(const SceneDev& s, const ProjParams& p, Compact out,
                           uint8_t* valid_mask, uint64_t* lb_state, uint32_t* ticket,
                           uint32_t* count_out, uint32_t* part_hist, hipStream_t st);
+// Chunk frustum skip (render/host/chunk_cull.h): per projection partition of the
+// scene, the box of mean +- k rho, rho = 3 sqrt(trace cov3d), the largest rho and
+// a non-finite flag (8 doubles per partition); per view, the partitions that lie
+// behind the near plane or beyond a padded side plane of the image.
+size_t chunk_box_doubles(int64_t n);
+hipError_t launch_chunk_boxes(const SceneDev& s, double k, double* box, hipStream_t st);
+hipError_t launch_chunk_cull(const double* box, int64_t n, const ProjParams& p, double k,
+                             uint8_t* skip, uint32_t* n_skipped, hipStream_t st);
 hipError_t launch_soa_transpose(const float* aos, int64_t n, int cols, const int* col_map,
                                 int planes, float* soa, hipStream_t st);
 size_t project_partitions(int64_t n);

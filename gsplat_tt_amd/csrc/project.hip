@@ -107,6 +107,9 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
     const uint32_t vid = s_vid;
     const int64_t base = (int64_t)vid * kProjPart;
     const int64_t n = s.n;
+    // a partition the view's frustum test rules out reads nothing: its Gaussians
+    // are all invalid (it still publishes its zero count to the compaction)
+    const bool skipped = p.skip != nullptr && p.skip[vid] != 0;
 
     float vmx[kProjItems], vmy[kProjItems], vtz[kProjItems];
     float va[kProjItems], vb[kProjItems], vc[kProjItems], vrx[kProjItems], vry[kProjItems];
@@ -118,7 +121,7 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
         const int64_t i = base + it * kProjThreads + tid;
         valid[it] = false;
         vmx[it] = vmy[it] = vtz[it] = va[it] = vb[it] = vc[it] = vrx[it] = vry[it] = 0.0f;
-        if (i < n) {
+        if (i < n && !skipped) {
             const float mx = s.mean[0][i], my = s.mean[1][i], mz = s.mean[2][i];
             const float rmx = mx * p.r[0] + my * p.r[1] + mz * p.r[2];
             const float rmy = mx * p.r[3] + my * p.r[4] + mz * p.r[5];
@@ -194,8 +197,8 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
                 vrx[it] = rx;
                 vry[it] = ry;
             }
-            if (valid_mask != nullptr) valid_mask[i] = valid[it] ? 1 : 0;
         }
+        if (i < n && valid_mask != nullptr) valid_mask[i] = valid[it] ? 1 : 0;
         bal[it] = __ballot(valid[it]);
         if (lane == 0) s_cnt[it][w] = (uint32_t)__popcll(bal[it]);
         if (part_hist != nullptr) {
@@ -276,6 +279,111 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
     }
 }
 
+// ---- chunk frustum skip ------------------------------------------------------
+// render/host/chunk_cull.h:26-58 (per scene) and :62-99 (per view), over this
+// kernel's partitions of kProjPart Gaussians; double precision throughout.
+
+// One workgroup per partition: min/max of mean -+ k rho over its Gaussians.
+__global__ __launch_bounds__(kProjThreads) void k_chunk_boxes(SceneDev s, double k,
+                                                              double* __restrict__ box) {
+    constexpr int W = kProjThreads / GS_WAVE;
+    __shared__ double s_v[7][W];
+    __shared__ int s_bad[W];
+    const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
+    const int64_t base = (int64_t)blockIdx.x * kProjPart;
+    double lo[3] = {1e300, 1e300, 1e300}, hi[3] = {-1e300, -1e300, -1e300}, rmax = 0.0;
+    bool bad = false;
+#pragma unroll
+    for (int it = 0; it < kProjItems; ++it) {
+        const int64_t i = base + it * kProjThreads + tid;
+        if (i >= s.n) continue;
+        const double tr = (double)s.cov[0][i] + (double)s.cov[3][i] + (double)s.cov[5][i];
+        if (!isfinite(tr)) bad = true;
+        const double rho = 3.0 * sqrt(tr > 0.0 ? tr : 0.0);
+        rmax = rho > rmax ? rho : rmax;
+#pragma unroll
+        for (int d = 0; d < 3; ++d) {
+            const double m = (double)s.mean[d][i];
+            if (!isfinite(m)) bad = true;
+            const double l = m - k * rho, h = m + k * rho;
+            lo[d] = l < lo[d] ? l : lo[d];
+            hi[d] = h > hi[d] ? h : hi[d];
+        }
+    }
+    for (int o = 1; o < GS_WAVE; o <<= 1) {
+#pragma unroll
+        for (int d = 0; d < 3; ++d) {
+            lo[d] = fmin(lo[d], __shfl_xor(lo[d], o, GS_WAVE));
+            hi[d] = fmax(hi[d], __shfl_xor(hi[d], o, GS_WAVE));
+        }
+        rmax = fmax(rmax, __shfl_xor(rmax, o, GS_WAVE));
+    }
+    const bool any_bad = __ballot(bad) != 0ull;
+    if (lane == 0) {
+        for (int d = 0; d < 3; ++d) {
+            s_v[d][w] = lo[d];
+            s_v[3 + d][w] = hi[d];
+        }
+        s_v[6][w] = rmax;
+        s_bad[w] = any_bad ? 1 : 0;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        double* b = box + 8 * (size_t)blockIdx.x;
+        int nb = 0;
+        for (int q = 0; q < 7; ++q) {
+            double v = s_v[q][0];
+            for (int ww = 1; ww < W; ++ww)
+                v = (q < 3) ? fmin(v, s_v[q][ww]) : fmax(v, s_v[q][ww]);
+            b[q] = v;
+        }
+        for (int ww = 0; ww < W; ++ww) nb |= s_bad[ww];
+        b[7] = nb ? 1.0 : 0.0;
+    }
+}
+
+// One thread per partition. Skipped when the box is behind z = near, or when
+// every corner lies beyond one side plane x = U0 z of the image widened by 5 px
+// and the largest rho, seen from the nearest depth, subtends less than that
+// plane's margin for k: no Gaussian's footprint can then reach the image.
+__global__ void k_chunk_cull(const double* __restrict__ box, int64_t nchunks, ProjParams p,
+                             double k, uint8_t* __restrict__ skip, uint32_t* __restrict__ n_skipped) {
+    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= nchunks) return;
+    const double* b = box + 8 * (size_t)c;
+    bool cull = false;
+    if (b[7] == 0.0) {
+        constexpr double kNear = 0.2, kPad = 5.0;
+        double pc[8][3];
+        double zmin = 1e300, zmax = -1e300;
+        for (int q = 0; q < 8; ++q) {
+            const double x = b[(q & 1) ? 3 : 0], y = b[(q & 2) ? 4 : 1], z = b[(q & 4) ? 5 : 2];
+            for (int a = 0; a < 3; ++a)
+                pc[q][a] = (double)p.r[3 * a] * x + (double)p.r[3 * a + 1] * y +
+                           (double)p.r[3 * a + 2] * z + (double)p.t[a];
+            zmin = fmin(zmin, pc[q][2]);
+            zmax = fmax(zmax, pc[q][2]);
+        }
+        cull = zmax <= kNear;
+        const double ang = b[6] / fmax(zmin, kNear);
+        const double W = (double)p.width, H = (double)p.height;
+        const double u0[4] = {(W - p.cx + kPad) / p.fx, (p.cx + kPad) / p.fx,
+                              (H - p.cy + kPad) / p.fy, (p.cy + kPad) / p.fy};
+        for (int sd = 0; sd < 4 && !cull; ++sd) {
+            const int axis = sd >> 1;
+            const double sgn = (sd & 1) ? -1.0 : 1.0, U0 = u0[sd];
+            const double uk = sqrt(fmax(0.0, k * k * (1.0 + U0 * U0) - 1.0));
+            const double margin = (uk - U0) / sqrt(1.0 + uk * uk);
+            if (ang > margin) continue;
+            bool all = true;
+            for (int q = 0; q < 8 && all; ++q) all = sgn * pc[q][axis] - U0 * pc[q][2] > 0.0;
+            cull = all;
+        }
+    }
+    skip[c] = cull ? 1 : 0;
+    if (cull && n_skipped != nullptr) atomicAdd(n_skipped, 1u);
+}
+
 struct ColMap {
     int c[64];
 };
@@ -330,6 +438,23 @@ hipError_t launch_project(const SceneDev& s, const ProjParams& p, Compact out,
 }
 
 size_t project_partitions(int64_t n) { return (size_t)((n + kProjPart - 1) / kProjPart); }
+
+size_t chunk_box_doubles(int64_t n) { return project_partitions(n) * 8; }
+
+hipError_t launch_chunk_boxes(const SceneDev& s, double k, double* box, hipStream_t st) {
+    if (s.n <= 0) return hipSuccess;
+    const unsigned grid = (unsigned)project_partitions(s.n);
+    k_chunk_boxes<<<grid, kProjThreads, 0, st>>>(s, k, box);
+    return hipGetLastError();
+}
+
+hipError_t launch_chunk_cull(const double* box, int64_t n, const ProjParams& p, double k,
+                             uint8_t* skip, uint32_t* n_skipped, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const int64_t nc = (int64_t)project_partitions(n);
+    k_chunk_cull<<<(unsigned)((nc + 255) / 256), 256, 0, st>>>(box, nc, p, k, skip, n_skipped);
+    return hipGetLastError();
+}
 
 hipError_t launch_soa_transpose(const float* aos, int64_t n, int cols, const int* col_map,
                                 int planes, float* soa, hipStream_t st) {

@@ -17,6 +17,9 @@
 // never writes it again while Python holds the image or any view of it.
 // GSPLAT_TT_OUT_ZEROCOPY=0 (or GSPLAT_TT_OUT_PINNED=0) returns a fresh array
 // instead; GSPLAT_TT_OUT_ZEROCOPY_SLOTS (default 4, at least 1) caps the ring.
+// GSPLAT_TT_CHUNK_CULL=1 turns on the chunk frustum skip with box factor
+// GSPLAT_TT_CHUNK_K (default 1.5), as render/host/pfwc_device.cpp:214-240 reads
+// them; the images are the same either way.
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 
@@ -71,6 +74,15 @@ unsigned env_uint(const char* name, unsigned dflt) {
 bool out_zerocopy() {
     return env_uint("GSPLAT_TT_OUT_ZEROCOPY", 1u) != 0u && env_uint("GSPLAT_TT_OUT_PINNED", 1u) != 0u;
 }
+double env_double(const char* name, double dflt) {
+    const char* v = std::getenv(name);
+    if (v == nullptr || *v == 0) return dflt;
+    char* end = nullptr;
+    const double x = std::strtod(v, &end);
+    return (end != nullptr && *end == 0) ? x : dflt;
+}
+bool g_chunk_on = false;
+double g_chunk_k = 1.5;
 int out_zerocopy_slots() {
     const unsigned n = env_uint("GSPLAT_TT_OUT_ZEROCOPY_SLOTS", 4u);
     return n < 1u ? 1 : (int)std::min(n, 1024u);
@@ -159,6 +171,13 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
         py::gil_scoped_release nogil;
         std::lock_guard<std::mutex> lock(g_mutex);
         gs_ctx* c = ctx_locked();
+        const bool chunk_on = env_uint("GSPLAT_TT_CHUNK_CULL", 0u) != 0u;
+        const double chunk_k = env_double("GSPLAT_TT_CHUNK_K", 1.5);
+        if (chunk_on != g_chunk_on || chunk_k != g_chunk_k) {
+            check(gs_set_chunk_cull(c, chunk_on ? 1 : 0, chunk_k));
+            g_chunk_on = chunk_on;
+            g_chunk_k = chunk_k;
+        }
         sc.version = g_scene_version;
         check(gs_scene_set(c, &sc));
         // the next view: this call's parameters at the announced pose
@@ -231,6 +250,8 @@ PYBIND11_MODULE(render_clean, m) {
         std::lock_guard<std::mutex> lock(g_mutex);
         if (g_ctx) gs_destroy(g_ctx);
         g_ctx = nullptr;
+        g_chunk_on = false;
+        g_chunk_k = 1.5;
     });
     m.def("stage_timings", []() {
         py::dict d;

@@ -80,6 +80,7 @@ typedef struct gs_stats {
     int64_t blend_iters;    /* wave apply iterations (timing on) */
     int64_t blend_kept;     /* kept (entry, microblock) pairs seen (timing on) */
     int64_t blend_max_iters; /* longest wave's apply iterations (timing on) */
+    int64_t chunks_skipped;  /* projection partitions the chunk frustum skip ruled out */
 } gs_stats;
 
 /* ---- context -------------------------------------------------------- */
@@ -115,6 +116,15 @@ int gs_render_batch(gs_ctx* ctx, const gs_view* views, int n, void* const* outs,
  * drops an announced frame. */
 int gs_render_next(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device,
                    const gs_view* next_view, gs_stats* stats);
+
+/* Chunk frustum skip (render/host/chunk_cull.h; GSPLAT_TT_CHUNK_CULL and
+ * GSPLAT_TT_CHUNK_K of render/host/pfwc_device.cpp:214-240): per scene, the box of
+ * mean +- k * 3 sqrt(trace cov3d) over each partition of 1024 consecutive
+ * Gaussians; per frame, partitions behind the near plane or beyond a side plane
+ * of the image (5 px pad) are not read. Images and counts are unchanged; it pays
+ * off when the scene is spatially ordered (Morton order, gsplat_tt_amd.prep).
+ * Off by default; k <= 0 selects 1.5. Not applied to views with k_cap > 3. */
+int gs_set_chunk_cull(gs_ctx* ctx, int on, double k);
 
 /* ---- zero-copy output ring (render/host/out_ring.h; render/host/render.cpp:
  * 334-340,598-612, GSPLAT_TT_OUT_ZEROCOPY) ------------------------------
