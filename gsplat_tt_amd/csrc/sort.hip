@@ -126,6 +126,53 @@ __global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ key
     }
 }
 
+// Per-digit decoupled look-back of partition vid (one thread per digit):
+// publishes the partition's count `agg` for the digit, walks back kLbBatch
+// predecessors per round trip (independent loads: one memory latency covers the
+// batch) until an inclusive prefix, publishes its own inclusive prefix and
+// returns the exclusive one.
+template <typename D, typename DT>
+__device__ __forceinline__ uint32_t digit_lookback(DT* state, uint32_t vid, int digit,
+                                                   uint32_t agg, uint32_t epoch) {
+    if (vid == 0) {
+        st_agent(&state[digit], D::make(epoch, 2u, agg));
+        return 0u;
+    }
+    st_agent(&state[(size_t)vid * 256 + digit], D::make(epoch, 1u, agg));
+    uint32_t excl = 0;
+    int64_t j = (int64_t)vid - 1;
+    uint32_t spins = 0;
+    bool done = false;
+    while (!done) {
+        DT sv[kLbBatch];
+#pragma unroll
+        for (int q = 0; q < kLbBatch; ++q)
+            sv[q] = (j - q >= 0) ? ld_agent(&state[(size_t)(j - q) * 256 + digit])
+                                 : D::make(epoch, 2u, 0u);
+        int used = 0;
+#pragma unroll
+        for (int q = 0; q < kLbBatch; ++q) {
+            if (done || used < q) continue;  // stop at the first gap
+            const uint32_t flag = D::flag(sv[q], epoch);
+            if (flag == 0u) continue;
+            excl += D::val(sv[q]);
+            ++used;
+            if (flag == 2u) done = true;
+        }
+        j -= used;
+        if (!done && used < kLbBatch) {
+            // bounded wait (see lookback_exclusive): never hang the GPU
+            if (++spins < kLbMaxSpins) {
+                __builtin_amdgcn_s_sleep(1);
+            } else {
+                done = true;
+            }
+        }
+    }
+    st_agent(&state[(size_t)vid * 256 + digit], D::make(epoch, 2u, excl + agg));
+    return excl;
+}
+
 // DROP: keys equal to kPairDrop are left out (not ranked, not written): the
 // pass stably compacts the kept keys while it sorts them.
 template <typename K, bool IOTA, int THREADS, int ITEMS, bool D32, bool DROP>
@@ -177,6 +224,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
             val[it] = 0;
         }
     }
+
     // Stable wave ranking: peers = lanes with the same digit (8 ballots);
     // rank = earlier items of this wave with that digit + lower peer lanes.
     const uint64_t lt = lanemask_lt();
@@ -212,44 +260,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         }
         // a digit absent from the whole pass publishes nothing and looks back at
         // nothing (all partitions agree: the histogram is global)
-        if (g_hist_pass[tid] == 0u) {
-        } else if (vid == 0) {
-            st_agent(&state[tid], D::make(epoch, 2u, tot));
-        } else {
-            st_agent(&state[(size_t)vid * 256 + tid], D::make(epoch, 1u, tot));
-            // Look back kLbBatch predecessors per round trip: the loads are
-            // independent, so one memory latency covers the whole batch.
-            int64_t j = (int64_t)vid - 1;
-            uint32_t spins = 0;
-            bool done = false;
-            while (!done) {
-                DT sv[kLbBatch];
-#pragma unroll
-                for (int q = 0; q < kLbBatch; ++q)
-                    sv[q] = (j - q >= 0) ? ld_agent(&state[(size_t)(j - q) * 256 + tid])
-                                         : D::make(epoch, 2u, 0u);
-                int used = 0;
-#pragma unroll
-                for (int q = 0; q < kLbBatch; ++q) {
-                    if (done || used < q) continue;  // stop at the first gap
-                    const uint32_t flag = D::flag(sv[q], epoch);
-                    if (flag == 0u) continue;
-                    excl += D::val(sv[q]);
-                    ++used;
-                    if (flag == 2u) done = true;
-                }
-                j -= used;
-                if (!done && used < kLbBatch) {
-                    // bounded wait (see lookback_exclusive): never hang the GPU
-                    if (++spins < kLbMaxSpins) {
-                        __builtin_amdgcn_s_sleep(1);
-                    } else {
-                        done = true;
-                    }
-                }
-            }
-            st_agent(&state[(size_t)vid * 256 + tid], D::make(epoch, 2u, excl + tot));
-        }
+        if (g_hist_pass[tid] != 0u) excl = digit_lookback<D, DT>(state, vid, tid, tot, epoch);
     }
     // Exclusive scans over the 256 digits: partition-local offsets (tot) and
     // global digit bases (histogram of this pass).
