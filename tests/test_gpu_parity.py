@@ -192,6 +192,54 @@ def test_render_edge_cases(gpu_ctx):
         gpu_ctx.render(L.make_view(cam.w2c, cam.K, 64, 80, tile_size=24))
 
 
+def test_render_degenerate_inputs(gpu_ctx):
+    """Scenes with NaN and infinite means, zero, negative and huge covariances,
+    opacities at and around the floor (0, 1/255, 1, NaN) and points on the near
+    plane: the projection matches the oracle bit for bit (validity and values),
+    and the frame's counts and image match the oracle's."""
+    scene, cam, cov = _scene(20_000, 27)
+    means = scene.means.copy()
+    cov = cov.copy()
+    op = scene.opacities.copy()
+    rng = np.random.default_rng(27)
+    idx = rng.permutation(means.shape[0])
+    groups = np.array_split(idx[:2000], 10)
+    means[groups[0], rng.integers(0, 3, groups[0].size)] = np.nan
+    means[groups[1], rng.integers(0, 3, groups[1].size)] = np.inf
+    means[groups[2], 2] = -np.inf
+    cov[groups[3]] = 0.0
+    c = cov[groups[4]].reshape(-1, 9)
+    c[:, [0, 4, 8]] *= -1.0
+    cov[groups[4]] = c.reshape(cov[groups[4]].shape)
+    cov[groups[5]] *= np.float32(1e4)
+    op[groups[6][0::4]] = 0.0
+    op[groups[6][1::4]] = np.float32(1.0 / 255.0)
+    op[groups[6][2::4]] = 1.0
+    op[groups[6][3::4]] = np.nan
+    # camera-space z exactly 0.2 (the near plane) for a group: the camera is the
+    # identity rotation plus translation in this scene's view
+    R = cam.w2c[:3, :3].astype(np.float64)
+    t = cam.w2c[:3, 3].astype(np.float64)
+    cam_pts = (means[groups[7]].astype(np.float64) @ R.T) + t
+    cam_pts[:, 2] = 0.2
+    means[groups[7]] = ((cam_pts - t) @ R).astype(np.float32)
+    view = L.make_view(cam.w2c, cam.K, cam.height, cam.width, tile_size=16, output="f32")
+    g = gpu_ctx.project(means, cov, op, scene.colors, view)
+    o = O.project(means, cov, cam.w2c, cam.K, scene.colors, op, cam.height, cam.width)
+    assert np.array_equal(g["valid"], o["valid"])
+    for k in ("means2d", "covs2d", "depths", "radii", "colors", "opacities"):
+        assert np.array_equal(_bits(g[k]), _bits(o[k])), k
+    img_o, st_o, _ = O.render_full(means, cov, op, scene.colors, cam.w2c, cam.K, cam.height,
+                                   cam.width, tile_size=16)
+    gpu_ctx.set_scene(means, cov, op, scene.colors)
+    img, st = gpu_ctx.render(view)
+    print("degenerate: M", st["num_visible"], "P", st["num_entries"], flush=True)
+    assert st["num_visible"] == st_o["num_visible"]
+    assert st["num_entries"] == st_o["num_entries"]
+    assert np.array_equal(np.isnan(img), np.isnan(img_o))
+    assert np.nanmax(np.abs(img - img_o)) <= 1e-5
+
+
 def test_sort_u64(gpu_ctx):
     rng = np.random.default_rng(7)
     for n in (0, 1, 4095, 4096, 4097, 100_003):
