@@ -387,7 +387,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": "forward render, 6M Gaussians (slab+shell), SH degree 3, "
                                "1237x822, 16x16 tiles, 64-view orbit r=4m h=1m fx=fy=1100, "
-                               "bf16 out", "global_batch": 1, "seq_len": 0,
+                               "bf16 out",
                    "parallelism": "single GPU", "n_gaussians": scene.n, "views": len(cams),
                    "frames_in_flight": FRAMES_IN_FLIGHT,
                    "stage_times": "16 frames one at a time with per-stage hipEvents"},
