@@ -194,7 +194,7 @@ def bench_morton(scene, cov, cams, steps, warmup):
             ctx.dev_free(o)
     finally:
         ctx.close()
-    nparts = (scene.n + 1023) // 1024
+    nparts = -(-scene.n // L.PROJECT_PARTITION)
     return {"frames_per_s": round(steps / dt, 1), "partitions": nparts,
             "partitions_skipped_avg": round(float(np.mean([s["chunks_skipped"] for s in sts])), 1),
             "num_visible_avg": round(float(np.mean([s["num_visible"] for s in sts])), 1),

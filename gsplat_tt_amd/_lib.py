@@ -17,6 +17,9 @@ LIB_PATH = os.path.join(HERE, "libgsplat_hip.so")
 
 GS_OK, GS_E_INVALID, GS_E_DEVICE, GS_E_CAPACITY = 0, -1, -2, -3
 OUT_FORMATS = {"u8": 0, "bf16": 1, "f32": 2}
+# Gaussians per projection partition (the unit of the visibility compaction and
+# of the chunk frustum skip; csrc/gs_internal.h kProjPartition)
+PROJECT_PARTITION = 2048
 
 EXPORTED = (
     "gs_create", "gs_destroy", "gs_last_error", "gs_set_timing", "gs_device_info",

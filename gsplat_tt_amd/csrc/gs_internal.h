@@ -155,7 +155,7 @@ hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,
                               const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
                               uint32_t* out, hipStream_t st);
 constexpr uint32_t kEmitPartition = 2048;   // candidates per emit partition
-constexpr uint32_t kProjPartition = 1024;   // Gaussians per project partition
+constexpr uint32_t kProjPartition = 2048;   // Gaussians per project partition
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t st);
 hipError_t launch_make_keys64(const uint32_t* gid, const uint32_t* tid, const float* depths,
                               uint32_t p, uint64_t* keys, hipStream_t st);

@@ -6,7 +6,7 @@
 // Jacobian, cov_cam from the 6 unique cov3d entries, cov2d + 0.3 low-pass,
 // opacity-aware radius and the image-overlap validity test. Visible
 // Gaussians are written in source order (project.cpp:710-797) with a
-// decoupled look-back over 1024-Gaussian partitions, so compact index m equals
+// decoupled look-back over 2048-Gaussian partitions, so compact index m equals
 // the reference's.
 //
 // All float expressions keep the reference's operation order and the unit is
@@ -18,7 +18,7 @@
 namespace gs {
 namespace {
 
-constexpr int kProjThreads = 256;
+constexpr int kProjThreads = 512;
 constexpr int kProjItems = 4;
 constexpr int kProjPart = kProjThreads * kProjItems;
 static_assert(kProjPart == (int)kProjPartition, "project partition size is part of the interface");

@@ -19,7 +19,7 @@
 namespace gs {
 namespace {
 
-constexpr int kTThreads = 256;
+constexpr int kTThreads = 512;
 constexpr int kTItems = 4;
 constexpr int kTPart = kTThreads * kTItems;
 static_assert(kTPart == (int)kProjPartition, "projection partition size");

@@ -119,7 +119,7 @@ int gs_render_next(gs_ctx* ctx, const gs_view* view, void* out, int out_on_devic
 
 /* Chunk frustum skip (render/host/chunk_cull.h; GSPLAT_TT_CHUNK_CULL and
  * GSPLAT_TT_CHUNK_K of render/host/pfwc_device.cpp:214-240): per scene, the box of
- * mean +- k * 3 sqrt(trace cov3d) over each partition of 1024 consecutive
+ * mean +- k * 3 sqrt(trace cov3d) over each partition of 2048 consecutive
  * Gaussians; per frame, partitions behind the near plane or beyond a side plane
  * of the image (5 px pad) are not read. Images and counts are unchanged; it pays
  * off when the scene is spatially ordered (Morton order, gsplat_tt_amd.prep).

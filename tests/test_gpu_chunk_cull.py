@@ -94,7 +94,7 @@ def test_chunk_cull_random_order_and_kcap(morton_scene):
         _, st_k = ctx.render(vk)
         ctx.set_chunk_cull(False)
         _, st_off = ctx.render(vk)
-        nparts = (a["means"].shape[0] + 1023) // 1024
+        nparts = -(-a["means"].shape[0] // L.PROJECT_PARTITION)
         assert st_on["chunks_skipped"] >= 0.9 * nparts  # the cloud is behind this camera
         assert st_on["num_visible"] == st_off["num_visible"]
         assert st_k["chunks_skipped"] == 0
