@@ -2,7 +2,7 @@
 //
 // One upsweep pass builds the digit histograms of every pass at once; each
 // digit pass is then a single kernel (Adinets & Merrill, "Onesweep", 2022):
-//   * a 5120 (u64 keys) or 7168 (u32 keys) key partition per 1024-thread
+//   * a 5120 (u64 keys) or 8192 (u32 keys) key partition per 1024-thread
 //     workgroup, partitions taken in order from an atomic ticket so look-back
 //     only waits on resident predecessors;
 //   * wave64 stable ranking with 8 ballots per key (peer mask of equal digits)
@@ -188,7 +188,12 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     constexpr int PART = THREADS * ITEMS;
     static_assert(THREADS >= 256, "one thread per digit");
     __shared__ uint32_t s_vid, s_count;
-    __shared__ uint32_t s_wcnt[WAVES][256];
+    // per-wave digit counts and their prefixes are below PART <= 65535: 16-bit
+    // counters halve this table, which leaves room for 8192 u32 keys per
+    // partition at two workgroups per CU
+    static_assert(PART <= 65535, "16-bit wave counters");
+    using WC = uint16_t;
+    __shared__ WC s_wcnt[WAVES][256];
     __shared__ uint32_t s_loff[256];
     __shared__ uint32_t s_gpos[256];
     __shared__ uint32_t s_tmp[2][4];
@@ -243,7 +248,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
             const uint32_t before = s_wcnt[w][d];
             rank[it] = before + (uint32_t)__popcll(peers & lt);
             const int leader = __ffsll((unsigned long long)peers) - 1;
-            if (lane == leader) s_wcnt[w][d] = before + (uint32_t)__popcll(peers);
+            if (lane == leader) s_wcnt[w][d] = (WC)(before + (uint32_t)__popcll(peers));
         }
     }
     __syncthreads();
@@ -255,7 +260,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
 #pragma unroll
         for (int ww = 0; ww < WAVES; ++ww) {
             const uint32_t c = s_wcnt[ww][tid];
-            s_wcnt[ww][tid] = tot;
+            s_wcnt[ww][tid] = (WC)tot;
             tot += c;
         }
         // a digit absent from the whole pass publishes nothing and looks back at
@@ -316,7 +321,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
 // counters must leave room for two workgroups per CU).
 #ifndef GS_SWEEP_T32
 #define GS_SWEEP_T32 1024
-#define GS_SWEEP_I32 7
+#define GS_SWEEP_I32 8
 #endif
 #ifndef GS_SWEEP_T64
 #define GS_SWEEP_T64 1024
