@@ -50,6 +50,9 @@ def parse():
                     help="skip the Morton-ordered orbit with the chunk frustum skip")
     ap.add_argument("--cpu-frames", type=int, default=10)
     ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--sequential-frames", type=int, default=0, metavar="K",
+                    help="only render K orbit views one at a time (device output, no frames "
+                         "in flight): the per-kernel split of a frame under a kernel trace")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run device-to-device copies of BYTES (PMC byte-counter scale)")
     return ap.parse_args()
@@ -199,6 +202,28 @@ def bench_morton(scene, cov, cams, steps, warmup):
             "partitions_skipped_avg": round(float(np.mean([s["chunks_skipped"] for s in sts])), 1),
             "num_visible_avg": round(float(np.mean([s["num_visible"] for s in sts])), 1),
             "reorder_s": round(reorder_s, 2)}
+
+
+def sequential_frames(args):
+    """Config 3's orbit views rendered one at a time (gs_render, device output),
+    nothing else: what a kernel trace splits into per-kernel frame times."""
+    from gsplat_tt_amd import _lib as L
+    from gsplat_tt_amd import scenes
+
+    scene, cams = scenes.config3(n=args.n, views=args.views)
+    cov = scenes.cov3d(scene.scales, scene.quats)
+    ctx = L.Context(0, timing=True)
+    ctx.set_scene(scene.means, cov, scene.opacities, scene.sh, sh_degree=3)
+    H, W = cams[0].height, cams[0].width
+    out = ctx.dev_alloc(H * W * 6)
+    sts = [ctx.render_dev(L.make_view(c.w2c, c.K, H, W, tile_size=16, output="bf16"), out)
+           for c in (cams[i % len(cams)] for i in range(args.sequential_frames))]
+    ctx.dev_free(out)
+    ctx.close()
+    keys = ("ms_project", "ms_depth_sort", "ms_tile_assign", "ms_tile_sort", "ms_blend")
+    print(json.dumps({"sequential_frames": len(sts),
+                      "ms": {k[3:]: round(float(np.mean([s[k] for s in sts[4:]])), 4) for k in keys}}),
+          flush=True)
 
 
 def bench_host_out(ctx, cams, frames):
@@ -364,6 +389,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.sequential_frames:
+        sequential_frames(args)
         return
     ctx, scene, cov, cams, stats, dt = bench_frames(args)
     st, avg, blend_flops = stage_summary(scene, stats)
