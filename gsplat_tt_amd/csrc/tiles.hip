@@ -31,6 +31,7 @@ constexpr int kEmitItems = 8;
 constexpr int kEmitPart = kThreads * kEmitItems;     // candidates per emit partition
 constexpr int kRankCache = 384;
 static_assert(kEmitPart == (int)kEmitPartition, "emit partition size is part of the interface");
+static_assert(kEmitPart + 1 <= 65535, "a partition's ranks are held as 16-bit indices");
 
 __device__ __forceinline__ float fmin_std(float a, float b) { return (b < a) ? b : a; }
 __device__ __forceinline__ float fmax_std(float a, float b) { return (a < b) ? b : a; }
@@ -220,10 +221,9 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     uint32_t* __restrict__ part_hist) {
     __shared__ uint32_t s_vid;
     __shared__ uint32_t s_off[kEmitPart + 1];
-    __shared__ uint32_t s_g[kEmitPart + 1];
     __shared__ uint32_t s_xy[kEmitPart + 1];
     __shared__ uint32_t s_w[kEmitPart + 1];
-    __shared__ uint32_t s_own[kEmitPart];
+    __shared__ uint16_t s_own[kEmitPart];  // rank heads, then each slot's rank (nr <= 2049)
     // centre and conic of the first kRankCache ranks (the usual partition has
     // ~10x fewer ranks than candidates; larger ones read them from memory)
     __shared__ float2 s_pc[kRankCache];
@@ -253,7 +253,6 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     const int64_t nr = min(rend - rlo, (int64_t)kEmitPart + 1);
     for (int64_t k = tid; k < nr; k += kThreads) {
         const int64_t r = rlo + k;
-        const uint32_t g = order ? order[r] : (uint32_t)r;
         const float4 rr = rect_r[r];
         const Rect q = tile_rect(rr, tp);
         const uint32_t o = offs[r];
@@ -262,10 +261,9 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
             if (tp.cull) s_cv[k] = cov_r[r];
         }
         s_off[k] = o;
-        s_g[k] = g;
         s_xy[k] = (uint32_t)q.x0 | ((uint32_t)q.y0 << 16);
         s_w[k] = (uint32_t)(q.x1 - q.x0 + 1);
-        if (o > c0 && o < c1) s_own[o - c0] = (uint32_t)k;  // rank head
+        if (o > c0 && o < c1) s_own[o - c0] = (uint16_t)k;  // rank head
     }
     __syncthreads();
     // inclusive max-scan of the heads: 8 consecutive slots per thread
@@ -289,7 +287,7 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
         __syncthreads();
         for (int ww = 0; ww < w; ++ww) pre = max(pre, s_wmax[ww]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s_own[tid * 8 + i] = max(pre, v[i]);
+        for (int i = 0; i < 8; ++i) s_own[tid * 8 + i] = (uint16_t)max(pre, v[i]);
     }
     __syncthreads();
 
@@ -308,7 +306,9 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
         off[it] = s_off[lo[it]];
         wdt[it] = s_w[lo[it]];
         xy[it] = s_xy[lo[it]];
-        gid[it] = s_g[lo[it]];
+        // the Gaussian id from the rank order itself (an L2-resident read; a
+        // table of it in LDS would cost a quarter of the workgroup's LDS)
+        gid[it] = order ? order[rlo + lo[it]] : (uint32_t)(rlo + lo[it]);
     }
 #pragma unroll
     for (int it = 0; it < kEmitItems; ++it) {
