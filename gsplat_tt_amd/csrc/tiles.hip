@@ -27,8 +27,10 @@ constexpr int kCountThreads = 512;
 constexpr int kCountWaves = kCountThreads / GS_WAVE;
 constexpr int kCountItems = 4;
 constexpr int kCountPart = kCountThreads * kCountItems;  // ranks per scan partition
-constexpr int kEmitItems = 8;
-constexpr int kEmitPart = kThreads * kEmitItems;     // candidates per emit partition
+constexpr int kEmitThreads = 512;                    // workgroup of the pair emission
+constexpr int kEmitWaves = kEmitThreads / GS_WAVE;
+constexpr int kEmitPart = 2048;                      // candidates per emit partition
+constexpr int kEmitItems = kEmitPart / kEmitThreads;
 constexpr int kRankCache = 384;
 static_assert(kEmitPart == (int)kEmitPartition, "emit partition size is part of the interface");
 static_assert(kEmitPart + 1 <= 65535, "a partition's ranks are held as 16-bit indices");
@@ -211,7 +213,7 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
 // kept count is added to *total_out: the tile sort's first pass drops the
 // culled slots, so no partition waits on another here.
 template <bool COMPACT>
-__global__ __launch_bounds__(kThreads) void k_pair_emit(
+__global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     const float4* __restrict__ rect_r, const float4* __restrict__ cov_r,
     const uint32_t* __restrict__ order, const uint32_t* __restrict__ offs,
     const uint32_t* __restrict__ bstart, int64_t m_cap, const uint32_t* __restrict__ m_dev,
@@ -228,17 +230,15 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     // ~10x fewer ranks than candidates; larger ones read them from memory)
     __shared__ float2 s_pc[kRankCache];
     __shared__ float4 s_cv[kRankCache];
-    __shared__ uint32_t s_wmax[kWaves];
-    __shared__ uint32_t s_cnt[kEmitItems][kWaves];
+    __shared__ uint32_t s_wmax[kEmitWaves];
+    __shared__ uint32_t s_cnt[kEmitItems][kEmitWaves];
     __shared__ uint32_t s_th[2][256];
     __shared__ uint64_t s_excl;
     const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
     if (COMPACT && tid == 0) s_vid = atomicAdd(ticket, 1u);
-    for (int i = tid; i < kEmitPart; i += kThreads) s_own[i] = 0;
-    if (part_hist != nullptr) {
-        s_th[0][tid] = 0;
-        s_th[1][tid] = 0;
-    }
+    for (int i = tid; i < kEmitPart; i += kEmitThreads) s_own[i] = 0;
+    if (part_hist != nullptr)
+        for (int i = tid; i < 512; i += kEmitThreads) (&s_th[0][0])[i] = 0;
     __syncthreads();
     const uint32_t vid = COMPACT ? s_vid : blockIdx.x;
     const int64_t m = m_dev ? min(m_cap, (int64_t)*m_dev) : m_cap;
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     const int64_t rend = (c1 < (uint64_t)p_pre) ? (int64_t)bstart[vid + 1] + 1 : m;
     // every rank owns >= 1 candidate, so nr <= kEmitPart + 1; clamp defensively
     const int64_t nr = min(rend - rlo, (int64_t)kEmitPart + 1);
-    for (int64_t k = tid; k < nr; k += kThreads) {
+    for (int64_t k = tid; k < nr; k += kEmitThreads) {
         const int64_t r = rlo + k;
         const float4 rr = rect_r[r];
         const Rect q = tile_rect(rr, tp);
@@ -266,13 +266,13 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
         if (o > c0 && o < c1) s_own[o - c0] = (uint16_t)k;  // rank head
     }
     __syncthreads();
-    // inclusive max-scan of the heads: 8 consecutive slots per thread
+    // inclusive max-scan of the heads: kEmitItems consecutive slots per thread
     {
-        uint32_t v[8];
+        uint32_t v[kEmitItems];
         uint32_t run = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            run = max(run, s_own[tid * 8 + i]);
+        for (int i = 0; i < kEmitItems; ++i) {
+            run = max(run, (uint32_t)s_own[tid * kEmitItems + i]);
             v[i] = run;
         }
         uint32_t inc = run;
@@ -287,20 +287,20 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
         __syncthreads();
         for (int ww = 0; ww < w; ++ww) pre = max(pre, s_wmax[ww]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s_own[tid * 8 + i] = (uint16_t)max(pre, v[i]);
+        for (int i = 0; i < kEmitItems; ++i) s_own[tid * kEmitItems + i] = (uint16_t)max(pre, v[i]);
     }
     __syncthreads();
 
     // Every slot of s_own holds a rank in [0, nr), also past c1, so all LDS
     // reads below are issued unconditionally, item by item in stages, and the
-    // eight evaluations overlap instead of waiting on each other.
+    // evaluations overlap instead of waiting on each other.
     bool keep[kEmitItems];
     uint32_t tile[kEmitItems], gid[kEmitItems];
     uint64_t bal[kEmitItems];
     uint32_t lo[kEmitItems], off[kEmitItems], wdt[kEmitItems], xy[kEmitItems];
     int tx[kEmitItems], ty[kEmitItems];
 #pragma unroll
-    for (int it = 0; it < kEmitItems; ++it) lo[it] = s_own[it * kThreads + tid];
+    for (int it = 0; it < kEmitItems; ++it) lo[it] = s_own[it * kEmitThreads + tid];
 #pragma unroll
     for (int it = 0; it < kEmitItems; ++it) {
         off[it] = s_off[lo[it]];
@@ -312,7 +312,7 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     }
 #pragma unroll
     for (int it = 0; it < kEmitItems; ++it) {
-        const uint64_t c = c0 + it * kThreads + tid;
+        const uint64_t c = c0 + it * kEmitThreads + tid;
         uint32_t row, col;
         divmod_small((uint32_t)c - off[it], wdt[it], row, col);
         ty[it] = (int)((xy[it] >> 16) + row);
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
         }
     }
     // bookkeeping after all candidates are evaluated, so the evaluations of the
-    // eight candidates can overlap
+    // candidates of one thread can overlap
 #pragma unroll
     for (int it = 0; it < kEmitItems; ++it) {
         bal[it] = __ballot(keep[it]);
@@ -360,13 +360,13 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
     }
     __syncthreads();
     if (part_hist != nullptr) {
-        part_hist[(size_t)vid * 512 + tid] = s_th[0][tid];
-        part_hist[(size_t)vid * 512 + 256 + tid] = s_th[1][tid];
+        for (int i = tid; i < 512; i += kEmitThreads)
+            part_hist[(size_t)vid * 512 + i] = (&s_th[0][0])[i];
     }
     if (!COMPACT) {
 #pragma unroll
         for (int it = 0; it < kEmitItems; ++it) {
-            const uint64_t c = c0 + it * kThreads + tid;
+            const uint64_t c = c0 + it * kEmitThreads + tid;
             if (c < c1 && c < cap) {
                 pair_tile[c] = keep[it] ? tile[it] : kPairDrop;
                 if (keep[it]) pair_id[c] = gid[it];
@@ -377,7 +377,7 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
 #pragma unroll
             for (int it = 0; it < kEmitItems; ++it)
 #pragma unroll
-                for (int ww = 0; ww < kWaves; ++ww) kept += s_cnt[it][ww];
+                for (int ww = 0; ww < kEmitWaves; ++ww) kept += s_cnt[it][ww];
             if (kept) atomicAdd(total_out, kept);
         }
         return;
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(kThreads) void k_pair_emit(
 #pragma unroll
     for (int it = 0; it < kEmitItems; ++it)
 #pragma unroll
-        for (int ww = 0; ww < kWaves; ++ww) {
+        for (int ww = 0; ww < kEmitWaves; ++ww) {
             if (ww == w) my_off[it] = total;
             total += s_cnt[it][ww];
         }
@@ -575,11 +575,11 @@ hipError_t launch_pair_emit(const float4* rect_r, const float4* cov_r, const uin
     if (p_pre == 0 || m <= 0) return hipSuccess;
     const unsigned grid = (unsigned)emit_partitions(p_pre);
     if (compact)
-        k_pair_emit<true><<<grid, kThreads, 0, st>>>(rect_r, cov_r, order, offs, bstart, m, m_dev,
+        k_pair_emit<true><<<grid, kEmitThreads, 0, st>>>(rect_r, cov_r, order, offs, bstart, m, m_dev,
                                                      p_pre, p_pre_dev, tp, pair_tile, pair_id,
                                                      cap, lb_state, ticket, total_out, part_hist);
     else
-        k_pair_emit<false><<<grid, kThreads, 0, st>>>(rect_r, cov_r, order, offs, bstart, m,
+        k_pair_emit<false><<<grid, kEmitThreads, 0, st>>>(rect_r, cov_r, order, offs, bstart, m,
                                                       m_dev, p_pre, p_pre_dev, tp, pair_tile,
                                                       pair_id, cap, lb_state, ticket, total_out,
                                                       part_hist);
