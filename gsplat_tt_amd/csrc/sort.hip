@@ -126,19 +126,23 @@ __global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ key
     }
 }
 
-// Per-digit decoupled look-back of partition vid (one thread per digit):
-// publishes the partition's count `agg` for the digit, walks back kLbBatch
-// predecessors per round trip (independent loads: one memory latency covers the
-// batch) until an inclusive prefix, publishes its own inclusive prefix and
-// returns the exclusive one.
+// Per-digit decoupled look-back of partition vid (one thread per digit), in two
+// steps so that the partition's local work runs between them:
+// digit_publish makes the partition's count `agg` for the digit visible
+// (already inclusive for the first partition); digit_walk then walks back
+// kLbBatch predecessors per round trip (independent loads: one memory latency
+// covers the batch) until an inclusive prefix, publishes its own inclusive
+// prefix and returns the exclusive one.
 template <typename D, typename DT>
-__device__ __forceinline__ uint32_t digit_lookback(DT* state, uint32_t vid, int digit,
-                                                   uint32_t agg, uint32_t epoch) {
-    if (vid == 0) {
-        st_agent(&state[digit], D::make(epoch, 2u, agg));
-        return 0u;
-    }
-    st_agent(&state[(size_t)vid * 256 + digit], D::make(epoch, 1u, agg));
+__device__ __forceinline__ void digit_publish(DT* state, uint32_t vid, int digit, uint32_t agg,
+                                              uint32_t epoch) {
+    st_agent(&state[(size_t)vid * 256 + digit], D::make(epoch, vid == 0 ? 2u : 1u, agg));
+}
+
+template <typename D, typename DT>
+__device__ __forceinline__ uint32_t digit_walk(DT* state, uint32_t vid, int digit, uint32_t agg,
+                                               uint32_t epoch) {
+    if (vid == 0) return 0u;
     uint32_t excl = 0;
     int64_t j = (int64_t)vid - 1;
     uint32_t spins = 0;
@@ -257,9 +261,12 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     }
     __syncthreads();
 
-    // Threads 0..255 own one digit each: per-wave exclusive offsets, digit
-    // total of this partition, decoupled look-back over earlier partitions.
-    uint32_t tot = 0, excl = 0;
+    // Threads 0..255 own one digit each: per-wave exclusive offsets and the
+    // digit total of this partition, published at once for later partitions.
+    // A digit absent from the whole pass publishes nothing and looks back at
+    // nothing (all partitions agree: the histogram is global).
+    uint32_t tot = 0;
+    const bool has_digit = tid < 256 && g_hist_pass[tid] != 0u;
     if (tid < 256) {
 #pragma unroll
         for (int ww = 0; ww < WAVES; ++ww) {
@@ -267,9 +274,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
             s_wcnt[ww][tid] = (WC)tot;
             tot += c;
         }
-        // a digit absent from the whole pass publishes nothing and looks back at
-        // nothing (all partitions agree: the histogram is global)
-        if (g_hist_pass[tid] != 0u) excl = digit_lookback<D, DT>(state, vid, tid, tot, epoch);
+        if (has_digit) digit_publish<D, DT>(state, vid, tid, tot, epoch);
     }
     // Exclusive scans over the 256 digits: partition-local offsets (tot) and
     // global digit bases (histogram of this pass).
@@ -282,19 +287,21 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         s_tmp[1][w] = i2;
     }
     __syncthreads();
+    uint32_t loff = 0, gbase = 0;
     if (tid < 256) {
         uint32_t p1 = 0, p2 = 0;
         for (int ww = 0; ww < w; ++ww) {
             p1 += s_tmp[0][ww];
             p2 += s_tmp[1][ww];
         }
-        const uint32_t loff = p1 + i1 - v1;
+        loff = p1 + i1 - v1;
+        gbase = p2 + i2 - v2;
         s_loff[tid] = loff;
         if (tid == 255) s_count = p1 + i1;  // keys of this partition (kept ones)
-        s_gpos[tid] = (p2 + i2 - v2) + excl - loff;
     }
     __syncthreads();
 
+    // keys re-ordered by digit in LDS while predecessors publish their prefixes
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
         const int64_t idx = wave_base + it * GS_WAVE + lane;
@@ -306,6 +313,10 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
                 if (!SPLIT) s_vals[lp] = val[it];
             }
         }
+    }
+    if (tid < 256) {
+        const uint32_t excl = has_digit ? digit_walk<D, DT>(state, vid, tid, tot, epoch) : 0u;
+        s_gpos[tid] = gbase + excl - loff;
     }
     __syncthreads();
     const int64_t cnt64 = n - part_base;
