@@ -457,7 +457,8 @@ struct gs_ctx {
                                     b_bstart.as<uint32_t>(), m, nullptr, p_pre, nullptr, tp,
                                     b_pair_tile.as<uint32_t>(), b_pair_id.as<uint32_t>(), p_pre,
                                     b_lb.as<uint64_t>(), b_cnt.as<uint32_t>() + 10,
-                                    b_cnt.as<uint32_t>() + 11, nullptr, true, st));
+                                    b_cnt.as<uint32_t>() + 11, nullptr,
+                                    tile_bits((int64_t)tp.tiles_x * tp.tiles_y), true, st));
         HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
         sync();
         return h_pin[11];
@@ -467,8 +468,8 @@ struct gs_ctx {
     // Frame-scratch layout (u32 words): counters, histograms, look-back states.
     static constexpr size_t kFrCnt = 0;         // 64 counters (below)
     static constexpr size_t kFrDepthHist = 64;  // [4][256] depth-key digits
-    static constexpr size_t kFrTileHist = 64 + 1024;  // [2][256] tile-id digits
-    static constexpr size_t kFrLb = 2048;       // look-back states (u64 each)
+    static constexpr size_t kFrTileHist = 64 + 1024;  // [2 or 4][256] tile-id digits
+    static constexpr size_t kFrLb = 64 + 1024 + 1024;  // look-back states (u64 each)
     enum : int {
         C_PROJ_TICKET = 0, C_M = 1, C_SKIPPED = 2, C_RECT_TICKET = 8, C_PPRE = 9, C_EMIT_TICKET = 10, C_P = 11,
         C_DSORT_TICKETS = 16, C_TSORT_TICKETS = 24
@@ -776,7 +777,7 @@ struct gs_ctx {
         b_pair_id.ensure((size_t)L.pcap * 4);
         b_ranges.ensure((size_t)T * 8);
         b_phist_proj.ensure(L.pparts * 1024 * 4);
-        b_phist_emit.ensure(L.eparts * 512 * 4);
+        b_phist_emit.ensure(L.eparts * gs::tile_hist_cols(tile_bits(T)) * 4);
         L.fwords = kFrLb + 2 * (L.pparts + L.rparts + L.eparts);
         b_frame.ensure(L.fwords * 4);
         ensure_sort(std::max<int64_t>(N, L.pcap), 4);
@@ -813,8 +814,9 @@ struct gs_ctx {
                                     L.pcap, cnt + C_PPRE, tp, b_pair_tile.as<uint32_t>(),
                                     b_pair_id.as<uint32_t>(), L.pcap, L.lb_emit,
                                     cnt + C_EMIT_TICKET, cnt + C_P, b_phist_emit.as<uint32_t>(),
-                                    false, st));
-        HIPCHK(gs::launch_reduce_rows(b_phist_emit.as<uint32_t>(), 512, (uint32_t)L.eparts,
+                                    tile_bits(T), false, st));
+        HIPCHK(gs::launch_reduce_rows(b_phist_emit.as<uint32_t>(),
+                                      gs::tile_hist_cols(tile_bits(T)), (uint32_t)L.eparts,
                                       cnt + C_PPRE, L.pcap, gs::kEmitPartition, fr + kFrTileHist,
                                       st));
         record(3);

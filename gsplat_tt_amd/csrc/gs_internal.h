@@ -134,16 +134,28 @@ hipError_t launch_rect_count_scan(const float4* rect, const float4* cov, int str
                                   uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
                                   uint32_t* ticket, uint32_t* total_out, float4* rect_r,
                                   float4* cov_r, hipStream_t st);
+// Digit width of a device sort over `bits` key bits: the fewest 8-bit-or-less
+// passes, with the bits spread evenly over them (12 tile bits: two passes of 6,
+// whose 64 digits give longer runs per digit than 256 would).
+inline int sort_digit_width(int bits) {
+    const int passes = (bits + 7) / 8;
+    return passes > 0 ? (bits + passes - 1) / passes : 8;
+}
+// Tile-id digit histograms that the pair emission produces: two for up to 16
+// tile bits (rows of 512 words), three above (rows of 1024 words, the last 256
+// zero).
+inline int tile_hist_cols(int tile_bits) { return tile_bits > 16 ? 1024 : 512; }
 // rect_r / cov_r are indexed by rank (rect[order[r]], ...; the plain arrays
 // when order is null); pair ids are order[r]. part_hist (optional):
-// per-partition digit histograms [emit_partitions][2][256] of the kept pairs'
-// tile ids (bits 0-7, 8-15).
+// per-partition digit histograms of the kept pairs' tile ids, one row of
+// tile_hist_cols(tile_bits) words per emit partition: 256 words per digit of
+// sort_digit_width(tile_bits) bits, lowest digit first.
 hipError_t launch_pair_emit(const float4* rect_r, const float4* cov_r, const uint32_t* order,
                             const uint32_t* offs, const uint32_t* bstart, int64_t m,
                             const uint32_t* m_dev, uint32_t p_pre, const uint32_t* p_pre_dev,
                             TileParams tp, uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
                             uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
-                            uint32_t* part_hist, bool compact, hipStream_t st);
+                            uint32_t* part_hist, int tile_bits, bool compact, hipStream_t st);
 hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, const uint32_t* p_dev,
                               uint32_t* ranges, int64_t num_tiles, hipStream_t st);
 // Same ranges by per-tile binary search over the sorted tile keys (reads

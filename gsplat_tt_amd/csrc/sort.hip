@@ -489,7 +489,9 @@ hipError_t sort_impl(K* keys, uint32_t* vals, int64_t n, int begin_bit, int end_
 }
 
 // Every pass runs (no trivial-pass skipping: the host does not see the
-// histogram); n is min(n_cap, *n_dev), read on the device.
+// histogram); n is min(n_cap, *n_dev), read on the device. The key bits are
+// spread evenly over the passes (sort_digit_width), and `hist` holds 256 words
+// per pass for digits of that width.
 template <typename K>
 hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t* n_dev,
                          int begin_bit, int end_bit, const uint32_t* hist, uint32_t* tickets,
@@ -505,9 +507,10 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
     uint32_t* vin = vals;
     K* kalt = static_cast<K*>(tmp.keys_alt);
     uint32_t* valt = tmp.vals_alt;
+    const int dw = sort_digit_width(end_bit - begin_bit);
     for (int p = 0; p < npass; ++p) {
-        const int shift = begin_bit + 8 * p;
-        const int bits = std::min(8, end_bit - shift);
+        const int shift = begin_bit + dw * p;
+        const int bits = std::min(dw, end_bit - shift);
         const bool drop = p == 0 && n_kept_dev != nullptr;
         const uint32_t* cnt = (p > 0 && n_kept_dev != nullptr) ? n_kept_dev : n_dev;
         hipError_t e = launch_pass<K>(p == 0 && vals_iota, kin, vin, kalt, valt, n_cap, cnt,

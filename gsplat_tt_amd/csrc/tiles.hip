@@ -212,7 +212,8 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
 // pair or kPairDrop for a culled one (the pair id only for kept ones), and the
 // kept count is added to *total_out: the tile sort's first pass drops the
 // culled slots, so no partition waits on another here.
-template <bool COMPACT>
+// NDIG: tile-id digit histograms made (2, or 3 above 16 tile bits).
+template <bool COMPACT, int NDIG>
 __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     const float4* __restrict__ rect_r, const float4* __restrict__ cov_r,
     const uint32_t* __restrict__ order, const uint32_t* __restrict__ offs,
@@ -220,7 +221,8 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     uint32_t p_pre_cap, const uint32_t* __restrict__ p_pre_dev, TileParams tp,
     uint32_t* __restrict__ pair_tile, uint32_t* __restrict__ pair_id, uint32_t cap,
     uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
-    uint32_t* __restrict__ part_hist) {
+    uint32_t* __restrict__ part_hist, int dig_bits) {
+    constexpr int kHistCols = NDIG == 2 ? 512 : 1024;  // tile_hist_cols
     __shared__ uint32_t s_vid;
     __shared__ uint32_t s_off[kEmitPart + 1];
     __shared__ uint32_t s_xy[kEmitPart + 1];
@@ -232,13 +234,13 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     __shared__ float4 s_cv[kRankCache];
     __shared__ uint32_t s_wmax[kEmitWaves];
     __shared__ uint32_t s_cnt[kEmitItems][kEmitWaves];
-    __shared__ uint32_t s_th[2][256];
+    __shared__ uint32_t s_th[NDIG][256];
     __shared__ uint64_t s_excl;
     const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
     if (COMPACT && tid == 0) s_vid = atomicAdd(ticket, 1u);
     for (int i = tid; i < kEmitPart; i += kEmitThreads) s_own[i] = 0;
     if (part_hist != nullptr)
-        for (int i = tid; i < 512; i += kEmitThreads) (&s_th[0][0])[i] = 0;
+        for (int i = tid; i < NDIG * 256; i += kEmitThreads) (&s_th[0][0])[i] = 0;
     __syncthreads();
     const uint32_t vid = COMPACT ? s_vid : blockIdx.x;
     const int64_t m = m_dev ? min(m_cap, (int64_t)*m_dev) : m_cap;
@@ -354,14 +356,16 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
         if (lane == 0) s_cnt[it][w] = (uint32_t)__popcll(bal[it]);
         if (part_hist != nullptr) {
             // digit histograms of the tile keys, for the tile sort's passes
-            hist_add_wave(s_th[0], tile[it] & 255u, keep[it]);
-            hist_add_wave(s_th[1], (tile[it] >> 8) & 255u, keep[it]);
+            const uint32_t dm = (1u << dig_bits) - 1u;
+#pragma unroll
+            for (int q = 0; q < NDIG; ++q)
+                hist_add_wave(s_th[q], (tile[it] >> (q * dig_bits)) & dm, keep[it]);
         }
     }
     __syncthreads();
     if (part_hist != nullptr) {
-        for (int i = tid; i < 512; i += kEmitThreads)
-            part_hist[(size_t)vid * 512 + i] = (&s_th[0][0])[i];
+        for (int i = tid; i < kHistCols; i += kEmitThreads)
+            part_hist[(size_t)vid * kHistCols + i] = i < NDIG * 256 ? (&s_th[0][0])[i] : 0u;
     }
     if (!COMPACT) {
 #pragma unroll
@@ -571,18 +575,23 @@ hipError_t launch_pair_emit(const float4* rect_r, const float4* cov_r, const uin
                             const uint32_t* m_dev, uint32_t p_pre, const uint32_t* p_pre_dev,
                             TileParams tp, uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
                             uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
-                            uint32_t* part_hist, bool compact, hipStream_t st) {
+                            uint32_t* part_hist, int tile_bits, bool compact, hipStream_t st) {
     if (p_pre == 0 || m <= 0) return hipSuccess;
     const unsigned grid = (unsigned)emit_partitions(p_pre);
-    if (compact)
-        k_pair_emit<true><<<grid, kEmitThreads, 0, st>>>(rect_r, cov_r, order, offs, bstart, m, m_dev,
-                                                     p_pre, p_pre_dev, tp, pair_tile, pair_id,
-                                                     cap, lb_state, ticket, total_out, part_hist);
-    else
-        k_pair_emit<false><<<grid, kEmitThreads, 0, st>>>(rect_r, cov_r, order, offs, bstart, m,
-                                                      m_dev, p_pre, p_pre_dev, tp, pair_tile,
-                                                      pair_id, cap, lb_state, ticket, total_out,
-                                                      part_hist);
+    // at most three digits of at most 8 bits (tile ids below 2^24)
+    if (tile_bits < 1 || tile_bits > 24) return hipErrorInvalidValue;
+    const int dbits = sort_digit_width(tile_bits);
+    const bool three = tile_hist_cols(tile_bits) > 512;
+#define GS_EMIT(CP, ND)                                                                    \
+    k_pair_emit<CP, ND><<<grid, kEmitThreads, 0, st>>>(                                    \
+        rect_r, cov_r, order, offs, bstart, m, m_dev, p_pre, p_pre_dev, tp, pair_tile, pair_id, \
+        cap, lb_state, ticket, total_out, part_hist, dbits)
+    if (compact) {
+        if (three) GS_EMIT(true, 3); else GS_EMIT(true, 2);
+    } else {
+        if (three) GS_EMIT(false, 3); else GS_EMIT(false, 2);
+    }
+#undef GS_EMIT
     return hipGetLastError();
 }
 

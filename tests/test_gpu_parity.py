@@ -139,6 +139,22 @@ def test_render_frame(gpu_ctx, ts, H, W):
     assert p >= 55.0
 
 
+def test_render_frame_three_tile_digits(gpu_ctx):
+    """A 4160x4200 frame has 260x263 = 68380 16-px tiles: 17 tile-id bits, so
+    the tile sort runs three passes (digits of 6, 6 and 5 bits) and the pair
+    emission produces three tile-digit histograms."""
+    H, W = 4160, 4200
+    scene, cam, cov = _scene(4_000, 31, H, W)
+    img_o, st_o, _ = O.render_full(scene.means, cov, scene.opacities, scene.colors, cam.w2c,
+                                   cam.K, H, W, tile_size=16)
+    gpu_ctx.set_scene(scene.means, cov, scene.opacities, scene.colors)
+    img, st = gpu_ctx.render(L.make_view(cam.w2c, cam.K, H, W, tile_size=16, output="f32"))
+    print(f"three tile digits: M={st['num_visible']} P={st['num_entries']}", flush=True)
+    assert st["num_visible"] == st_o["num_visible"]
+    assert st["num_entries"] == st_o["num_entries"]
+    assert np.abs(img - img_o).max() <= 1e-5
+
+
 def test_render_pair_capacity_retry():
     """A fresh context starts with room for max(2^20, 4N) candidate pairs; 4200
     large Gaussians make 1.3M pairs, so the first frame overflows, is detected
