@@ -366,7 +366,10 @@ struct gs_ctx {
             b_state.ensure(sb);
             HIPCHK(hipMemsetAsync(b_state.p, 0, b_state.cap, st));
             sort.epoch = 0;
+            sort.dirty[0] = sort.dirty[1] = 0u;
+            sort.half = 0;
         }
+        sort.state_parts = b_state.cap / (256 * sizeof(uint64_t));
         sort.keys_alt = b_kalt.p;
         sort.vals_alt = b_valt.as<uint32_t>();
         sort.hist = b_hist.as<uint32_t>();

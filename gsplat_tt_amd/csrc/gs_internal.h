@@ -86,6 +86,13 @@ struct SortTemp {
     uint32_t* hist = nullptr;      // sort_hist_words(): [8][256] histograms + 8 tickets
     uint64_t* state = nullptr;     // sort_state_bytes(n): look-back descriptors
     uint32_t epoch = 0;            // bumped per pass; tags descriptors (no clearing)
+    // 32-bit descriptors (below 2^30 keys) use the two halves of `state` in
+    // turn: a pass clears, row by row, the half that the next pass uses, so no
+    // pass needs a clearing kernel. dirty[h]: leading partition rows of half h
+    // that may hold descriptors (cleared by a kernel before that half is used).
+    size_t state_parts = 0;        // partition rows per half (state bytes / 2048)
+    uint32_t dirty[2] = {0u, 0u};
+    int half = 0;
     hipEvent_t* pass_events = nullptr;  // optional: 2 per pass (start, stop)
     int max_timed_passes = 0;
 };

@@ -187,7 +187,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     const K* __restrict__ kin, const uint32_t* __restrict__ vin, K* __restrict__ kout,
     uint32_t* __restrict__ vout, int64_t n_cap, const uint32_t* __restrict__ n_dev, int shift,
     int bits, const uint32_t* __restrict__ g_hist_pass, void* __restrict__ state_raw,
-    uint32_t* __restrict__ ticket, uint32_t epoch) {
+    uint32_t* __restrict__ ticket, uint32_t epoch, uint32_t* __restrict__ clear_next) {
     using D = Desc<D32>;
     using DT = typename D::T;
     DT* state = static_cast<DT*>(state_raw);
@@ -214,6 +214,8 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     const uint32_t mask = (1u << bits) - 1u;
 
     if (tid == 0) s_vid = atomicAdd(ticket, 1u);
+    // this workgroup's row of the descriptors that the next pass uses
+    if (clear_next != nullptr && tid < 256) clear_next[(size_t)blockIdx.x * 256 + tid] = 0u;
     for (int i = tid; i < WAVES * 256; i += THREADS) (&s_wcnt[0][0])[i] = 0;
     __syncthreads();
     const uint32_t vid = s_vid;
@@ -395,14 +397,31 @@ hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uin
     constexpr bool SP = CFG::SPLIT;
     const unsigned grid = (unsigned)((n_cap + T * I - 1) / (T * I));
     const bool d32 = n_cap < ((int64_t)1 << 30);
-    const size_t words = (size_t)grid * 256 * (d32 ? 1 : 2);
-    k_fill_u32<<<(unsigned)((words + 255) / 256), 256, 0, st>>>(
-        reinterpret_cast<uint32_t*>(tmp.state), 0u, words);
+    uint32_t* state = reinterpret_cast<uint32_t*>(tmp.state);
+    uint32_t* clear_next = nullptr;
+    if (d32 && tmp.state_parts >= grid) {
+        const size_t half_words = tmp.state_parts * 256;
+        uint32_t* cur = state + (size_t)tmp.half * half_words;
+        clear_next = state + (size_t)(tmp.half ^ 1) * half_words;
+        if (tmp.dirty[tmp.half] != 0u) {
+            const size_t words = (size_t)tmp.dirty[tmp.half] * 256;
+            k_fill_u32<<<(unsigned)((words + 255) / 256), 256, 0, st>>>(cur, 0u, words);
+        }
+        // this pass dirties rows [0, grid) of its half and clears them in the other
+        tmp.dirty[tmp.half] = grid;
+        if (grid >= tmp.dirty[tmp.half ^ 1]) tmp.dirty[tmp.half ^ 1] = 0u;
+        tmp.half ^= 1;
+        state = cur;
+    } else {
+        const size_t words = (size_t)grid * 256 * (d32 ? 1 : 2);
+        k_fill_u32<<<(unsigned)((words + 255) / 256), 256, 0, st>>>(state, 0u, words);
+        tmp.dirty[0] = tmp.dirty[1] = (uint32_t)std::min<size_t>(tmp.state_parts, 0xFFFFFFFFu);
+    }
     const uint32_t epoch = ++tmp.epoch;
 #define GS_OS(IO, DD, DR)                                                                         \
     k_onesweep<K, IO, T, I, DD, DR, SP><<<grid, T, 0, st>>>(kin, vin, kout, vout, n_cap, n_dev,  \
-                                                            shift, bits, hist_pass, tmp.state,   \
-                                                            ticket, epoch)
+                                                            shift, bits, hist_pass, state,       \
+                                                            ticket, epoch, clear_next)
     if (drop) {
         if (iota || sizeof(K) != 4) return hipErrorInvalidValue;
         if (d32) GS_OS(false, true, true); else GS_OS(false, false, true);
