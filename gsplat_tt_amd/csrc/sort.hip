@@ -103,16 +103,24 @@ __global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ key
             ok[it] = i < n;
             k[it] = ok[it] ? keys[i] : K(0);
         }
+        // passes outside, items inside: the items' digit tests of one pass are
+        // independent and interleave
+        for (int p = 0; p < npass; ++p) {
+            const int shift = begin_bit + 8 * p;
+            const uint32_t mask = (1u << min(8, end_bit - shift)) - 1u;
+            uint32_t d[kHistItems], d0[kHistItems];
+            uint64_t same[kHistItems];
 #pragma unroll
-        for (int it = 0; it < kHistItems; ++it) {
-            for (int p = 0; p < npass; ++p) {
-                const int shift = begin_bit + 8 * p;
-                const int bits = min(8, end_bit - shift);
-                const uint32_t d = digit_of(k[it], shift, (1u << bits) - 1u);
-                const uint32_t d0 = __builtin_amdgcn_readfirstlane(d);
-                const uint64_t same = __ballot(ok[it] && d == d0);
-                if (ok[it] && d != d0) atomicAdd(&h[w][p][d], 1u);
-                if (lane == 0 && same != 0ull) atomicAdd(&h[w][p][d0], (uint32_t)__popcll(same));
+            for (int it = 0; it < kHistItems; ++it) {
+                d[it] = digit_of(k[it], shift, mask);
+                d0[it] = __builtin_amdgcn_readfirstlane(d[it]);
+                same[it] = __ballot(ok[it] && d[it] == d0[it]);
+            }
+#pragma unroll
+            for (int it = 0; it < kHistItems; ++it) {
+                if (ok[it] && d[it] != d0[it]) atomicAdd(&h[w][p][d[it]], 1u);
+                if (lane == 0 && same[it] != 0ull)
+                    atomicAdd(&h[w][p][d0[it]], (uint32_t)__popcll(same[it]));
             }
         }
     }
