@@ -2,13 +2,15 @@
 //
 // One upsweep pass builds the digit histograms of every pass at once; each
 // digit pass is then a single kernel (Adinets & Merrill, "Onesweep", 2022):
-//   * a 5120 (u64 keys) or 8192 (u32 keys) key partition per 1024-thread
-//     workgroup, partitions taken in order from an atomic ticket so look-back
-//     only waits on resident predecessors;
+//   * an 8192-key partition per 1024-thread workgroup (64-bit keys staged in
+//     LDS without their values), partitions taken in order from an atomic
+//     ticket so look-back only waits on resident predecessors;
 //   * wave64 stable ranking with 8 ballots per key (peer mask of equal digits)
 //     plus per-wave digit counters in LDS;
-//   * per-digit decoupled look-back over epoch-tagged 64-bit descriptors (no
-//     clearing between passes or sorts);
+//   * per-digit decoupled look-back, walked after the partition has published
+//     its counts and re-ordered its keys in LDS (32-bit descriptors in two
+//     alternating halves, each pass clearing the next one's; epoch-tagged
+//     64-bit descriptors above 2^30 keys);
 //   * keys re-ordered by digit in LDS and written out in digit runs, so global
 //     stores are contiguous per digit.
 // Stability across passes makes the whole sort stable, which is what the
