@@ -34,6 +34,8 @@ EXPORTED = (
     "gs_render_next",
     "gs_render_out_ring", "gs_out_release", "gs_out_ring_config", "gs_out_ring_info",
     "gs_set_chunk_cull",
+    "gs_frame_readback", "gs_set_cull_stats", "gs_set_spin_limit",
+    "gs_sort_tile_depth_dev", "gs_last_ranges_ms",
 )
 TRAIN_PARAMS = ("means", "log_scales", "quats", "opacity_logits", "sh")
 
@@ -64,7 +66,8 @@ class GsStats(ctypes.Structure):
                 ("ms_total", ctypes.c_float), ("blend_evals", ctypes.c_int64),
                 ("blend_batches", ctypes.c_int64), ("blend_iters", ctypes.c_int64),
                 ("blend_kept", ctypes.c_int64), ("blend_max_iters", ctypes.c_int64),
-                ("chunks_skipped", ctypes.c_int64)]
+                ("chunks_skipped", ctypes.c_int64), ("pairs_dropped_mb", ctypes.c_int64),
+                ("pairs_kept_mb", ctypes.c_int64)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
@@ -141,6 +144,9 @@ def load_library():
         L.gs_last_error.restype = ctypes.c_char_p
         L.gs_destroy.restype = None
         L.gs_out_release.argtypes = [ctypes.c_uint64]
+        L.gs_set_spin_limit.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
+        L.gs_last_ranges_ms.restype = ctypes.c_float
+        L.gs_last_ranges_ms.argtypes = [ctypes.c_void_p]
         for name in EXPORTED:
             getattr(L, name)  # every declared symbol must resolve
         _LIB = L
@@ -217,6 +223,7 @@ class Context:
             _check(self._L.gs_set_timing(self._c, 1))
         self._keep = None
         self._version = 0
+        self._last_tiles = 0
 
     def close(self):
         if self._c:
@@ -266,6 +273,8 @@ class Context:
             out = np.empty((H, W, 3), _OUT_DTYPE[view.out_format])
         st = GsStats()
         _check(self._L.gs_render(self._c, ctypes.byref(view), _ptr(out), 0, ctypes.byref(st)))
+        ts = view.tile_size
+        self._last_tiles = ((W + ts - 1) // ts) * ((H + ts - 1) // ts)
         return out, st.as_dict()
 
     def train_loss(self, image, target, lambda_dssim=0.2, loss_scale=1.0):
@@ -335,10 +344,56 @@ class Context:
                                        ctypes.c_int(1 if out_on_device else 0), sts))
         return [st.as_dict() for st in sts]
 
+    def frame_readback(self, ids=True, ranges=True):
+        """The last render()'s frame: dict(M, pairs_pre, P, sorted_ids int64 (P,),
+        tile_ranges int64 (T, 2)) - the tile-sorted compact ids and the tile
+        ranges of the frame path itself (gs_frame_readback)."""
+        cnt = np.zeros(3, np.int64)
+        _check(self._L.gs_frame_readback(self._c, _ptr(cnt), None, ctypes.c_int64(0), None,
+                                         ctypes.c_int64(0)))
+        M, ppre, P = (int(x) for x in cnt)
+        out = dict(M=M, pairs_pre=ppre, P=P)
+        T = self._last_tiles
+        sid = np.empty(max(P, 1), np.int64) if ids else None
+        rg = np.empty((T, 2), np.int64) if ranges else None
+        _check(self._L.gs_frame_readback(self._c, None, _ptr(sid), ctypes.c_int64(P if ids else 0),
+                                         _ptr(rg), ctypes.c_int64(T if ranges else 0)))
+        if ids:
+            out["sorted_ids"] = sid[:P]
+        if ranges:
+            out["tile_ranges"] = rg
+        return out
+
+    def set_cull_stats(self, on: bool = True):
+        """Per-frame counts of the reference's microblock cull in the stats
+        (pairs_dropped_mb, pairs_kept_mb)."""
+        _check(self._L.gs_set_cull_stats(self._c, ctypes.c_int(1 if on else 0)))
+
+    def set_spin_limit(self, limit: int = 0):
+        """Spin limit of the kernels' bounded look-back waits (0: default); a tiny
+        limit makes a wait give up, and the call then fails (tests of that path)."""
+        _check(self._L.gs_set_spin_limit(self._c, ctypes.c_uint32(limit)))
+
+    def sort_tile_depth_dev(self, keys_ptr: int, vals_ptr: int, n: int, num_tiles: int,
+                            ranges_ptr: int):
+        """Stable sort of (tile << 32 | depth bits, value) pairs on the device plus the
+        per-tile [start, end) ranges (num_tiles x 2 u32 at ranges_ptr)."""
+        passes = ctypes.c_int()
+        _check(self._L.gs_sort_tile_depth_dev(self._c, ctypes.c_void_p(keys_ptr),
+                                              ctypes.c_void_p(vals_ptr), ctypes.c_int64(n),
+                                              ctypes.c_int64(num_tiles),
+                                              ctypes.c_void_p(ranges_ptr), ctypes.byref(passes)))
+        return passes.value
+
+    def last_ranges_ms(self) -> float:
+        return float(self._L.gs_last_ranges_ms(self._c))
+
     def render_dev(self, view: GsView, dev_out_ptr: int):
         st = GsStats()
         _check(self._L.gs_render(self._c, ctypes.byref(view), ctypes.c_void_p(dev_out_ptr), 1,
                                  ctypes.byref(st)))
+        ts = view.tile_size
+        self._last_tiles = ((view.image_width + ts - 1) // ts) * ((view.image_height + ts - 1) // ts)
         return st.as_dict()
 
     # ---- stages (host arrays)

@@ -80,6 +80,8 @@ class HipBackend:
         self.use_isoellipse = bool(use_isoellipse)
         self.tile_size = int(tile_size)
         self.ctx = L.Context(device, timing=True)  # raises without library / GPU
+        # render_fused reports the microblock cull's pairs_dropped / pairs_kept_per_mb
+        self.ctx.set_cull_stats(True)
         self._cov_key = None
         self._cov = None
 
@@ -191,25 +193,30 @@ class HipBackend:
                      use_isoellipse: bool = False):
         """backends/cpu_cpp/backend.py:319-380: one call from the Gaussians to the
         (H,W,3) float32 image and a stats dict (project_ms, tile_assign_ms,
-        sort_ms, blend_ms, total_ms, num_visible, num_entries, pairs_in,
-        pairs_dropped). `gaussians` has means, scales, rotations, opacities and
-        colors (N,3) RGB."""
+        sort_ms, cull_ms, blend_ms, total_ms, num_visible, num_entries, pairs_in,
+        pairs_dropped, pairs_kept_per_mb). `gaussians` has means, scales,
+        rotations, opacities and colors (N,3) RGB. As in the reference, the
+        contrib_floor / k_cap / use_isoellipse arguments of this call are not
+        read: the constructor's settings apply (the per-pair floor is the
+        microblock floor unless the constructor overrode it)."""
+        del contrib_floor, k_cap, use_isoellipse  # the reference ignores them too
         means = _np(gaussians.means, np.float32)
         cov = self._cached_cov3d(_np(gaussians.scales, np.float32),
                                  _np(gaussians.rotations, np.float32))
         op = _np(gaussians.opacities, np.float32).reshape(-1)
         col = _np(gaussians.colors, np.float32).reshape(means.shape[0], 3)
         self.ctx.set_scene(means, cov, op, col)
-        view = self._view(extrinsics, intrinsics, image_height, image_width,
-                          contrib_floor=contrib_floor, k_cap=k_cap,
-                          use_isoellipse=use_isoellipse)
+        view = self._view(extrinsics, intrinsics, image_height, image_width)
         img, st = self.ctx.render(view)
+        # pairs_in = the tile-sorted pairs the microblock cull reads
+        # (cull_and_blend.cpp:700); dropped / kept_per_mb from its counts
         stats = {"project_ms": st["ms_project"] + st["ms_depth_sort"],
                  "tile_assign_ms": st["ms_tile_assign"], "sort_ms": st["ms_tile_sort"],
-                 "blend_ms": st["ms_blend"], "total_ms": st["ms_total"],
+                 "cull_ms": 0.0, "blend_ms": st["ms_blend"], "total_ms": st["ms_total"],
                  "num_visible": int(st["num_visible"]), "num_entries": int(st["num_entries"]),
                  "pairs_in": int(st["num_entries"]),
-                 "pairs_dropped": int(st["pairs_pre"] - st["num_entries"])}
+                 "pairs_dropped": int(st["pairs_dropped_mb"]),
+                 "pairs_kept_per_mb": int(st["pairs_kept_mb"])}
         return img, stats
 
     def close(self) -> None:

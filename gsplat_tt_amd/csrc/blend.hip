@@ -18,6 +18,8 @@
 // image-edge microblocks follow its scalar rule (exp, T *= 1-alpha, test after
 // every entry) (cull_and_blend.cpp:506-670, simd_exp_avx2.h:12-32). A half
 // whose microblock is done stops issuing; the wave exits when both are done.
+#include <algorithm>
+
 #include "gs_common.h"
 #include "gs_internal.h"
 
@@ -51,6 +53,19 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
     uint32_t u = __float_as_uint(x);
     u += 0x7FFFu + ((u >> 16) & 1u);
     return (uint16_t)(u >> 16);
+}
+
+// u8 of a bf16 colour, uint8(float32(clip(float32(b), 0, 1)) * 255) with
+// truncation, in integer form: a bf16 in [0, 1) is (128 + m) 2^(e - 134), so
+// the product with 255 is exact and truncates to ((128 + m) 255) >> (134 - e)
+// (render/kernels/dataflow/img_pack_u8.h:9-14,31-41, the u8 that the
+// reference's render_view returns).
+__device__ __forceinline__ uint8_t bf16_to_u8(uint32_t b) {
+    const uint32_t e = (b >> 7) & 0xFFu;
+    if ((b & 0x8000u) != 0u || e < 119u) return 0u;
+    if (e >= 127u) return 255u;
+    const uint32_t sig = 128u + (b & 0x7Fu);
+    return (uint8_t)(((sig << 8) - sig) >> (134u - e));
 }
 
 // Per-wave geometry of one 16x4 band (two microblocks).
@@ -353,6 +368,8 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
                                                    const uint32_t* __restrict__ ranges,
                                                    BlendParams bp, void* __restrict__ out) {
     const int lane = threadIdx.x;
+    // after an earlier give-up the sorted ids may be wrong: read nothing
+    if (__builtin_amdgcn_readfirstlane(upstream_failed(bp.ctl) ? 1 : 0)) return;
     const Band g = make_band<TS>(bp, lane);
     float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
     uint32_t cnt = 0, n_batch = 0, n_iter = 0, n_kept = 0;
@@ -394,10 +411,91 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
         img[o + 1] = f32_to_bf16_rne(cg);
         img[o + 2] = f32_to_bf16_rne(cb);
     } else {
+        // the bf16 image packed to u8, as the reference's render_view does
         uint8_t* img = static_cast<uint8_t*>(out);
-        img[o + 0] = (uint8_t)(fminf(fmaxf(cr, 0.0f), 1.0f) * 255.0f);
-        img[o + 1] = (uint8_t)(fminf(fmaxf(cg, 0.0f), 1.0f) * 255.0f);
-        img[o + 2] = (uint8_t)(fminf(fmaxf(cb, 0.0f), 1.0f) * 255.0f);
+        img[o + 0] = bf16_to_u8(f32_to_bf16_rne(cr));
+        img[o + 1] = bf16_to_u8(f32_to_bf16_rne(cg));
+        img[o + 2] = bf16_to_u8(f32_to_bf16_rne(cb));
+    }
+}
+
+// Statistics of the reference's per-microblock cull (cull_and_blend.cpp:
+// 384-504, 835-836) over the tile-sorted pairs: pairs that no microblock keeps
+// (out[0]) and kept (pair, microblock) pairs (out[1]). The reference walks the
+// 4x8 grid of 8x4-pixel microblocks at the tile origin whatever the tile size
+// (with 16-pixel tiles that grid reaches past the tile), and so does this
+// count; the blend itself evaluates the microblocks inside the tile only.
+constexpr int kStatThreads = 256;
+__global__ __launch_bounds__(kStatThreads) void k_mb_stats(
+    const float4* __restrict__ brec, const uint32_t* __restrict__ sid,
+    const uint32_t* __restrict__ stile, uint32_t p_cap, const uint32_t* __restrict__ p_dev,
+    int tiles_x, int tile_size, int cull_disabled, unsigned long long* __restrict__ out,
+    const uint32_t* ctl) {
+    if (__builtin_amdgcn_readfirstlane(upstream_failed(ctl) ? 1 : 0)) return;
+    const uint32_t p = p_dev ? min(p_cap, *p_dev) : p_cap;
+    uint32_t dropped = 0, kept = 0;
+    for (uint32_t i = blockIdx.x * kStatThreads + threadIdx.x; i < p;
+         i += gridDim.x * kStatThreads) {
+        const uint32_t t = stile[i], gi = sid[i];
+        const float4 r0 = brec[3 * (size_t)gi + 0], r1 = brec[3 * (size_t)gi + 1];
+        const float lt = r1.w;
+        if (lt >= 0.0f) {
+            ++dropped;
+            continue;
+        }
+        const float tx_tile = (float)((int)(t % (uint32_t)tiles_x) * tile_size);
+        const float ty_tile = (float)((int)(t / (uint32_t)tiles_x) * tile_size);
+        const float mx = r0.x, my = r0.y;
+        const int mx_lo = max(0, (int)floorf(((mx - r0.z) - tx_tile) / 8.0f));
+        const int mx_hi = min(3, (int)floorf(((mx + r0.z) - tx_tile) / 8.0f));
+        const int my_lo = max(0, (int)floorf(((my - r0.w) - ty_tile) / 4.0f));
+        const int my_hi = min(7, (int)floorf(((my + r0.w) - ty_tile) / 4.0f));
+        if (mx_lo > mx_hi || my_lo > my_hi) {
+            ++dropped;
+            continue;
+        }
+        const float ci_a = r1.x, ci_b = r1.y, ci_c = r1.z;
+        const float thresh_m2 = -2.0f * lt;
+        const float ci_a_safe = fmax_std(ci_a, 1e-12f), ci_c_safe = fmax_std(ci_c, 1e-12f);
+        uint32_t k = 0;
+        for (int by = my_lo; by <= my_hi; ++by) {
+            const float v_lo = (ty_tile + (float)(by * 4)) - my;
+            const float v_hi = v_lo + 4.0f;
+            const bool y_in = (v_lo <= 0.0f) && (0.0f <= v_hi);
+            const float v_fix = (v_lo > 0.0f) ? v_lo : v_hi;
+            for (int bx = mx_lo; bx <= mx_hi; ++bx) {
+                const float u_lo = (tx_tile + (float)(bx * 8)) - mx;
+                const float u_hi = u_lo + 8.0f;
+                const bool x_in = (u_lo <= 0.0f) && (0.0f <= u_hi);
+                float m2_min = 0.0f;
+                if (!cull_disabled && !(x_in && y_in)) {
+                    float m2_v = __builtin_inff(), m2_h = __builtin_inff();
+                    if (!x_in) {
+                        const float uf = (u_lo > 0.0f) ? u_lo : u_hi;
+                        const float vs = fclamp_std(-ci_b * uf / ci_c_safe, v_lo, v_hi);
+                        m2_v = ci_a * uf * uf + 2.0f * ci_b * uf * vs + ci_c * vs * vs;
+                    }
+                    if (!y_in) {
+                        const float us = fclamp_std(-ci_b * v_fix / ci_a_safe, u_lo, u_hi);
+                        m2_h = ci_a * us * us + 2.0f * ci_b * us * v_fix + ci_c * v_fix * v_fix;
+                    }
+                    m2_min = fmin_std(m2_v, m2_h);
+                }
+                k += (m2_min <= thresh_m2) ? 1u : 0u;
+            }
+        }
+        kept += k;
+        dropped += (k == 0u) ? 1u : 0u;
+    }
+    unsigned long long d = dropped, kk = kept;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        d += __shfl_xor(d, o, GS_WAVE);
+        kk += __shfl_xor(kk, o, GS_WAVE);
+    }
+    if (lane_id() == 0) {
+        if (d) atomicAdd(out + 0, d);
+        if (kk) atomicAdd(out + 1, kk);
     }
 }
 
@@ -415,6 +513,17 @@ hipError_t launch_ts(const float4* brec, const uint32_t* sid, const uint32_t* ra
 }
 
 }  // namespace
+
+hipError_t launch_mb_stats(const float4* brec, const uint32_t* sid, const uint32_t* stile,
+                           uint32_t p_cap, const uint32_t* p_dev, int tiles_x, int tile_size,
+                           int cull_disabled, unsigned long long* out, const uint32_t* ctl,
+                           hipStream_t st) {
+    if (p_cap == 0 || tiles_x <= 0) return hipSuccess;
+    const unsigned grid = std::min<unsigned>((p_cap + kStatThreads - 1) / kStatThreads, 4096u);
+    k_mb_stats<<<grid, kStatThreads, 0, st>>>(brec, sid, stile, p_cap, p_dev, tiles_x, tile_size,
+                                              cull_disabled, out, ctl);
+    return hipGetLastError();
+}
 
 hipError_t launch_blend(const float4* brec, const uint32_t* sid, const uint32_t* ranges,
                         BlendParams bp, void* out, hipStream_t st) {

@@ -145,6 +145,7 @@ struct gs_ctx {
     hipEvent_t ev[12] = {};
     hipEvent_t sort_ev[16] = {};
     int last_sort_passes = 0;
+    float last_ranges_ms = 0.0f;  // tile-range extraction of the last gs_sort_tile_depth_dev
     int num_cus = 0;
 
     // scene
@@ -175,6 +176,33 @@ struct gs_ctx {
     std::vector<uint64_t> h_evals = std::vector<uint64_t>(64 * 8);
     uint32_t* h_pin = nullptr;  // pinned: counters + histograms
     gs::SortTemp sort;
+
+    // Control words of the kernels (ctl[0] error flags, ctl[1] look-back spin
+    // limit): words C_CTL.. of the frame counters, or of b_cnt for the stage
+    // entry points.
+    uint32_t spin_limit = 0;   // 0: the kernels' default (gs_set_spin_limit)
+    bool cull_stats = false;   // microblock-cull statistics per frame (gs_set_cull_stats)
+    // Enqueues the reset of a pair of control words (flags 0, spin limit).
+    void ctl_reset(uint32_t* ctl) {
+        HIPCHK(gs::launch_fill_u32(ctl, 0u, 1, st));
+        HIPCHK(gs::launch_fill_u32(ctl + 1, spin_limit, 1, st));
+    }
+    // Turns raised error flags into an error: the outputs are not trusted.
+    static void ctl_check(uint32_t flags, const char* what) {
+        if (flags & gs::kErrKeyRange)
+            throw GsError(GS_E_INVALID, std::string(what) + ": a key's tile id is >= num_tiles");
+        if (flags != 0u)
+            throw GsError(GS_E_DEVICE, std::string(what) +
+                                           ": a bounded look-back wait gave up (outputs discarded)");
+    }
+
+    // The last gs_render frame of this context, for gs_frame_readback: its
+    // tile-sorted compact ids and tile ids live in the frame buffers until the
+    // next call that reuses them.
+    bool rb_valid = false, rb_empty = false;
+    uint32_t* rb_ids = nullptr;
+    uint32_t* rb_tiles = nullptr;
+    int64_t rb_T = 0, rb_M = 0, rb_ppre = 0, rb_P = 0;
 
     ~gs_ctx() {
         for (gs_ctx* p : peers) delete p;
@@ -411,7 +439,10 @@ struct gs_ctx {
         HIPCHK(gs::launch_fill_u32(b_cnt.as<uint32_t>(), 0u, 64, st));
         HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, parts * 2, st));
         if (n == 0) return 0;
+        uint32_t* ctl = b_cnt.as<uint32_t>() + C_CTL;
+        if (spin_limit) ctl_reset(ctl);
         gs::ProjParams p = proj_params(v);
+        p.ctl = ctl;
         gs::Compact c{b_rc.as<float4>(), b_dkey.as<uint32_t>(),
                       b_brec.as<float4>(), want_src ? b_src.as<uint32_t>() : nullptr};
         HIPCHK(gs::launch_project(sd, p, c, want_valid ? b_valid.as<uint8_t>() : nullptr,
@@ -419,6 +450,7 @@ struct gs_ctx {
                                   b_cnt.as<uint32_t>() + 1, nullptr, st));
         HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
         sync();
+        ctl_check(h_pin[C_CTL], "project");
         return h_pin[1];
     }
 
@@ -432,16 +464,21 @@ struct gs_ctx {
         b_lb.ensure(rparts * 8);
         if (b_bstart.cap < 4096 * 4) b_bstart.ensure(4096 * 4);
         uint32_t p_pre = 0;
+        uint32_t* ctl = b_cnt.as<uint32_t>() + C_CTL;
+        gs::TileParams tpc = tp;
+        tpc.ctl = ctl;
+        ctl_reset(ctl);
         for (int attempt = 0; attempt < 2; ++attempt) {
             HIPCHK(gs::launch_fill_u32(b_cnt.as<uint32_t>() + 8, 0u, 8, st));
             HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, rparts * 2, st));
-            HIPCHK(gs::launch_rect_count_scan(rect, cov, 1, order, m, nullptr, tp,
+            HIPCHK(gs::launch_rect_count_scan(rect, cov, 1, order, m, nullptr, tpc,
                                               b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(),
                                               (uint32_t)(b_bstart.cap / 4), b_lb.as<uint64_t>(),
                                               b_cnt.as<uint32_t>() + 8, b_cnt.as<uint32_t>() + 9,
                                               nullptr, nullptr, st));
             HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
             sync();
+            ctl_check(h_pin[C_CTL], "tile_assign");
             p_pre = h_pin[9];
             if (p_pre == 0xFFFFFFFFu)
                 throw GsError(GS_E_CAPACITY, "tile_assign: more than 2^32-1 candidate pairs");
@@ -457,13 +494,14 @@ struct gs_ctx {
         b_lb.ensure(eparts * 8);
         HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, eparts * 2, st));
         HIPCHK(gs::launch_pair_emit(rect, cov, order, b_offs.as<uint32_t>(),
-                                    b_bstart.as<uint32_t>(), m, nullptr, p_pre, nullptr, tp,
+                                    b_bstart.as<uint32_t>(), m, nullptr, p_pre, nullptr, tpc,
                                     b_pair_tile.as<uint32_t>(), b_pair_id.as<uint32_t>(), p_pre,
                                     b_lb.as<uint64_t>(), b_cnt.as<uint32_t>() + 10,
                                     b_cnt.as<uint32_t>() + 11, nullptr,
                                     tile_bits((int64_t)tp.tiles_x * tp.tiles_y), true, st));
         HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
         sync();
+        ctl_check(h_pin[C_CTL], "tile_assign");
         return h_pin[11];
     }
 
@@ -474,8 +512,9 @@ struct gs_ctx {
     static constexpr size_t kFrTileHist = 64 + 1024;  // [2 or 4][256] tile-id digits
     static constexpr size_t kFrLb = 64 + 1024 + 1024;  // look-back states (u64 each)
     enum : int {
-        C_PROJ_TICKET = 0, C_M = 1, C_SKIPPED = 2, C_RECT_TICKET = 8, C_PPRE = 9, C_EMIT_TICKET = 10, C_P = 11,
-        C_DSORT_TICKETS = 16, C_TSORT_TICKETS = 24
+        C_PROJ_TICKET = 0, C_M = 1, C_SKIPPED = 2, C_CTL = 4, C_RECT_TICKET = 8, C_PPRE = 9,
+        C_EMIT_TICKET = 10, C_P = 11, C_DSORT_TICKETS = 16, C_TSORT_TICKETS = 24,
+        C_MBSTAT = 40  // two u64: pairs no microblock keeps, kept (pair, microblock)
     };
     uint64_t pair_cap = 0;  // candidate-pair capacity of the frame buffers
     DevBuf b_frame, b_phist_proj, b_phist_emit, b_rect_r, b_cov_r;
@@ -520,6 +559,7 @@ struct gs_ctx {
         pend = Pending{};
         pend.t0 = std::chrono::steady_clock::now();
         tr.fwd_valid = false;  // the frame buffers are about to be reused
+        rb_valid = false;
         check_view(v);
         REQUIRE(out != nullptr, "render: null output");
         if (!shared_terms) ensure_terms(v);
@@ -587,11 +627,20 @@ struct gs_ctx {
             enqueue_attempt();
         }
         pend.active = false;
+        s.pairs_dropped_mb = -1;
+        s.pairs_kept_mb = -1;
         if (!pend.empty) {
+            ctl_check(h_pin[C_CTL], "render");
             s.num_visible = h_pin[C_M];
             s.pairs_pre = h_pin[C_PPRE];
             s.num_entries = h_pin[C_P];
             s.chunks_skipped = h_pin[C_SKIPPED];
+            if (cull_stats) {
+                uint64_t mb[2];
+                std::memcpy(mb, h_pin + C_MBSTAT, sizeof(mb));
+                s.pairs_dropped_mb = (int64_t)mb[0];
+                s.pairs_kept_mb = (int64_t)mb[1];
+            }
             if (timing) {
                 s.ms_project = elapsed(0, 1);
                 s.ms_depth_sort = elapsed(1, 2);
@@ -603,6 +652,16 @@ struct gs_ctx {
         }
         s.ms_total = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() -
                                                                pend.t0).count();
+        rb_valid = true;
+        rb_empty = pend.empty;
+        rb_T = pend.T;
+        rb_M = pend.empty ? 0 : (int64_t)h_pin[C_M];
+        rb_ppre = pend.empty ? 0 : (int64_t)h_pin[C_PPRE];
+        rb_P = pend.empty ? 0 : (int64_t)h_pin[C_P];
+        if (pend.empty) {
+            s.pairs_dropped_mb = cull_stats ? 0 : -1;
+            s.pairs_kept_mb = cull_stats ? 0 : -1;
+        }
         if (pend.stats) *pend.stats = s;
     }
 
@@ -622,6 +681,8 @@ struct gs_ctx {
         }
         for (gs_ctx* p : peers) {
             p->timing = timing;
+            p->spin_limit = spin_limit;
+            p->cull_stats = cull_stats;
             p->sd = sd;
             p->has_opac = has_opac;
             p->skey.valid = true;
@@ -797,9 +858,11 @@ struct gs_ctx {
     // cnt[C_M], depth-key histograms reduced) to the tile-sorted compact ids and
     // tile ranges: depth sort, candidate scan, pair emission + cull, tile sort,
     // tile bounds. Returns the sorted compact ids.
-    uint32_t* frame_tiles(const FrameLayout& L, int64_t N, int64_t T, const gs::TileParams& tp) {
+    uint32_t* frame_tiles(const FrameLayout& L, int64_t N, int64_t T, const gs::TileParams& tp,
+                          uint32_t** tiles_out) {
         uint32_t* fr = L.fr;
         uint32_t* cnt = L.cnt;
+        sort.ctl = cnt + C_CTL;
         // depth order of the visible Gaussians (stable: ties keep index order)
         void* kf = nullptr;
         uint32_t* order = nullptr;
@@ -833,6 +896,7 @@ struct gs_ctx {
                                         &ids_sorted, cnt + C_P));
         HIPCHK(gs::launch_tile_bounds(static_cast<uint32_t*>(tiles_sorted), L.pcap, cnt + C_P,
                                       b_ranges.as<uint32_t>(), T, st));
+        if (tiles_out) *tiles_out = static_cast<uint32_t*>(tiles_sorted);
         return ids_sorted;
     }
 
@@ -843,8 +907,10 @@ struct gs_ctx {
         const FrameLayout L = frame_prepare(N, T);
         record(0);
         HIPCHK(gs::launch_fill_u32(L.fr, 0u, L.fwords, st));
+        if (spin_limit) HIPCHK(gs::launch_fill_u32(L.cnt + C_CTL + 1, spin_limit, 1, st));
         if (timing) HIPCHK(gs::launch_fill_u32(b_evals.as<uint32_t>(), 0u, 64 * 8 * 2, st));
         gs::ProjParams p = proj_params(v);
+        p.ctl = L.cnt + C_CTL;
         // the boxes bound three standard deviations: no skipping for wider k
         if (sd.chunk_box != nullptr && v->k_cap <= 3.0f) {
             b_skip.ensure(gs::project_partitions(N));
@@ -859,15 +925,24 @@ struct gs_ctx {
         HIPCHK(gs::launch_reduce_rows(b_phist_proj.as<uint32_t>(), 1024, (uint32_t)L.pparts,
                                       nullptr, 0, 0, L.fr + kFrDepthHist, st));
         record(1);
-        gs::TileParams tp{tiles_x, tiles_y, v->tile_size, v->cull_disabled ? 0 : 1};
-        uint32_t* ids_sorted = frame_tiles(L, N, T, tp);
+        gs::TileParams tp{tiles_x, tiles_y, v->tile_size, v->cull_disabled ? 0 : 1,
+                          L.cnt + C_CTL};
+        uint32_t* tiles_sorted = nullptr;
+        uint32_t* ids_sorted = frame_tiles(L, N, T, tp, &tiles_sorted);
         record(4);
         gs::BlendParams bp{tiles_x, tiles_y, v->tile_size, v->image_height, v->image_width,
                            v->cull_disabled ? 1 : 0, v->transmittance_threshold, v->out_format,
-                           timing ? b_evals.as<unsigned long long>() : nullptr};
+                           timing ? b_evals.as<unsigned long long>() : nullptr, L.cnt + C_CTL};
         HIPCHK(gs::launch_blend(b_brec.as<float4>(), ids_sorted, b_ranges.as<uint32_t>(), bp,
                                 dout, st));
         record(5);
+        if (cull_stats)
+            HIPCHK(gs::launch_mb_stats(b_brec.as<float4>(), ids_sorted, tiles_sorted, L.pcap,
+                                       L.cnt + C_P, tiles_x, v->tile_size, v->cull_disabled,
+                                       reinterpret_cast<unsigned long long*>(L.cnt + C_MBSTAT),
+                                       L.cnt + C_CTL, st));
+        rb_ids = ids_sorted;
+        rb_tiles = tiles_sorted;
     }
 
     // ------------------------------------------------------------ training
@@ -1053,6 +1128,8 @@ struct gs_ctx {
                 if (!e) HIPCHK(hipEventCreate(&e));
         if (timing) HIPCHK(hipEventRecord(tev[0], st));
         HIPCHK(gs::launch_fill_u32(L.fr, 0u, L.fwords, st));
+        if (spin_limit) HIPCHK(gs::launch_fill_u32(L.cnt + C_CTL + 1, spin_limit, 1, st));
+        tr.cam.ctl = L.cnt + C_CTL;
         HIPCHK(gs::launch_fill_u32(t_loss.as<uint32_t>(), 0u, 4, st));
         gs::Compact cpt{b_rc.as<float4>(), b_dkey.as<uint32_t>(),
                         nullptr, b_src.as<uint32_t>()};
@@ -1062,8 +1139,8 @@ struct gs_ctx {
                                         b_phist_proj.as<uint32_t>(), dbg, st));
         HIPCHK(gs::launch_reduce_rows(b_phist_proj.as<uint32_t>(), 1024, (uint32_t)L.pparts,
                                       nullptr, 0, 0, L.fr + kFrDepthHist, st));
-        gs::TileParams tp{tr.tiles_x, tr.tiles_y, 16, 1};
-        tr.ids = frame_tiles(L, std::max<int64_t>(N, 1), T, tp);
+        gs::TileParams tp{tr.tiles_x, tr.tiles_y, 16, 1, L.cnt + C_CTL};
+        tr.ids = frame_tiles(L, std::max<int64_t>(N, 1), T, tp, nullptr);
         gs::TrainFwdParams fp{};
         fp.tiles_x = tr.tiles_x;
         fp.tiles_y = tr.tiles_y;
@@ -1081,6 +1158,7 @@ struct gs_ctx {
         fp.grad_scale = (float)((double)c->loss_scale * (1.0 - (double)c->lambda_dssim) /
                                 (3.0 * (double)px));
         fp.loss = reinterpret_cast<double*>(t_loss.p);
+        fp.ctl = L.cnt + C_CTL;
         HIPCHK(gs::launch_train_fwd(b_brec.as<float4>(), tr.ids, b_ranges.as<uint32_t>(), fp, st));
         if (tgt_dev != nullptr && c->lambda_dssim > 0.0f)
             enqueue_ssim(t_img.as<float>(), tgt_dev, H, W, c->lambda_dssim, c->loss_scale,
@@ -1105,12 +1183,14 @@ struct gs_ctx {
         ensure_counters();
         tr.fwd_valid = false;
         tr.grads_valid = false;
+        rb_valid = false;
         if (pair_cap == 0) pair_cap = std::max<uint64_t>(1u << 20, (uint64_t)tr.n * 4);
         for (int attempt = 0;; ++attempt) {
             train_forward_enqueue(v, c, tgt, dbg);
             HIPCHK(hipMemcpyAsync(h_pin, b_frame.p, 64 * 4, hipMemcpyDeviceToHost, st));
             HIPCHK(hipMemcpyAsync(h_pin + 64, t_loss.p, 16, hipMemcpyDeviceToHost, st));
             sync();
+            ctl_check(h_pin[C_CTL], "train forward");
             const uint32_t p_pre = h_pin[C_PPRE];
             if (p_pre == 0xFFFFFFFFu)
                 throw GsError(GS_E_CAPACITY, "train: more than 2^32-1 candidate pairs");
@@ -1284,6 +1364,53 @@ int gs_render(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device, gs
     });
 }
 
+int gs_frame_readback(gs_ctx* ctx, int64_t* counts, int64_t* sorted_ids, int64_t ids_cap,
+                      int64_t* tile_ranges, int64_t num_tiles) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        REQUIRE(ctx->rb_valid, "frame_readback: no gs_render frame to read (or a later call "
+                               "reused its buffers)");
+        HIPCHK(hipSetDevice(ctx->device));
+        if (counts) {
+            counts[0] = ctx->rb_M;
+            counts[1] = ctx->rb_ppre;
+            counts[2] = ctx->rb_P;
+        }
+        const int64_t P = ctx->rb_P, T = ctx->rb_T;
+        if (sorted_ids) REQUIRE(ids_cap >= P, "frame_readback: ids_cap is smaller than the pair count");
+        if (tile_ranges) REQUIRE(num_tiles == T, "frame_readback: num_tiles is not the frame's tile count");
+        std::vector<uint32_t> ids(sorted_ids && P > 0 ? (size_t)P : 0), rg(tile_ranges ? (size_t)T * 2 : 0);
+        if (!ctx->rb_empty) {
+            if (!ids.empty())
+                HIPCHK(hipMemcpyAsync(ids.data(), ctx->rb_ids, (size_t)P * 4, hipMemcpyDeviceToHost,
+                                      ctx->st));
+            if (!rg.empty())
+                HIPCHK(hipMemcpyAsync(rg.data(), ctx->b_ranges.p, (size_t)T * 8,
+                                      hipMemcpyDeviceToHost, ctx->st));
+            ctx->sync();
+        }
+        for (size_t i = 0; i < ids.size(); ++i) sorted_ids[i] = ids[i];
+        if (tile_ranges)
+            for (int64_t i = 0; i < T * 2; ++i) tile_ranges[i] = rg.empty() ? 0 : rg[(size_t)i];
+    });
+}
+
+int gs_set_cull_stats(gs_ctx* ctx, int on) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        ctx->drain_spec();
+        ctx->cull_stats = on != 0;
+    });
+}
+
+int gs_set_spin_limit(gs_ctx* ctx, uint32_t limit) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        ctx->drain_spec();
+        ctx->spin_limit = limit;
+    });
+}
+
 int gs_render_next(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device,
                    const gs_view* next_view, gs_stats* stats) {
     return guard([&] {
@@ -1353,6 +1480,7 @@ int gs_project(gs_ctx* ctx, const gs_scene* scene, const gs_view* view, uint8_t*
         REQUIRE(ctx && m_out, "null argument");
         HIPCHK(hipSetDevice(ctx->device));
         ctx->drain_spec();
+        ctx->rb_valid = false;
         ctx->set_scene(scene);
         ctx->check_view(view);
         ctx->ensure_terms(view);
@@ -1406,6 +1534,7 @@ int gs_tile_assign(gs_ctx* ctx, const float* means2d, const float* radii, int64_
         REQUIRE(m == 0 || (means2d && radii), "null means2d/radii");
         HIPCHK(hipSetDevice(ctx->device));
         ctx->drain_spec();
+        ctx->rb_valid = false;
         const bool cull = covs2d != nullptr && opac != nullptr;
         *p_out = 0;
         if (p_pre_out) *p_pre_out = 0;
@@ -1460,6 +1589,7 @@ int gs_sort_and_bin(gs_ctx* ctx, const int64_t* gids, const int64_t* tids, const
         REQUIRE(p >= 0 && p < ((int64_t)1 << 32) - 1, "p out of range");
         HIPCHK(hipSetDevice(ctx->device));
         ctx->drain_spec();
+        ctx->rb_valid = false;
         const int64_t T = (int64_t)tiles_x * tiles_y;
         REQUIRE(T < ((int64_t)1 << 31), "too many tiles");
         std::vector<uint32_t> g((size_t)p), t((size_t)p);
@@ -1488,6 +1618,9 @@ int gs_sort_and_bin(gs_ctx* ctx, const int64_t* gids, const int64_t* tids, const
         HIPCHK(gs::launch_make_keys64(ctx->b_tmp_a.as<uint32_t>(), ctx->b_tmp_b.as<uint32_t>(),
                                       ctx->b_tmp_c.as<float>(), (uint32_t)p, keys, ctx->st));
         ctx->ensure_sort(p, 8);
+        uint32_t* ctl = ctx->b_cnt.as<uint32_t>() + gs_ctx::C_CTL;
+        ctx->ctl_reset(ctl);
+        ctx->sort.ctl = ctl;
         ctx->sync();
         int passes = 0;
         void* kf = nullptr;
@@ -1495,12 +1628,15 @@ int gs_sort_and_bin(gs_ctx* ctx, const int64_t* gids, const int64_t* tids, const
         HIPCHK(gs::radix_sort_pairs(keys, ctx->b_tmp_a.as<uint32_t>(), p, 8, 0,
                                     32 + tile_bits(T), ctx->sort, ctx->h_pin + 64, ctx->st,
                                     &passes, false, &kf, &vf));
-        HIPCHK(gs::launch_tile_ranges64(static_cast<uint64_t*>(kf), (uint32_t)p,
-                                        ctx->b_ranges.as<uint32_t>(), T, ctx->st));
+        HIPCHK(gs::launch_tile_bounds64(static_cast<uint64_t*>(kf), (uint32_t)p,
+                                        ctx->b_ranges.as<uint32_t>(), T, ctl, ctx->st));
         std::vector<uint32_t> sid((size_t)p), rg((size_t)T * 2);
+        uint32_t flags = 0;
         HIPCHK(hipMemcpyAsync(sid.data(), vf, (size_t)p * 4, hipMemcpyDeviceToHost, ctx->st));
         HIPCHK(hipMemcpyAsync(rg.data(), ctx->b_ranges.p, (size_t)T * 8, hipMemcpyDeviceToHost, ctx->st));
+        HIPCHK(hipMemcpyAsync(&flags, ctl, 4, hipMemcpyDeviceToHost, ctx->st));
         ctx->sync();
+        gs_ctx::ctl_check(flags, "sort_and_bin");
         for (int64_t i = 0; i < p; ++i) sorted_ids[i] = sid[i];
         for (int64_t i = 0; i < T * 2; ++i) tile_ranges[i] = rg[i];
     });
@@ -1515,6 +1651,7 @@ int gs_cull_and_blend(gs_ctx* ctx, const float* means2d, const float* covs2d,
         REQUIRE(m >= 0 && m < ((int64_t)1 << 31) && p >= 0 && p < ((int64_t)1 << 32), "size out of range");
         HIPCHK(hipSetDevice(ctx->device));
         ctx->drain_spec();
+        ctx->rb_valid = false;
         ctx->check_view(view);
         const int H = view->image_height, W = view->image_width, ts = view->tile_size;
         const int tiles_x = (W + ts - 1) / ts, tiles_y = (H + ts - 1) / ts;
@@ -1558,12 +1695,50 @@ int gs_cull_and_blend(gs_ctx* ctx, const float* means2d, const float* covs2d,
         const size_t bytes = (size_t)H * W * 3 * ebytes;
         ctx->b_out.ensure(bytes);
         gs::BlendParams bp{tiles_x, tiles_y, ts, H, W, view->cull_disabled ? 1 : 0,
-                           view->transmittance_threshold, view->out_format, nullptr};
+                           view->transmittance_threshold, view->out_format, nullptr, nullptr};
         HIPCHK(gs::launch_blend(ctx->b_brec.as<float4>(), ctx->b_pair_id.as<uint32_t>(),
                                 ctx->b_ranges.as<uint32_t>(), bp, ctx->b_out.p, ctx->st));
         HIPCHK(hipMemcpyAsync(image_out, ctx->b_out.p, bytes, hipMemcpyDeviceToHost, ctx->st));
         ctx->sync();
     });
+}
+
+// The standalone u64 sort, and with ranges != null the per-tile [start, end)
+// of (tile << 32 | depth bits) keys (sort.cpp:146-165) from the sorted keys.
+static void sort_u64_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n, int begin_bit,
+                         int end_bit, int64_t num_tiles, uint32_t* ranges, int* passes_out) {
+    HIPCHK(hipSetDevice(ctx->device));
+    ctx->drain_spec();
+    ctx->rb_valid = false;
+    ctx->ensure_counters();
+    ctx->ensure_sort(n, 8);
+    uint32_t* ctl = ctx->b_cnt.as<uint32_t>() + gs_ctx::C_CTL;
+    ctx->ctl_reset(ctl);
+    ctx->sort.ctl = ctl;
+    ctx->sync();
+    int passes = 0;
+    void* kf = nullptr;
+    uint32_t* vf = nullptr;
+    HIPCHK(gs::radix_sort_pairs(keys, vals, n, 8, begin_bit, end_bit, ctx->sort, ctx->h_pin + 64,
+                                ctx->st, &passes, false, &kf, &vf));
+    if (kf != keys) {
+        HIPCHK(hipMemcpyAsync(keys, kf, (size_t)n * 8, hipMemcpyDeviceToDevice, ctx->st));
+        HIPCHK(hipMemcpyAsync(vals, vf, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->st));
+    }
+    if (ranges != nullptr) {
+        const bool timed = ctx->timing;
+        if (timed) HIPCHK(hipEventRecord(ctx->ev[6], ctx->st));
+        HIPCHK(gs::launch_tile_bounds64(keys, (uint32_t)n, ranges, num_tiles, ctl, ctx->st));
+        if (timed) HIPCHK(hipEventRecord(ctx->ev[7], ctx->st));
+    }
+    HIPCHK(hipMemcpyAsync(ctx->h_pin + 64 + 8 * 256, ctl, 4, hipMemcpyDeviceToHost, ctx->st));
+    ctx->sync();
+    ctx->last_sort_passes = passes;
+    ctx->last_ranges_ms = 0.0f;
+    if (ranges != nullptr && ctx->timing)
+        (void)hipEventElapsedTime(&ctx->last_ranges_ms, ctx->ev[6], ctx->ev[7]);
+    if (passes_out) *passes_out = passes;
+    gs_ctx::ctl_check(ctx->h_pin[64 + 8 * 256], "sort");
 }
 
 int gs_sort_pairs_u64_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n, int begin_bit,
@@ -1572,25 +1747,25 @@ int gs_sort_pairs_u64_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n
         REQUIRE(ctx && keys && vals, "null argument");
         REQUIRE(n >= 0 && n < ((int64_t)1 << 32) - 1, "n out of range");
         REQUIRE(0 <= begin_bit && begin_bit < end_bit && end_bit <= 64, "bad bit range");
-        HIPCHK(hipSetDevice(ctx->device));
-        ctx->drain_spec();
-        ctx->ensure_counters();
-        ctx->ensure_sort(n, 8);
-        ctx->sync();
-        int passes = 0;
-        void* kf = nullptr;
-        uint32_t* vf = nullptr;
-        HIPCHK(gs::radix_sort_pairs(keys, vals, n, 8, begin_bit, end_bit, ctx->sort,
-                                    ctx->h_pin + 64, ctx->st, &passes, false, &kf, &vf));
-        if (kf != keys) {
-            HIPCHK(hipMemcpyAsync(keys, kf, (size_t)n * 8, hipMemcpyDeviceToDevice, ctx->st));
-            HIPCHK(hipMemcpyAsync(vals, vf, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->st));
-        }
-        ctx->sync();
-        ctx->last_sort_passes = passes;
-        if (passes_out) *passes_out = passes;
+        sort_u64_dev(ctx, keys, vals, n, begin_bit, end_bit, 0, nullptr, passes_out);
     });
 }
+
+int gs_sort_tile_depth_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n,
+                           int64_t num_tiles, uint32_t* tile_ranges, int* passes_out) {
+    return guard([&] {
+        REQUIRE(ctx && keys && vals && tile_ranges, "null argument");
+        REQUIRE(n >= 0 && n < ((int64_t)1 << 32) - 1, "n out of range");
+        REQUIRE(num_tiles >= 1 && num_tiles <= ((int64_t)1 << 31), "num_tiles out of range");
+        if (ctx->timing)
+            for (int i : {6, 7})
+                if (!ctx->ev[i]) HIPCHK(hipEventCreate(&ctx->ev[i]));
+        sort_u64_dev(ctx, keys, vals, n, 0, 32 + tile_bits(num_tiles), num_tiles, tile_ranges,
+                     passes_out);
+    });
+}
+
+float gs_last_ranges_ms(gs_ctx* ctx) { return ctx ? ctx->last_ranges_ms : 0.0f; }
 
 int gs_last_sort_pass_ms(gs_ctx* ctx, float* ms, int max_passes) {
     if (!ctx || !ctx->timing) return 0;

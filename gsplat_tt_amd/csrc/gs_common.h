@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "gs_internal.h"
+
 #define GS_WAVE 64
 
 namespace gs {
@@ -64,29 +66,62 @@ __device__ __forceinline__ void hist_add_wave(uint32_t* hist, uint32_t bin, bool
 }
 
 // ---------------------------------------------------------------------------
+// Control words of a launch (ctl, may be null): ctl[0] collects error flags
+// (kErrLookback: a bounded look-back wait gave up, so a prefix may be wrong),
+// ctl[1] is the wait's spin limit (0: kLbMaxSpins). The host clears ctl[0]
+// before the launches and turns a nonzero value into an error status.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kLbMaxSpins = 1u << 24;
+
+// Read only when a wait happens, with a plain load (the host wrote it before
+// the launch): an atomic load of one address by every wave would serialise.
+__device__ __forceinline__ uint32_t spin_limit(const uint32_t* ctl) {
+    const uint32_t v = ctl != nullptr ? ctl[1] : 0u;
+    return v != 0u ? v : kLbMaxSpins;
+}
+__device__ __forceinline__ void report_error(uint32_t* ctl, uint32_t bits) {
+    if (ctl != nullptr) __hip_atomic_fetch_or(ctl, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// True once a launch earlier in the sequence raised an error flag. Kernels
+// whose indices come from a look-back result (compaction slots, scan offsets,
+// sorted ids) return at once then, before taking a ticket: their inputs may
+// be wrong, so they write nothing and read nothing through them, and the host
+// reports the error.
+// A plain load: a flag that matters here was raised by an earlier launch, and
+// launch boundaries make it visible (an agent-scope atomic load of the one
+// address by every workgroup would serialise on it).
+__device__ __forceinline__ bool upstream_failed(const uint32_t* ctl) {
+    return ctl != nullptr && *ctl != 0u;
+}
+
+// ---------------------------------------------------------------------------
 // Decoupled look-back over a chain of 64-bit partition descriptors.
 // Descriptor = flag (2 bits, 62..63) | value (62 bits). flag 0 = not yet
 // published, 1 = aggregate of this partition only, 2 = inclusive prefix.
 // The caller is one full wave (all 64 lanes) of the partition with virtual id
 // `vid` (taken from an atomic ticket, so every predecessor is already
-// resident and never waits on us). Returns the exclusive prefix.
+// resident and never waits on us). Returns the exclusive prefix. The wait for
+// an unpublished predecessor is bounded: after spin_limit(ctl) rounds the wave
+// goes on with what it has and flags kErrLookback in ctl[0].
 // ---------------------------------------------------------------------------
 constexpr uint64_t kLbAgg = 1ull << 62;
 constexpr uint64_t kLbInc = 2ull << 62;
 constexpr uint64_t kLbVal = (1ull << 62) - 1;
-constexpr uint32_t kLbMaxSpins = 1u << 24;
 
 __device__ __forceinline__ uint64_t lookback_exclusive(uint64_t* state, uint32_t vid,
-                                                      uint64_t aggregate) {
+                                                      uint64_t aggregate, uint32_t* ctl) {
     const int l = lane_id();
     if (vid == 0) {
         if (l == 0) st_agent(&state[0], kLbInc | aggregate);
         return 0;
     }
     if (l == 0) st_agent(&state[vid], kLbAgg | aggregate);
+    uint32_t limit = 0;  // read at the first wait
     uint64_t excl = 0;
     int64_t base = (int64_t)vid - 1;
     uint32_t spins = 0;
+    bool gave_up = false;
     while (true) {
         const int64_t idx = base - l;
         uint64_t s = (idx >= 0) ? ld_agent(&state[idx]) : (kLbInc | 0ull);
@@ -102,12 +137,14 @@ __device__ __forceinline__ uint64_t lookback_exclusive(uint64_t* state, uint32_t
             need = ~0ull;
         }
         if ((rdy_mask & need) != need) {
-            // Bounded wait: predecessors are resident (ticket order), so this
-            // only trips on a broken chain; better a wrong count than a hang.
-            if (++spins < kLbMaxSpins) {
+            // predecessors are resident (ticket order), so this only trips on
+            // a broken chain or a host-set tiny limit: report, never hang
+            if (limit == 0) limit = spin_limit(ctl);
+            if (++spins < limit) {
                 __builtin_amdgcn_s_sleep(1);
                 continue;
             }
+            gave_up = true;
         }
         uint64_t v = ((need >> l) & 1ull) ? (s & kLbVal) : 0ull;
 #pragma unroll
@@ -116,7 +153,10 @@ __device__ __forceinline__ uint64_t lookback_exclusive(uint64_t* state, uint32_t
         if (inc_mask) break;
         base -= GS_WAVE;
     }
-    if (l == 0) st_agent(&state[vid], kLbInc | (excl + aggregate));
+    if (l == 0) {
+        if (gave_up) report_error(ctl, kErrLookback);
+        st_agent(&state[vid], kLbInc | (excl + aggregate));
+    }
     return excl;
 }
 

@@ -8,6 +8,13 @@
 
 namespace gs {
 
+// Error flags that kernels raise in ctl[0], the first of a launch's two
+// control words (ctl[1]: the spin limit of a bounded look-back wait, 0 for the
+// default). The host clears the flags before a launch sequence and turns any
+// raised flag into an error status.
+constexpr uint32_t kErrLookback = 1u;  // a look-back wait gave up: a prefix may be wrong
+constexpr uint32_t kErrKeyRange = 2u;  // a sorted key's tile id is past the tile count
+
 // Scene resident in HBM, structure-of-arrays (one coalesced dword stream per
 // attribute). `sh` holds (d+1)^2*3 planes of n floats, plane index k*3+c.
 struct SceneDev {
@@ -46,6 +53,7 @@ struct ProjParams {
     // per projection partition: nonzero = no Gaussian of it can reach the image
     // (its loads are skipped); nullptr = no partition is skipped
     const uint8_t* skip;
+    uint32_t* ctl;             // control words (gs_common.h), may be null
 };
 
 // Compact (visible-only) Gaussian records, index m in [0, M).
@@ -95,6 +103,7 @@ struct SortTemp {
     int half = 0;
     hipEvent_t* pass_events = nullptr;  // optional: 2 per pass (start, stop)
     int max_timed_passes = 0;
+    uint32_t* ctl = nullptr;       // control words of the passes (gs_common.h)
 };
 size_t sort_partitions(int64_t n);
 size_t sort_state_bytes(int64_t n);
@@ -126,6 +135,7 @@ hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const
 struct TileParams {
     int tiles_x, tiles_y, tile_size;
     int cull;          // per-pair Mahalanobis cull on
+    uint32_t* ctl;     // control words (gs_common.h), may be null
 };
 // offs: exclusive scan of rectangle areas in `order`; bstart[b]: rank owning
 // candidate b*emit_part (b < bstart_cap).
@@ -169,6 +179,10 @@ hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, const uin
 // O(tiles * log p) keys instead of all p; no clearing pass).
 hipError_t launch_tile_bounds(const uint32_t* sorted_tile, uint32_t p_cap, const uint32_t* p_dev,
                               uint32_t* ranges, int64_t num_tiles, hipStream_t st);
+// The same ranges over (tile << 32 | depth bits) keys sorted ascending; a tile
+// id >= num_tiles is flagged kErrKeyRange in ctl[0] (its keys get no range).
+hipError_t launch_tile_bounds64(const uint64_t* sorted_keys, uint32_t p, uint32_t* ranges,
+                                int64_t num_tiles, uint32_t* ctl, hipStream_t st);
 // out[c] += sum over rows of part[r][c] (out must be cleared by the caller).
 hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,
                               const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
@@ -194,9 +208,17 @@ struct BlendParams {
     // evaluations, entry batches, apply iterations, kept (entry, microblock)
     // pairs, max apply iterations of one wave
     unsigned long long* evals;
+    const uint32_t* ctl;  // control words of the frame (nothing is read after an error)
 };
 hipError_t launch_blend(const float4* brec, const uint32_t* sorted_id, const uint32_t* ranges,
                         BlendParams bp, void* out, hipStream_t st);
+// Counts of the reference's microblock cull over the tile-sorted pairs (ids
+// `sid`, tile ids `stile`, min(p_cap, *p_dev) of them): out[0] += pairs kept by
+// no microblock, out[1] += kept (pair, microblock) pairs.
+hipError_t launch_mb_stats(const float4* brec, const uint32_t* sid, const uint32_t* stile,
+                           uint32_t p_cap, const uint32_t* p_dev, int tiles_x, int tile_size,
+                           int cull_disabled, unsigned long long* out, const uint32_t* ctl,
+                           hipStream_t st);
 
 // ---- train.hip: training step (3DGS forward rules, L1, backward, sparse Adam)
 constexpr int kMaxTrainPlanes = 64;  // 11 geometry/opacity planes + 3 (d+1)^2 SH planes
@@ -220,6 +242,7 @@ struct TrainCam {
     float ccx, ccy, ccz;       // camera centre -R^T t
     float near, lowpass, alpha_min;
     int H, W;
+    uint32_t* ctl;             // control words (gs_common.h), may be null
 };
 
 // Optional Gaussian-indexed copies of the projection values (parity tests).
@@ -243,6 +266,7 @@ struct TrainFwdParams {
     float* dimage;         // dL/dimage (H,W,3), written with a target
     float grad_scale;      // loss_scale / (3HW)
     double* loss;          // accumulates sum |image - target|
+    const uint32_t* ctl;   // control words of the forward (nothing is read after an error)
 };
 
 // Full 3DGS loss terms (1 - lambda) L1 + lambda (1 - SSIM) on an (H,W,3) image.

@@ -226,7 +226,7 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
         }
     }
     if (w == 0) {
-        const uint64_t excl = lookback_exclusive(lb_state, vid, total);
+        const uint64_t excl = lookback_exclusive(lb_state, vid, total, p.ctl);
         if (lane == 0) {
             s_excl = excl;
             if (vid == gridDim.x - 1) *count_out = (uint32_t)(excl + total);

@@ -10,6 +10,17 @@
 // Extensions, all keyword-only with defaults that keep the reference's
 // behaviour: `output` ("u8" default, "bf16" as uint16 bits, "f32") and SH
 // colours (colors of shape (N, K, 3), K = (d+1)^2, evaluated on the GPU).
+// The u8 image is the bf16 image packed as img_pack_u8.h:9-14 does
+// (uint8(clip(float(bf16), 0, 1) * 255), truncation), the reference's
+// render_view output.
+//
+// One deliberate difference: the reference's device render_view ignores
+// contrib_floor, transmittance_threshold, k_cap and use_isoellipse
+// (render.cpp:274-278; its device path bakes its own values). Here they act
+// as in the CPU renderer that defines this path's results
+// (_gsplat_cpu.render_full, backends/cpu_cpp/pybind_module.cpp:2071-2091):
+// with the values run.py passes (contrib_floor = mb_contrib_floor, threshold
+// 1/255, k_cap 3, no isoellipse) both agree.
 //
 // Zero-copy output, on by default as in the reference (render.cpp:334-340,
 // 598-612; env_config.h:251-277): the returned image is a pinned buffer of the
@@ -43,9 +54,12 @@ gs_ctx* g_ctx = nullptr;
 uint64_t g_scene_version = 0;
 
 struct Timings {
-    int64_t views = 0;
+    int64_t views = 0, xview_hits = 0, xview_misses = 0;
     double project = 0, depth_sort = 0, tile_assign = 0, tile_sort = 0, blend = 0, view_total = 0;
 } g_t;
+// the view announced by the last call's next_extrinsics (xview hit accounting)
+bool g_have_next = false;
+gs_view g_next{};
 
 void check(int rc) {
     if (rc == GS_OK) return;
@@ -190,6 +204,12 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
             check(gs_render_next(c, &v, out, 0, ne ? &nv : nullptr, &st));
         }
         g_t.views++;
+        if (g_have_next) {
+            if (std::memcmp(&g_next, &v, sizeof(gs_view)) == 0) g_t.xview_hits++;
+            else g_t.xview_misses++;
+        }
+        g_have_next = (bool)ne;
+        if (ne) g_next = nv;
         g_t.project += st.ms_project;
         g_t.depth_sort += st.ms_depth_sort;
         g_t.tile_assign += st.ms_tile_assign;
@@ -252,16 +272,43 @@ PYBIND11_MODULE(render_clean, m) {
         g_ctx = nullptr;
         g_chunk_on = false;
         g_chunk_k = 1.5;
+        g_have_next = false;
     });
+    // Totals in ms over every render_view since reset_stage_timings, under the
+    // reference's keys (render/host/render.cpp:662-720): project (projection +
+    // depth sort), tile_assign, sort (tile sort), blend (microblock cull + blend,
+    // one kernel), view_total (wall clock), xview_hits / xview_misses (calls whose
+    // view was / was not the one the previous call announced). The device
+    // stages are hipEvent times. Keys of Tenstorrent sub-steps that this path
+    // does not have (head, blend_setup, mat, cull, d2h, assemble, tail, xview,
+    // sort_*, project_cov3d, project_pfwc_*, project_gather_*, tile_assign_*)
+    // are present and stay 0.0; depth_sort is this path's own extra key.
     m.def("stage_timings", []() {
         py::dict d;
         d["views"] = g_t.views;
-        d["project"] = g_t.project;
+        for (const char* k : {"head", "blend_setup", "mat", "cull", "d2h", "assemble", "tail",
+                              "xview", "sort_pread", "sort_bin_count", "sort_bin_hist_d2h",
+                              "sort_bin_layout", "sort_upload", "sort_bin_emit", "sort_kernel",
+                              "sort_d2h", "sort_compact", "sort_publish_host",
+                              "sort_publish_wait", "sort_mat", "sort_pre", "sort_log",
+                              "sort_cont_prep", "sort_cont_rtargs", "sort_cont_other",
+                              "project_cov3d", "project_pfwc_setup", "project_pfwc_rtargs",
+                              "project_pfwc_chunkcull", "project_pfwc_enqueue",
+                              "project_pfwc_finish", "project_gather_setup",
+                              "project_gather_rtargs", "project_gather_enqueue",
+                              "project_gather_wait", "project_gather_result",
+                              "tile_assign_setup", "tile_assign_rtargs", "tile_assign_enqueue",
+                              "tile_assign_scan_finish", "tile_assign_p_d2h",
+                              "tile_assign_k2_finish", "tile_assign_publish"})
+            d[k] = 0.0;
+        d["project"] = g_t.project + g_t.depth_sort;
         d["depth_sort"] = g_t.depth_sort;
         d["tile_assign"] = g_t.tile_assign;
         d["sort"] = g_t.tile_sort;
         d["blend"] = g_t.blend;
         d["view_total"] = g_t.view_total;
+        d["xview_hits"] = g_t.xview_hits;
+        d["xview_misses"] = g_t.xview_misses;
         return d;
     });
     m.def("reset_stage_timings", []() { g_t = Timings{}; });

@@ -151,8 +151,9 @@ __device__ __forceinline__ void digit_publish(DT* state, uint32_t vid, int digit
 
 template <typename D, typename DT>
 __device__ __forceinline__ uint32_t digit_walk(DT* state, uint32_t vid, int digit, uint32_t agg,
-                                               uint32_t epoch) {
+                                               uint32_t epoch, uint32_t* ctl) {
     if (vid == 0) return 0u;
+    uint32_t limit = 0;  // read at the first wait
     uint32_t excl = 0;
     int64_t j = (int64_t)vid - 1;
     uint32_t spins = 0;
@@ -175,10 +176,13 @@ __device__ __forceinline__ uint32_t digit_walk(DT* state, uint32_t vid, int digi
         }
         j -= used;
         if (!done && used < kLbBatch) {
-            // bounded wait (see lookback_exclusive): never hang the GPU
-            if (++spins < kLbMaxSpins) {
+            // bounded wait (see lookback_exclusive): never hang the GPU; a
+            // give-up is reported to the host through ctl
+            if (limit == 0) limit = spin_limit(ctl);
+            if (++spins < limit) {
                 __builtin_amdgcn_s_sleep(1);
             } else {
+                report_error(ctl, kErrLookback);
                 done = true;
             }
         }
@@ -197,7 +201,8 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     const K* __restrict__ kin, const uint32_t* __restrict__ vin, K* __restrict__ kout,
     uint32_t* __restrict__ vout, int64_t n_cap, const uint32_t* __restrict__ n_dev, int shift,
     int bits, const uint32_t* __restrict__ g_hist_pass, void* __restrict__ state_raw,
-    uint32_t* __restrict__ ticket, uint32_t epoch, uint32_t* __restrict__ clear_next) {
+    uint32_t* __restrict__ ticket, uint32_t epoch, uint32_t* __restrict__ clear_next,
+    uint32_t* ctl) {
     using D = Desc<D32>;
     using DT = typename D::T;
     DT* state = static_cast<DT*>(state_raw);
@@ -327,7 +332,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         }
     }
     if (tid < 256) {
-        const uint32_t excl = has_digit ? digit_walk<D, DT>(state, vid, tid, tot, epoch) : 0u;
+        const uint32_t excl = has_digit ? digit_walk<D, DT>(state, vid, tid, tot, epoch, ctl) : 0u;
         s_gpos[tid] = gbase + excl - loff;
     }
     __syncthreads();
@@ -431,7 +436,7 @@ hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uin
 #define GS_OS(IO, DD, DR)                                                                         \
     k_onesweep<K, IO, T, I, DD, DR, SP><<<grid, T, 0, st>>>(kin, vin, kout, vout, n_cap, n_dev,  \
                                                             shift, bits, hist_pass, state,       \
-                                                            ticket, epoch, clear_next)
+                                                            ticket, epoch, clear_next, tmp.ctl)
     if (drop) {
         if (iota || sizeof(K) != 4) return hipErrorInvalidValue;
         if (d32) GS_OS(false, true, true); else GS_OS(false, false, true);

@@ -122,9 +122,10 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
     __shared__ uint32_t s_wsum[kCountItems][kCountWaves];
     __shared__ uint64_t s_excl;
     const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
-    if (tid == 0) s_vid = atomicAdd(ticket, 1u);
+    if (tid == 0) s_vid = upstream_failed(tp.ctl) ? 0xFFFFFFFFu : atomicAdd(ticket, 1u);
     __syncthreads();
     const uint32_t vid = s_vid;
+    if (vid == 0xFFFFFFFFu) return;  // the depth order may be wrong: touch nothing
     // the grid may be sized for a capacity; the real count can live on the device
     const int64_t m = m_dev ? min(m_cap, (int64_t)*m_dev) : m_cap;
     const uint32_t nparts = (uint32_t)((m + kCountPart - 1) / kCountPart);
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
             total += s_wsum[it][ww];
         }
     if (w == 0) {
-        const uint64_t ex = lookback_exclusive(lb_state, vid, total);
+        const uint64_t ex = lookback_exclusive(lb_state, vid, total, tp.ctl);
         if (lane == 0) {
             s_excl = ex;
             if (vid == nparts - 1) {
@@ -237,12 +238,18 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     __shared__ uint32_t s_th[NDIG][256];
     __shared__ uint64_t s_excl;
     const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
-    if (COMPACT && tid == 0) s_vid = atomicAdd(ticket, 1u);
+    // one thread decides for the workgroup: after an earlier give-up the scan's
+    // offsets and owner table may be wrong, so touch nothing
+    if (tid == 0) {
+        const bool failed = upstream_failed(tp.ctl);
+        s_vid = failed ? 0xFFFFFFFFu : (COMPACT ? atomicAdd(ticket, 1u) : blockIdx.x);
+    }
     for (int i = tid; i < kEmitPart; i += kEmitThreads) s_own[i] = 0;
     if (part_hist != nullptr)
         for (int i = tid; i < NDIG * 256; i += kEmitThreads) (&s_th[0][0])[i] = 0;
     __syncthreads();
-    const uint32_t vid = COMPACT ? s_vid : blockIdx.x;
+    const uint32_t vid = s_vid;
+    if (vid == 0xFFFFFFFFu) return;
     const int64_t m = m_dev ? min(m_cap, (int64_t)*m_dev) : m_cap;
     const uint32_t p_pre = p_pre_dev ? min(p_pre_cap, *p_pre_dev) : p_pre_cap;
     const uint32_t nparts = (uint32_t)(((uint64_t)p_pre + kEmitPart - 1) / kEmitPart);
@@ -395,7 +402,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
             total += s_cnt[it][ww];
         }
     if (w == 0) {
-        const uint64_t ex = lookback_exclusive(lb_state, vid, total);
+        const uint64_t ex = lookback_exclusive(lb_state, vid, total, tp.ctl);
         if (lane == 0) {
             s_excl = ex;
             if (vid == nparts - 1) {
@@ -429,36 +436,46 @@ __global__ void k_tile_ranges(const uint32_t* __restrict__ st, uint32_t p_cap,
     }
 }
 
-// First index in [0, p) whose key is >= t, by a wave-wide 64-ary search
+// Tile id of a sorted key: the key itself (u32 tile keys) or its high word
+// ((tile << 32) | depth bits).
+__device__ __forceinline__ uint32_t tile_of(uint32_t k) { return k; }
+__device__ __forceinline__ uint32_t tile_of(uint64_t k) { return (uint32_t)(k >> 32); }
+
+// First index in [0, p) whose tile is >= t, by a wave-wide 64-ary search
 // (about log64(p) dependent loads). Keys are sorted ascending.
-__device__ __forceinline__ uint32_t wave_lower_bound(const uint32_t* __restrict__ keys,
-                                                     uint32_t p, uint32_t t, int lane) {
+template <typename K>
+__device__ __forceinline__ uint32_t wave_lower_bound(const K* __restrict__ keys, uint32_t p,
+                                                     uint32_t t, int lane) {
     uint32_t lo = 0, hi = p;  // answer in [lo, hi]
     while (hi - lo > (uint32_t)GS_WAVE) {
         const uint32_t step = (hi - lo + GS_WAVE - 1) / GS_WAVE;
         const uint64_t q = (uint64_t)lo + (uint64_t)(lane + 1) * step - 1;
-        const bool pred = q < hi && keys[q] < t;
+        const bool pred = q < hi && tile_of(keys[q]) < t;
         const uint32_t c = (uint32_t)__popcll(__ballot(pred));
         const uint64_t nhi = (uint64_t)lo + (uint64_t)(c + 1) * step - 1;
         lo += c * step;
         hi = (uint32_t)min((uint64_t)hi, nhi);
     }
     const uint32_t q = lo + (uint32_t)lane;
-    const bool pred = q < hi && keys[q] < t;
+    const bool pred = q < hi && tile_of(keys[q]) < t;
     return lo + (uint32_t)__popcll(__ballot(pred));
 }
 
-// ranges[t] = [first, end) of tile t in the tile-sorted pairs, (0, 0) when
-// empty; one wave per tile, no clearing pass needed.
-__global__ __launch_bounds__(256) void k_tile_bounds(const uint32_t* __restrict__ st,
-                                                     uint32_t p_cap,
+// ranges[t] = [first, end) of tile t in the tile-sorted keys, (0, 0) when
+// empty (sort.cpp:146-165); one wave per tile, no clearing pass needed. A key
+// whose tile is >= num_tiles (only the last key can show it) is flagged
+// kErrKeyRange in ctl; no range is written for it.
+template <typename K>
+__global__ __launch_bounds__(256) void k_tile_bounds(const K* __restrict__ st, uint32_t p_cap,
                                                      const uint32_t* __restrict__ p_dev,
                                                      uint32_t* __restrict__ ranges,
-                                                     uint32_t num_tiles) {
+                                                     uint32_t num_tiles, uint32_t* ctl) {
     const uint32_t p = p_dev ? min(p_cap, *p_dev) : p_cap;
     const uint32_t t = blockIdx.x * (256 / GS_WAVE) + threadIdx.x / GS_WAVE;
     const int lane = lane_id();
     if (t >= num_tiles) return;
+    if (t == 0 && lane == 0 && p > 0 && tile_of(st[p - 1]) >= num_tiles)
+        report_error(ctl, kErrKeyRange);
     const uint32_t a = wave_lower_bound(st, p, t, lane);
     const uint32_t b = wave_lower_bound(st, p, t + 1, lane);
     if (lane == 0) {
@@ -608,7 +625,17 @@ hipError_t launch_tile_bounds(const uint32_t* sorted_tile, uint32_t p_cap, const
                               uint32_t* ranges, int64_t num_tiles, hipStream_t st) {
     if (num_tiles <= 0) return hipSuccess;
     const unsigned grid = (unsigned)((num_tiles + 3) / 4);
-    k_tile_bounds<<<grid, 256, 0, st>>>(sorted_tile, p_cap, p_dev, ranges, (uint32_t)num_tiles);
+    k_tile_bounds<uint32_t><<<grid, 256, 0, st>>>(sorted_tile, p_cap, p_dev, ranges,
+                                                  (uint32_t)num_tiles, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_bounds64(const uint64_t* sorted_keys, uint32_t p, uint32_t* ranges,
+                                int64_t num_tiles, uint32_t* ctl, hipStream_t st) {
+    if (num_tiles <= 0) return hipSuccess;
+    const unsigned grid = (unsigned)((num_tiles + 3) / 4);
+    k_tile_bounds<uint64_t><<<grid, 256, 0, st>>>(sorted_keys, p, nullptr, ranges,
+                                                  (uint32_t)num_tiles, ctl);
     return hipGetLastError();
 }
 

@@ -282,7 +282,7 @@ __global__ __launch_bounds__(kTThreads) void k_train_project(
             total += s_cnt[it][ww];
         }
     if (w == 0) {
-        const uint64_t excl = lookback_exclusive(lb_state, vid, total);
+        const uint64_t excl = lookback_exclusive(lb_state, vid, total, cam.ctl);
         if (lane == 0) {
             s_excl = excl;
             if (vid == gridDim.x - 1) *count_out = (uint32_t)(excl + total);
@@ -317,6 +317,9 @@ __global__ __launch_bounds__(256) void k_train_fwd(const float4* __restrict__ tr
                                                    TrainFwdParams fp) {
     __shared__ float4 s0[256], s1[256], s2[256];
     __shared__ double s_loss[4];
+    // after an earlier give-up the sorted ids may be wrong: read nothing (the
+    // flag was raised by an earlier launch, so every thread sees the same value)
+    if (upstream_failed(fp.ctl)) return;
     const int tid = threadIdx.x;
     const int tile = blockIdx.x;
     const int tx = tile % fp.tiles_x, ty = tile / fp.tiles_x;

@@ -25,7 +25,8 @@ extern "C" {
 #define GS_E_DEVICE -2    /* HIP runtime / kernel failure (-> RuntimeError) */
 #define GS_E_CAPACITY -3  /* a size limit of this build was exceeded */
 
-#define GS_OUT_U8 0       /* uint8(clip(rgb,0,1)*255), truncation */
+#define GS_OUT_U8 0       /* u8 of the bf16 image: uint8(clip(float(bf16(rgb)),0,1)*255),
+                           truncation (render/kernels/dataflow/img_pack_u8.h:9-14) */
 #define GS_OUT_BF16 1     /* bf16, round to nearest even */
 #define GS_OUT_F32 2
 
@@ -81,6 +82,11 @@ typedef struct gs_stats {
     int64_t blend_kept;     /* kept (entry, microblock) pairs seen (timing on) */
     int64_t blend_max_iters; /* longest wave's apply iterations (timing on) */
     int64_t chunks_skipped;  /* projection partitions the chunk frustum skip ruled out */
+    /* The reference's microblock-cull counts (cull_and_blend.cpp:835-836, the
+     * pairs_dropped / pairs_kept_per_mb of render_full's stats), when
+     * gs_set_cull_stats is on; -1 otherwise. */
+    int64_t pairs_dropped_mb;  /* pairs that no microblock keeps */
+    int64_t pairs_kept_mb;     /* kept (pair, microblock) pairs */
 } gs_stats;
 
 /* ---- context -------------------------------------------------------- */
@@ -116,6 +122,28 @@ int gs_render_batch(gs_ctx* ctx, const gs_view* views, int n, void* const* outs,
  * drops an announced frame. */
 int gs_render_next(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device,
                    const gs_view* next_view, gs_stats* stats);
+
+/* The last gs_render frame of this context, read back for parity checks (the
+ * SortResult of src/gsplat_cpu/sort.cpp:146-165,217-257 after the frame's
+ * tile_assign, backends/cpu_cpp/pybind_module.cpp:1149-1575). counts (3):
+ * M, candidate pairs before the per-pair cull, P. sorted_ids (ids_cap >= P):
+ * the tile-sorted compact ids (compact id = rank among the visible Gaussians
+ * in source order, the reference's m), stable by (tile, depth bits, id).
+ * tile_ranges (num_tiles x 2, num_tiles = the frame's tile count): [start,
+ * end), (0, 0) for empty tiles. Any NULL output is skipped. GS_E_INVALID when
+ * no frame is held (a later call reused the frame buffers). */
+int gs_frame_readback(gs_ctx* ctx, int64_t* counts, int64_t* sorted_ids, int64_t ids_cap,
+                      int64_t* tile_ranges, int64_t num_tiles);
+/* Per-frame counts of the reference's microblock cull (gs_stats.pairs_dropped_mb,
+ * pairs_kept_mb; cull_and_blend.cpp:384-504,835-836): one more pass over the
+ * frame's pairs after the blend, off by default. */
+int gs_set_cull_stats(gs_ctx* ctx, int on);
+/* Spin limit of every bounded look-back wait of this context's kernels (0: the
+ * default, 2^24 rounds). A wait that reaches it goes on without the missing
+ * prefix and the call returns GS_E_DEVICE ("look-back wait gave up") instead of
+ * results; every kernel still exits normally. A tiny limit is for tests of that
+ * error path only. */
+int gs_set_spin_limit(gs_ctx* ctx, uint32_t limit);
 
 /* Chunk frustum skip (render/host/chunk_cull.h; GSPLAT_TT_CHUNK_CULL and
  * GSPLAT_TT_CHUNK_K of render/host/pfwc_device.cpp:214-240): per scene, the box of
@@ -190,6 +218,18 @@ int gs_sort_pairs_u64_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n
 /* Average device time (ms) of each onesweep pass kernel of the last
  * gs_sort_pairs_u64_dev call when timing is on; returns the pass count. */
 int gs_last_sort_pass_ms(gs_ctx* ctx, float* ms, int max_passes);
+/* The standalone tile/depth sort with its per-tile ranges: the stable sort of
+ * (u64 key, u32 value) by key bits [0, 32 + ceil(log2 num_tiles)) - keys are
+ * (tile << 32) | fp32 depth bits, tile < num_tiles - then tile_ranges (device,
+ * num_tiles x 2 u32) = [start, end) of each tile in the sorted keys, (0, 0)
+ * when empty. Replaces the bin + per-tile radix + range table of
+ * src/gsplat_cpu/sort.cpp:124-165,217-257 for a whole key array. A key with a
+ * tile id >= num_tiles gives GS_E_INVALID. */
+int gs_sort_tile_depth_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n,
+                           int64_t num_tiles, uint32_t* tile_ranges, int* passes_out);
+/* Device time (ms) of the range extraction of the last gs_sort_tile_depth_dev
+ * call when timing is on (0 otherwise). */
+float gs_last_ranges_ms(gs_ctx* ctx);
 
 /* ---- training (3DGS rules: forward, L1, backward, sparse Adam) ---------
  * Follows the reference's training oracle gsplat/train_oracle.py (forward

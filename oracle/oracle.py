@@ -104,6 +104,27 @@ def project(means, cov3d9, w2c, intr, colors, opac, H, W, min_opacity=1.0 / 255.
                 opacities=op[:M].copy() if opac is not None else None)
 
 
+def tile_count(means2d, radii, H, W, tile_size):
+    """tile_assign.cpp:60-111: candidate pairs before the per-pair cull (the sum
+    of the rectangle areas)."""
+    means2d, radii = _f(means2d), _f(radii)
+    return int(lib().orc_tile_count(_p(means2d, _f32p), _p(radii, _f32p),
+                                    ctypes.c_int64(means2d.shape[0]), ctypes.c_int(H),
+                                    ctypes.c_int(W), ctypes.c_int(tile_size)))
+
+
+def pack_u8(img_f32):
+    """The u8 image that the reference's render_view returns for an fp32 colour
+    image: bf16 round-to-nearest-even, then uint8(clip(float(bf16), 0, 1) * 255)
+    with truncation (render/kernels/dataflow/img_pack_u8.h:9-14; the product of
+    a bf16 and 255 is exact in fp32, so float arithmetic gives the integer rule's
+    result)."""
+    u = np.ascontiguousarray(img_f32, np.float32).view(np.uint32).astype(np.uint64)
+    b = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32) & 0xFFFF
+    f = (b << 16).astype(np.uint32).view(np.float32)
+    return (np.clip(f, np.float32(0), np.float32(1)) * np.float32(255)).astype(np.uint8)
+
+
 def tile_assign(means2d, radii, H, W, tile_size, covs2d=None, opac=None,
                 contrib_floor=1.0 / 16384.0):
     """tile_assign.cpp:26-368 -> (gaussian_ids, tile_ids) int64."""

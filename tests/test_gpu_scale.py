@@ -1,0 +1,190 @@
+"""Parity of the product frame path at every benchmark workload's stated size.
+
+The frame that ships (depth sort, pair emission with drop keys, tile sort whose
+first pass drops the culled slots, tile bounds, blend) is read back after
+gs_render (gs_frame_readback) and compared with the reference pipeline id for id:
+M, candidate pairs, P, tile-sorted ids (stable by tile, depth bits, id) and tile
+ranges bit-exact (src/gsplat_cpu/tile_assign.cpp:121-349, sort.cpp:146-165,
+217-257); images within max-abs 2e-3 and PSNR >= 55 dB (bf16 out) or 1e-5 (f32).
+
+  * 100K Gaussians at 640x480 (RGB, fp32 out);
+  * 1M Gaussians at 1280x720, SH degree 3, bf16 out;
+  * two views of the 64-view orbit of the 6M-Gaussian scene at 1237x822;
+  * the 50M-key tile/depth sort with its per-tile ranges, against numpy's
+    stable argsort;
+  * the 1M-Gaussian SH-1 training step at 1280x720 through size-independent
+    properties: the loss falls, only visible rows move, and central finite
+    differences of a linear image loss match the backward.
+"""
+import numpy as np
+import pytest
+
+from gsplat_tt_amd import _lib as L
+from gsplat_tt_amd import scenes
+from oracle import oracle as O
+from tests import oracle_frames as F
+
+pytestmark = pytest.mark.gpu
+
+
+def test_c1_100k_640x480_frame(gpu_ctx):
+    print("C1 100K frame", flush=True)
+    scene, cams = scenes.config1()
+    cam = cams[0]
+    cov = O.cov3d(scene.scales, scene.quats)
+    ref = F.frame(scene.means, cov, scene.opacities, scene.colors, cam, 16)
+    gpu_ctx.set_scene(scene.means, cov, scene.opacities, scene.colors)
+    for out in ("f32", "bf16"):
+        view = L.make_view(cam.w2c, cam.K, cam.height, cam.width, tile_size=16, output=out)
+        img, st = gpu_ctx.render(view)
+        F.check_frame(gpu_ctx, view, ref, img, st, bf16=out == "bf16", label=f"C1 {out}")
+
+
+def test_c2_1m_1280x720_sh3_frame(gpu_ctx):
+    print("C2 1M SH3 frame", flush=True)
+    scene, cams = scenes.config2()
+    cam = cams[0]
+    cov = scenes.cov3d(scene.scales, scene.quats)
+    rgb = O.sh_rgb(scene.means, scene.sh, 3, cam.w2c)
+    ref = F.frame(scene.means, cov, scene.opacities, rgb, cam, 16)
+    assert ref["M"] > 100_000 and ref["P"] > 500_000
+    gpu_ctx.set_scene(scene.means, cov, scene.opacities, scene.sh, sh_degree=3)
+    view = L.make_view(cam.w2c, cam.K, cam.height, cam.width, tile_size=16, output="bf16")
+    img, st = gpu_ctx.render(view)
+    F.check_frame(gpu_ctx, view, ref, img, st, bf16=True, label="C2")
+
+
+@pytest.fixture(scope="module")
+def c3_scene():
+    scene, cams = scenes.config3()
+    return scene, cams, scenes.cov3d(scene.scales, scene.quats)
+
+
+@pytest.mark.parametrize("view_index", [0, 21])
+def test_c3_6m_orbit_view_frame(gpu_ctx, c3_scene, view_index):
+    print(f"C3 6M orbit view {view_index}", flush=True)
+    scene, cams, cov = c3_scene
+    cam = cams[view_index]
+    rgb = O.sh_rgb(scene.means, scene.sh, 3, cam.w2c)
+    ref = F.frame(scene.means, cov, scene.opacities, rgb, cam, 16)
+    assert 20_000_000 <= ref["P"] <= 40_000_000, ref["P"]  # the scene's stated pair load
+    gpu_ctx.set_scene(scene.means, cov, scene.opacities, scene.sh, sh_degree=3)
+    view = L.make_view(cam.w2c, cam.K, cam.height, cam.width, tile_size=16, output="bf16")
+    img, st = gpu_ctx.render(view)
+    rb = F.check_frame(gpu_ctx, view, ref, img, st, bf16=True, label=f"C3 view {view_index}")
+    heaviest = int((rb["tile_ranges"][:, 1] - rb["tile_ranges"][:, 0]).max())
+    print(f"C3 view {view_index}: heaviest tile {heaviest} pairs", flush=True)
+
+
+def test_c4_50m_key_sort_with_tile_ranges(gpu_ctx):
+    print("C4 50M-key sort + ranges", flush=True)
+    n, tiles = 50_000_000, 5000
+    keys, vals = scenes.config4_keys(n=n, tiles=tiles)
+    dk, dv = gpu_ctx.dev_alloc(n * 8), gpu_ctx.dev_alloc(n * 4)
+    dr = gpu_ctx.dev_alloc(tiles * 8)
+    try:
+        gpu_ctx.h2d(dk, keys)
+        gpu_ctx.h2d(dv, vals)
+        passes = gpu_ctx.sort_tile_depth_dev(dk, dv, n, tiles, dr)
+        ko, vo = np.empty(n, np.uint64), np.empty(n, np.uint32)
+        rg = np.empty((tiles, 2), np.uint32)
+        gpu_ctx.d2h(ko, dk)
+        gpu_ctx.d2h(vo, dv)
+        gpu_ctx.d2h(rg, dr)
+    finally:
+        for p in (dk, dv, dr):
+            gpu_ctx.dev_free(p)
+    print(f"C4: {passes} passes", flush=True)
+    order = np.argsort(keys, kind="stable")
+    assert np.array_equal(vo, order.astype(np.uint32))
+    assert np.array_equal(ko, keys[order])
+    t = (ko >> np.uint64(32)).astype(np.int64)
+    lo = np.searchsorted(t, np.arange(tiles), "left")
+    hi = np.searchsorted(t, np.arange(tiles), "right")
+    empty = lo == hi
+    exp = np.stack([np.where(empty, 0, lo), np.where(empty, 0, hi)], 1)
+    assert np.array_equal(rg.astype(np.int64), exp)
+    print(f"C4: {int((~empty).sum())} non-empty tiles, largest {int((hi - lo).max())}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def c5_setup(gpu_ctx):
+    scene, tgt_scene, cams = scenes.config5()
+    cam = cams[0]
+    view = L.make_view(cam.w2c, cam.K, cam.height, cam.width, tile_size=16)
+    cfg = L.make_train_cfg()
+    tr_t = L.Trainer(gpu_ctx, scenes.train_params(tgt_scene), 1)
+    target, _, _, _ = tr_t.forward(view, cfg)
+    return scene, view, cfg, target
+
+
+def test_c5_1m_training_properties(gpu_ctx, c5_setup):
+    """Loss falls over steps; sparse Adam moves only the rows visible in the
+    step's forward (every parameter and moment of the other rows keeps its bits)."""
+    print("C5 1M training: loss and sparse rows", flush=True)
+    scene, view, cfg, target = c5_setup
+    params = scenes.train_params(scene)
+    tr = L.Trainer(gpu_ctx, params, 1)
+    _, _, proj, st0 = tr.forward(view, cfg, target, want_proj=True)
+    vis = proj["visible"]
+    assert 0 < vis.sum() < vis.size
+    tr.backward(cfg)
+    tr.adam(cfg)
+    after = tr.read(0)
+    m1 = tr.read(1)
+    for k in L.TRAIN_PARAMS:
+        a = np.asarray(after[k]).reshape(scene.n, -1)
+        b = np.asarray(params[k], np.float32).reshape(scene.n, -1)
+        assert np.array_equal(a[~vis].view(np.uint32), b[~vis].view(np.uint32)), k
+        assert not np.any(np.asarray(m1[k]).reshape(scene.n, -1)[~vis]), k
+    assert np.any(after["means"][vis] != params["means"][vis])
+    losses = [st0["loss"]]
+    for _ in range(12):
+        losses.append(tr.step(view, cfg, target)["loss"])
+    print(f"C5 losses {losses[0]:.6f} -> {losses[-1]:.6f}", flush=True)
+    assert losses[-1] < 0.9 * losses[0]
+
+
+def test_c5_1m_finite_differences(gpu_ctx, c5_setup):
+    """The backward of a linear image loss L = sum(w * image) (dL/dimage = w)
+    against central differences of the GPU forward, for the five largest
+    gradients of four kinds (mean x, log-scale y, opacity logit, SH DC red).
+    The forward's alpha_min skip and early stop make the image jump where a
+    pixel crosses them, by up to alpha_min (resp. t_min) per pixel, which the
+    analytic gradient leaves out and a central difference cannot avoid (the
+    number of crossings grows with the step); with both thresholds near zero the
+    forward is smooth and the two must agree."""
+    print("C5 1M training: finite differences", flush=True)
+    scene, view, _, _ = c5_setup
+    cfg = L.make_train_cfg(alpha_min=1e-7, t_min=1e-9)
+    params = scenes.train_params(scene)
+    tr = L.Trainer(gpu_ctx, params, 1)
+    H, W = view.image_height, view.image_width
+    w = np.random.default_rng(55).standard_normal((H, W, 3)).astype(np.float32)
+    tr.forward(view, cfg)
+    tr.backward(cfg, dimage=w)
+    grads = tr.read(3)
+
+    def loss(p):
+        tr.write(0, p)
+        img, _, _, _ = tr.forward(view, cfg)
+        return float(np.sum(w.astype(np.float64) * img.astype(np.float64)))
+
+    checks = [("means", 0, 2e-5), ("log_scales", 1, 2e-4), ("opacity_logits", 0, 2e-4),
+              ("sh", 0, 2e-4)]
+    for name, col, h in checks:
+        g = np.asarray(grads[name]).reshape(scene.n, -1)
+        for i in np.argsort(-np.abs(g[:, col]))[:5]:
+            i = int(i)
+            p_plus = {k: np.array(v, np.float32, copy=True) for k, v in params.items()}
+            p_minus = {k: np.array(v, np.float32, copy=True) for k, v in params.items()}
+            fp, fm = p_plus[name].reshape(scene.n, -1), p_minus[name].reshape(scene.n, -1)
+            x0 = float(fp[i, col])
+            fp[i, col] = np.float32(x0 + h)
+            fm[i, col] = np.float32(x0 - h)
+            span = float(fp[i, col]) - float(fm[i, col])
+            fd = (loss(p_plus) - loss(p_minus)) / span
+            an = float(g[i, col])
+            print(f"C5 FD {name}[{i},{col}]: analytic {an:.6g} numeric {fd:.6g}", flush=True)
+            assert abs(fd - an) <= 3e-2 * abs(an) + 1e-6, (name, i, an, fd)
+    tr.write(0, params)

@@ -99,3 +99,28 @@ def test_tile_assign_cull_vs_brute_force():
         if want != ((gi, ti) in kept) and abs(m2min - thr) > 1e-2 * max(thr, 1.0):
             mismatches += 1
     assert mismatches == 0
+
+
+def test_pack_u8_matches_reference_header():
+    """oracle.pack_u8 (bf16 round-to-nearest-even, then float clip * 255 with
+    truncation) against the reference's integer rule compiled from its own header
+    (render/kernels/dataflow/img_pack_u8.h:31-41, via oracle/img_pack_u8_dump.cpp)
+    for every bf16 pattern except NaN, plus fixed points of the rule."""
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(O.__file__), "_ref", "img_pack_u8_dump")
+    if not os.path.exists(exe):
+        pytest.skip("oracle/_ref/img_pack_u8_dump not built (reference sources absent)")
+    ref = np.array(subprocess.run([exe], check=True, capture_output=True,
+                                  text=True).stdout.split(), np.int64)
+    assert ref.shape == (65536,)
+    bits = np.arange(65536, dtype=np.uint32)
+    f = (bits << 16).view(np.float32)
+    ok = ~np.isnan(f)
+    got = O.pack_u8(f).astype(np.int64)   # a bf16 value rounds to itself
+    assert np.array_equal(got[ok], ref[ok])
+    # fixed points: 1.0 -> 255, 0.5 -> 127 (truncation), negatives and tiny -> 0
+    assert list(O.pack_u8(np.array([1.0, 0.5, -0.25, 1e-3, 2.0], np.float32))) == \
+        [255, 127, 0, 0, 255]
+    # rounding to bf16 happens first: 0.99999 rounds up to 1.0 -> 255
+    assert O.pack_u8(np.array([0.99999], np.float32))[0] == 255
