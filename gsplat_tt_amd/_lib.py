@@ -36,6 +36,7 @@ EXPORTED = (
     "gs_set_chunk_cull",
     "gs_frame_readback", "gs_set_cull_stats", "gs_set_spin_limit",
     "gs_sort_tile_depth_dev", "gs_last_ranges_ms",
+    "gs_sort_tile_depth_noalloc",
 )
 TRAIN_PARAMS = ("means", "log_scales", "quats", "opacity_logits", "sh")
 

@@ -1301,6 +1301,9 @@ struct gs_ctx {
 
 };
 
+gs::CtxInfo gs::ctx_info(const gs_ctx* ctx) { return gs::CtxInfo{ctx->device, ctx->st}; }
+void gs::set_last_error(const char* msg) { g_err = msg ? msg : ""; }
+
 extern "C" {
 
 const char* gs_last_error(void) { return g_err.c_str(); }

@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+struct gs_ctx;  // include/gsplat_hip.h
+
 namespace gs {
 
 // Error flags that kernels raise in ctl[0], the first of a launch's two
@@ -106,6 +108,11 @@ struct SortTemp {
     uint32_t* ctl = nullptr;       // control words of the passes (gs_common.h)
 };
 size_t sort_partitions(int64_t n);
+// Adds the digit histograms of every pass of radix_sort_pairs_dev over 64-bit
+// keys (digits of sort_digit_width(end_bit - begin_bit) bits, 256 words per
+// pass) into hist, which the caller clears.
+hipError_t launch_digit_hist_u64(const uint64_t* keys, int64_t n, int begin_bit, int end_bit,
+                                 uint32_t* hist, hipStream_t st);
 size_t sort_state_bytes(int64_t n);
 size_t sort_hist_words();
 // Stable sort of (keys, vals) by key bits [begin_bit, end_bit). key_bytes = 4
@@ -130,6 +137,15 @@ hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const
                                 uint32_t* tickets, SortTemp& tmp, hipStream_t st, bool vals_iota,
                                 void** keys_final, uint32_t** vals_final,
                                 const uint32_t* n_kept_dev = nullptr);
+
+// Device and stream of a context (gs_api.cpp), for entry points in other units.
+struct CtxInfo {
+    int device;
+    hipStream_t stream;
+};
+CtxInfo ctx_info(const ::gs_ctx* ctx);
+// Sets the calling thread's gs_last_error() message.
+void set_last_error(const char* msg);
 
 // ---- tiles.hip
 struct TileParams {

@@ -85,7 +85,7 @@ constexpr int kHistItems = 4;
 template <typename K>
 __global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ keys, int64_t n,
                                                        int begin_bit, int end_bit, int npass,
-                                                       uint32_t* __restrict__ g_hist) {
+                                                       int dw, uint32_t* __restrict__ g_hist) {
     __shared__ uint32_t h[kWaves][kMaxPasses][256];
     const int w = threadIdx.x / GS_WAVE;
     const int lane = lane_id();
@@ -108,8 +108,8 @@ __global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ key
         // passes outside, items inside: the items' digit tests of one pass are
         // independent and interleave
         for (int p = 0; p < npass; ++p) {
-            const int shift = begin_bit + 8 * p;
-            const uint32_t mask = (1u << min(8, end_bit - shift)) - 1u;
+            const int shift = begin_bit + dw * p;
+            const uint32_t mask = (1u << min(dw, end_bit - shift)) - 1u;
             uint32_t d[kHistItems], d0[kHistItems];
             uint64_t same[kHistItems];
 #pragma unroll
@@ -482,7 +482,7 @@ hipError_t sort_impl(K* keys, uint32_t* vals, int64_t n, int begin_bit, int end_
     }
     const unsigned hgrid =
         (unsigned)std::min<int64_t>((n + kHistThreads * kHistItems - 1) / (kHistThreads * kHistItems), 2048);
-    k_hist<K><<<hgrid, kHistThreads, 0, st>>>(keys, n, begin_bit, end_bit, npass, tmp.hist);
+    k_hist<K><<<hgrid, kHistThreads, 0, st>>>(keys, n, begin_bit, end_bit, npass, 8, tmp.hist);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = hipMemcpyAsync(host_hist, tmp.hist, (size_t)npass * 256 * 4,
                             hipMemcpyDeviceToHost, st)) != hipSuccess)
@@ -586,6 +586,18 @@ hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const
 }
 
 size_t sort_partitions(int64_t n) { return (size_t)((n + kMinPart - 1) / kMinPart); }
+
+hipError_t launch_digit_hist_u64(const uint64_t* keys, int64_t n, int begin_bit, int end_bit,
+                                 uint32_t* hist, hipStream_t st) {
+    const int npass = (end_bit - begin_bit + 7) / 8;
+    if (n <= 0) return hipSuccess;
+    if (npass <= 0 || npass > kMaxPasses) return hipErrorInvalidValue;
+    const int dw = sort_digit_width(end_bit - begin_bit);
+    const unsigned grid = (unsigned)std::min<int64_t>(
+        (n + kHistThreads * kHistItems - 1) / (kHistThreads * kHistItems), 2048);
+    k_hist<uint64_t><<<grid, kHistThreads, 0, st>>>(keys, n, begin_bit, end_bit, npass, dw, hist);
+    return hipGetLastError();
+}
 size_t sort_state_bytes(int64_t n) { return sort_partitions(n) * 256 * sizeof(uint64_t); }
 size_t sort_hist_words() { return (size_t)kMaxPasses * 256 + kMaxPasses; }
 

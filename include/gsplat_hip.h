@@ -230,6 +230,17 @@ int gs_sort_tile_depth_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t 
 /* Device time (ms) of the range extraction of the last gs_sort_tile_depth_dev
  * call when timing is on (0 otherwise). */
 float gs_last_ranges_ms(gs_ctx* ctx);
+/* gs_sort_tile_depth_dev with no allocation of any kind. It has no counterpart
+ * in the reference: it is for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). Its
+ * scratch (ping-pong keys and values, look-back descriptors, digit histograms,
+ * control words) is one file-scope device array of 12.5 MiB per GPU, held
+ * until the process ends, so n is at most 2^20 keys (larger n: GS_E_CAPACITY,
+ * nothing done). Calls that overlap on one GPU share that array and race;
+ * each call clears what must start at zero. Same results as
+ * gs_sort_tile_depth_dev on the context's stream. */
+int gs_sort_tile_depth_noalloc(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n,
+                               int64_t num_tiles, uint32_t* tile_ranges, int* passes_out);
 
 /* ---- training (3DGS rules: forward, L1, backward, sparse Adam) ---------
  * Follows the reference's training oracle gsplat/train_oracle.py (forward
