@@ -1,6 +1,7 @@
 """Benchmark: forward render of the 6M-Gaussian scene (SH degree 3, 1237x822,
-16x16 tiles, 64-view orbit) on one MI355X, plus the standalone 50M-key
-tile/depth radix sort, with roofline figures and the CPU baseline.
+16x16 tiles, 64-view orbit) on one MI355X, plus the 100K and 1M single-view
+renders, the standalone 50M-key tile/depth radix sort with its per-tile ranges
+and the 1M-Gaussian training step, with roofline figures and the CPU baselines.
 
 Contract: `python bench.py --gpus N --steps K --warmup W` prints ONE JSON line.
 A step is one frame: the whole five-stage pipeline of one orbit view, from the
@@ -21,12 +22,14 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
-FP32_PEAK_TFLOPS = 157.3     # MI355X FP32 vector peak
+FP32_PEAK_TFLOPS = 157.3     # MI355X FP32 peak (packed FP32 VALU issue)
 # per pixel x Gaussian evaluation: dx, dy (2 sub), quadratic form (3 mul + 2 FMA),
 # clamp, exp, alpha (mul + min), alpha*T, 3 colour FMA, T update; FMA = 2 flops
 BLEND_FLOPS_PER_EVAL = 20
 # frame slots of gs_render_batch; one output buffer per slot
 FRAMES_IN_FLIGHT = 3
+# host threads of one GPU's share of the box (its worker pools are sized to it)
+BOX_CPU_SHARE = 16
 
 
 def log(msg):
@@ -49,7 +52,12 @@ def parse():
     ap.add_argument("--no-morton", action="store_true",
                     help="skip the Morton-ordered orbit with the chunk frustum skip")
     ap.add_argument("--cpu-frames", type=int, default=10)
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="CPU baseline threads (0: the process's logical cores, at most the "
+                         "box's share of one GPU)")
+    ap.add_argument("--no-views", action="store_true",
+                    help="skip the 100K and 1M single-view legs")
+    ap.add_argument("--view-steps", type=int, default=64)
     ap.add_argument("--sequential-frames", type=int, default=0, metavar="K",
                     help="only render K orbit views one at a time (device output, no frames "
                          "in flight): the per-kernel split of a frame under a kernel trace")
@@ -99,13 +107,14 @@ def bench_frames(args):
     return ctx, scene, cov, cams, stats, dt
 
 
-def stage_summary(scene, stats):
-    """Per-stage times (hipEvents on the render stream) and roofline figures from
-    the per-unit algorithmic work: projection N*(12+24+4+12*(d+1)^2) B read +
-    M*48 B written; tile assignment M*40 B read + P*12 B written; sort 16 B per
-    key per 8-bit pass (u32 key + u32 payload, read + write) over the depth keys
-    (M, 4 passes) and the tile keys (P, tile-bit passes); blend 20 FP32 flops per
-    pixel-Gaussian evaluation."""
+def stage_summary(n, sh_degree, tiles, stats):
+    """Per-stage times (hipEvents on the render stream, frames rendered one at a
+    time) and roofline figures from the per-unit algorithmic work:
+    projection N*(12+24+4+12*(d+1)^2) B read + M*48 B written (d+1)^2 = 1 for RGB);
+    depth sort 16 B per key per pass, 4 passes over the M depth keys; tile
+    assignment M*40 B read + P*12 B written; tile sort 16 B per pair per pass over
+    P (passes: the tile bits spread over 8-bit-or-less digits); blend 20 FP32 flops
+    per pixel-Gaussian evaluation."""
     keys = ("ms_project", "ms_depth_sort", "ms_tile_assign", "ms_tile_sort", "ms_blend",
             "ms_total")
     avg = {k: float(np.mean([s[k] for s in stats])) for k in keys}
@@ -115,10 +124,11 @@ def stage_summary(scene, stats):
     evals = float(np.mean([s["blend_evals"] for s in stats]))
     diag = {k: float(np.mean([s[k] for s in stats])) for k in ("blend_batches", "blend_iters",
                                                                  "blend_kept", "blend_max_iters")}
-    N = scene.n
-    tile_passes = 2   # 4056 tiles of 16 px -> 12 tile bits
+    K = 1 if sh_degree < 0 else (sh_degree + 1) ** 2
+    tile_bits = max(1, math.ceil(math.log2(tiles)))
+    tile_passes = (tile_bits + 7) // 8
     work = {
-        "project": ("GB/s", N * (12 + 24 + 4 + 12 * 16) + M * 48),
+        "project": ("GB/s", n * (12 + 24 + 4 + 12 * K) + M * 48),
         "depth_sort": ("GB/s", M * 16 * 4),
         "tile_assign": ("GB/s", M * 40 + P * 12),
         "tile_sort": ("GB/s", P * 16 * tile_passes),
@@ -127,20 +137,43 @@ def stage_summary(scene, stats):
     roof = {}
     for k, (unit, amount) in work.items():
         sec = avg["ms_" + k] * 1e-3
+        if sec <= 0:
+            continue
         if unit == "GB/s":
             ach = amount / sec / 1e9
-            roof[k] = {"ms": round(avg["ms_" + k], 4), "achieved_gbs": round(ach, 1),
-                       "frac_hbm": round(ach / HBM_PEAK_GBS, 4)}
+            roof[k] = {"ms": round(avg["ms_" + k], 4), "bytes": round(amount),
+                       "achieved_gbs": round(ach, 1), "frac_hbm": round(ach / HBM_PEAK_GBS, 4)}
         else:
             ach = amount / sec / 1e12
-            roof[k] = {"ms": round(avg["ms_" + k], 4), "achieved_tflops": round(ach, 3),
+            roof[k] = {"ms": round(avg["ms_" + k], 4), "flops": round(amount),
+                       "achieved_tflops": round(ach, 3),
                        "frac_fp32": round(ach / FP32_PEAK_TFLOPS, 4)}
-    st = {
-        "N": N, "M_avg": M, "pairs_avg": P, "pairs_pre_avg": Ppre, "blend_evals_avg": evals,
+    return {
+        "N": n, "M_avg": M, "pairs_avg": P, "pairs_pre_avg": Ppre, "blend_evals_avg": evals,
         "blend_diag": diag, "ms": {k[3:]: round(v, 4) for k, v in avg.items()},
         "roofline": roof,
     }
-    return st, avg, evals * BLEND_FLOPS_PER_EVAL
+
+
+def dominant_roofline(st):
+    """The roofline object of the frame's dominant kernel: k_project (the project
+    stage is that one kernel plus a small histogram reduction, HBM-bound) or
+    k_blend (FP32 VALU-bound; no MFMA on this path), whichever takes longer."""
+    r = st["roofline"]
+    proj_ms, blend_ms = r["project"]["ms"], r["blend"]["ms"]
+    if blend_ms >= proj_ms:
+        b = r["blend"]
+        return {"kernel": "k_blend", "bound": "valu", "pipe": "fp32 VALU (no MFMA issued)",
+                "achieved": b["achieved_tflops"], "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": b["frac_fp32"], "traffic": pmc_traffic("k_blend"),
+                "flops_per_launch": b["flops"], "ms_per_launch": b["ms"],
+                "work_model": "20 FP32 flops per pixel-Gaussian evaluation"}
+    p = r["project"]
+    return {"kernel": "k_project", "bound": "hbm", "achieved": p["achieved_gbs"],
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": p["frac_hbm"],
+            "traffic": pmc_traffic("k_project"), "bytes_per_launch": p["bytes"],
+            "ms_per_launch": p["ms"],
+            "work_model": "N*(12+24+4+12*(d+1)^2) B read + M*48 B written"}
 
 
 def pmc_traffic(kernel):
@@ -253,53 +286,110 @@ def bench_host_out(ctx, cams, frames):
     return res
 
 
-def bench_sort(ctx, n):
+def bench_view(ctx, name, scene, cam, steps, warmup, cpu_frames, cpu_threads, out="bf16"):
+    """One workload's single view, rendered `steps` times through gs_render_batch
+    (three frames in flight), then 8 frames one at a time with per-stage events;
+    the reference's CPU renderer on the same view for the CPU figure."""
+    from gsplat_tt_amd import _lib as L
+    from gsplat_tt_amd import scenes
+
+    deg = scene.sh_degree if scene.sh is not None else -1
+    colors = scene.sh if scene.sh is not None else scene.colors
+    cov = scenes.cov3d(scene.scales, scene.quats)
+    ctx.set_scene(scene.means, cov, scene.opacities, colors, sh_degree=deg)
+    H, W = cam.height, cam.width
+    view = L.make_view(cam.w2c, cam.K, H, W, tile_size=16, output=out)
+    eb = {"bf16": 2, "f32": 4, "u8": 1}[out]
+    outs = [ctx.dev_alloc(H * W * 3 * eb) for _ in range(FRAMES_IN_FLIGHT)]
+    L._check(ctx._L.gs_set_timing(ctx.handle, 0))
+    ctx.render_batch([view] * warmup, [outs[i % FRAMES_IN_FLIGHT] for i in range(warmup)])
+    t0 = time.perf_counter()
+    ctx.render_batch([view] * steps, [outs[i % FRAMES_IN_FLIGHT] for i in range(steps)])
+    ctx._L.gs_sync(ctx.handle)
+    dt = time.perf_counter() - t0
+    L._check(ctx._L.gs_set_timing(ctx.handle, 1))
+    stats = [ctx.render_dev(view, outs[0]) for _ in range(8)]
+    for o in outs:
+        ctx.dev_free(o)
+    tiles = ((W + 15) // 16) * ((H + 15) // 16)
+    st = stage_summary(scene.n, deg, tiles, stats)
+    res = {"workload": f"{scene.n} Gaussians, {W}x{H}, "
+                       f"{'SH degree %d' % deg if deg >= 0 else 'RGB'}, 16x16 tiles, {out} out, "
+                       "one view", "frames": steps, "frames_per_s": round(steps / dt, 1),
+           "ms_per_frame": round(dt / steps * 1e3, 4), "stages": st,
+           "roofline": dominant_roofline(st)}
+    if cpu_frames > 0:
+        res["cpu_baseline"] = cpu_baseline(scene, cov, [cam], cpu_frames, cpu_threads,
+                                           f"{cpu_frames} renders of the {name} view after 1 "
+                                           "warm-up")
+    log(f"{name}: {res['frames_per_s']} frames/s, stages {st['ms']}")
+    return res
+
+
+def bench_sort(ctx, n, tiles=5000):
+    """The 50M-key tile/depth sort with its per-tile ranges (gs_sort_tile_depth_dev):
+    wall time from the host around the call (inputs restored outside it), the
+    bytes model keys*(24*passes + 8) over that wall time, the onesweep passes'
+    own event times, and the range extraction's."""
     from gsplat_tt_amd import scenes
 
     t = time.time()
-    keys, vals = scenes.config4_keys(n=n)
+    keys, vals = scenes.config4_keys(n=n, tiles=tiles)
     log(f"sort keys generated in {time.time() - t:.1f}s")
-    dk, dv = ctx.dev_alloc(n * 8), ctx.dev_alloc(n * 4)
+    dk, dv, dr = ctx.dev_alloc(n * 8), ctx.dev_alloc(n * 4), ctx.dev_alloc(tiles * 8)
     L = ctx._L
-    times, passes, pass_ms = [], 0, []
-    for rep in range(4):
+    times, passes, pass_ms, ranges_ms = [], 0, [], []
+    for rep in range(5):
         ctx.h2d(dk, keys)   # restore the unsorted input, outside the timed region
         ctx.h2d(dv, vals)
         L.gs_sync(ctx.handle)
         t0 = time.perf_counter()
-        passes = ctx.sort_pairs_u64_dev(dk, dv, n, 0, 45)
+        passes = ctx.sort_tile_depth_dev(dk, dv, n, tiles, dr)
         times.append(time.perf_counter() - t0)
         pass_ms.append(ctx.last_sort_pass_ms())
-    # spot-check: sortedness, tile ranges contiguity and permutation checksum
+        ranges_ms.append(ctx.last_ranges_ms())
+    # spot-check: sortedness, permutation checksum, a prefix against the input
     ko = np.empty(n, np.uint64)
     vo = np.empty(n, np.uint32)
+    rg = np.empty((tiles, 2), np.uint32)
     ctx.d2h(ko, dk)
     ctx.d2h(vo, dv)
+    ctx.d2h(rg, dr)
     ok = bool(np.all(ko[1:] >= ko[:-1])) and int(vo.astype(np.uint64).sum()) == n * (n - 1) // 2
     ok = ok and bool(np.array_equal(keys[vo[: 1 << 20]], ko[: 1 << 20]))
-    for p in (dk, dv):
+    ok = ok and int(rg[:, 1].max()) == n and int((rg[:, 1] - rg[:, 0]).astype(np.int64).sum()) == n
+    for p in (dk, dv, dr):
         ctx.dev_free(p)
-    best = min(times[1:]) if len(times) > 1 else times[0]
-    kernel_ms = float(np.mean([sum(p) for p in pass_ms[1:]])) if len(pass_ms) > 1 else float(sum(pass_ms[0]))
-    per_pass_ms = float(np.mean([np.mean(p) for p in pass_ms[1:] if p])) if len(pass_ms) > 1 else 0.0
+    best = min(times[1:])
+    kernel_ms = float(np.mean([sum(p) for p in pass_ms[1:]]))
+    per_pass_ms = float(np.mean([np.mean(p) for p in pass_ms[1:] if p]))
     bytes_total = n * (24 * passes + 8)
+    traffic = pmc_traffic("sort_50M")
+    ach = bytes_total / best / 1e9
     return {
-        "keys": n, "tiles": 5000, "zipf_s": 1.1, "passes": passes, "ok": ok,
-        "wall_ms": round(best * 1e3, 3), "kernel_ms": round(kernel_ms, 3),
+        "keys": n, "tiles": tiles, "zipf_s": 1.1, "passes": passes, "ok": ok,
+        "wall_ms": round(best * 1e3, 3), "passes_ms": round(kernel_ms, 3),
+        "ranges_ms": round(float(np.mean(ranges_ms[1:])), 4),
         "gkeys_per_s": round(n / best / 1e9, 3),
-        "gkeys_per_s_kernels": round(n / (kernel_ms * 1e-3) / 1e9, 3) if kernel_ms > 0 else None,
-        "roofline": {"bound": "hbm", "achieved": round(n * 24 / (per_pass_ms * 1e-3) / 1e9, 1)
-                     if per_pass_ms > 0 else None, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(n * 24 / (per_pass_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
-                     if per_pass_ms > 0 else None, "traffic": None,
-                     "bytes_model": f"keys*(24*passes+8) = {bytes_total}"},
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
+                     "bytes_model": f"keys*(24*passes+8) = {bytes_total}, over the wall time "
+                                    "of the sort call (histogram, passes, ranges)",
+                     "per_pass": {"ms": round(per_pass_ms, 4),
+                                  "achieved": round(n * 24 / (per_pass_ms * 1e-3) / 1e9, 1),
+                                  "frac": round(n * 24 / (per_pass_ms * 1e-3) / 1e9
+                                                / HBM_PEAK_GBS, 4)}},
     }
 
 
 def bench_train(ctx, n, steps):
     """Config 5: one training step = forward (3DGS rules) + L1 against a target +
     blend/projection backward + sparse Adam, fp32, 1M Gaussians, SH degree 1,
-    1280x720. The target is the GPU forward of the perturbed copy."""
+    1280x720. The target is the GPU forward of the perturbed copy. Rooflines:
+    sparse Adam reads param, m, v, grad (16 B) and writes param, m, v (12 B) per
+    scalar of the visible rows; the backward reads the 48-B forward record per
+    pair and adds 9 gradient terms per (Gaussian, tile) by atomics."""
     from gsplat_tt_amd import _lib as L
     from gsplat_tt_amd import scenes
 
@@ -312,6 +402,8 @@ def bench_train(ctx, n, steps):
     tr = L.Trainer(ctx, scenes.train_params(tgt_scene), 1)
     target, _, _, _ = tr.forward(view, cfg)
     tr = L.Trainer(ctx, scenes.train_params(scene), 1)
+    _, _, proj, _ = tr.forward(view, cfg, target, want_proj=True)
+    visible = int(proj["visible"].sum())
     H, W = cam.height, cam.width
     dt = ctx.dev_alloc(H * W * 12)
     ctx.h2d(dt, np.ascontiguousarray(target, np.float32))
@@ -334,13 +426,30 @@ def bench_train(ctx, n, steps):
     keys = ("ms_forward", "ms_backward", "ms_adam")
     avg = {k: float(np.mean([s[k] for s in stats])) for k in keys}
     avg_s = {k: float(np.mean([s[k] for s in stats_s])) for k in keys}
+    planes = 11 + 3 * 4
+    adam_bytes = visible * planes * 28
+    P = stats[-1]["num_entries"]
+    bwd_bytes = P * 48 + stats[-1]["num_blendable"] * 9 * 4 * 2
     return {"workload": "training step, 1M Gaussians (64-component mixture), SH degree 1, "
                         "1280x720, L1 vs render of a perturbed copy, sparse Adam, fp32",
             "steps": steps, "ms_per_step": round(el / steps * 1e3, 4),
             "steps_per_s": round(steps / el, 2),
             "ms": {k[3:]: round(v, 4) for k, v in avg.items()},
-            "M": stats[-1]["num_blendable"], "pairs": stats[-1]["num_entries"],
+            "M": stats[-1]["num_blendable"], "pairs": P, "visible_rows": visible,
             "loss_first": round(stats[0]["loss"], 6), "loss_last": round(stats[-1]["loss"], 6),
+            "roofline": {
+                "adam": {"bound": "hbm", "bytes": adam_bytes,
+                         "achieved": round(adam_bytes / (avg["ms_adam"] * 1e-3) / 1e9, 1),
+                         "frac": round(adam_bytes / (avg["ms_adam"] * 1e-3) / 1e9
+                                       / HBM_PEAK_GBS, 4),
+                         "model": "visible rows x 23 planes x (16 B read + 12 B write)"},
+                "backward": {"bound": "valu (per-pixel recomputation and wave sums)",
+                             "bytes": bwd_bytes,
+                             "achieved": round(bwd_bytes / (avg["ms_backward"] * 1e-3) / 1e9, 1),
+                             "frac": round(bwd_bytes / (avg["ms_backward"] * 1e-3) / 1e9
+                                           / HBM_PEAK_GBS, 4),
+                             "model": "pairs x 48 B records + M x 9 gradient terms "
+                                      "(read + write)"}},
             "full_loss": {"loss": "0.8 L1 + 0.2 (1 - SSIM)",
                           "ms_per_step": round(el_s / steps * 1e3, 4),
                           "steps_per_s": round(steps / el_s, 2),
@@ -349,36 +458,76 @@ def bench_train(ctx, n, steps):
                           "loss_last": round(stats_s[-1]["loss"], 6)}}
 
 
-def cpu_baseline(scene, cov, cams, frames, threads):
+def cpu_info():
+    """Logical cores this process may run on, the host's count, and the CPU model."""
+    n_os = os.cpu_count() or 1
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = n_os
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": aff, "os_cpu_count": n_os, "model": model}
+
+
+def sh_rgb_parallel(O, means, sh, deg, w2c, threads):
+    """The oracle's SH colour in `threads` slices at once (the C call releases
+    the GIL), so the CPU figure does not run its colour stage on one core."""
+    from concurrent.futures import ThreadPoolExecutor
+    n = means.shape[0]
+    cuts = np.linspace(0, n, threads + 1).astype(np.int64)
+    with ThreadPoolExecutor(threads) as ex:
+        parts = list(ex.map(lambda k: O.sh_rgb(means[cuts[k]:cuts[k + 1]],
+                                               sh[cuts[k]:cuts[k + 1]], deg, w2c),
+                            range(threads)))
+    return np.concatenate(parts, 0)
+
+
+def cpu_baseline(scene, cov, cams, frames, threads, sample):
     """The reference's own CPU renderer (_gsplat_cpu.render_full, compiled from its
     sources into oracle/_ref) on a bounded sample of the same workload; SH colour
-    evaluated on the CPU first (oracle, single thread) and included."""
+    (when the scene has SH) evaluated first on the same threads and included."""
+    info = cpu_info()
+    if threads <= 0:
+        threads = max(1, min(info["nproc"], BOX_CPU_SHARE))
     os.environ["GSPLAT_TT_NUM_THREADS"] = str(threads)
     from oracle import oracle as O
 
     R = O.ref_module()
-    kind = "reference"
+    kind = "reference" if R is not None else "port"
     times = []
     for i in range(frames + 1):
         cam = cams[(i * 7) % len(cams)]
         t0 = time.perf_counter()
-        rgb = O.sh_rgb(scene.means, scene.sh, 3, cam.w2c)
+        if scene.sh is not None:
+            rgb = sh_rgb_parallel(O, scene.means, scene.sh, scene.sh_degree, cam.w2c, threads)
+        else:
+            rgb = scene.colors
         if R is not None:
             R.render_full(scene.means, cov, scene.opacities, rgb, cam.w2c, cam.K, cam.height,
                           cam.width, tile_size=16)
         else:
-            kind = "port"
             O.render_full(scene.means, cov, scene.opacities, rgb, cam.w2c, cam.K, cam.height,
                           cam.width, tile_size=16)
         dt = time.perf_counter() - t0
         if i > 0:
             times.append(dt)
-        log(f"cpu frame {i}: {dt:.2f}s")
     med = float(np.median(times))
-    return {"value": round(1.0 / med, 4), "unit": "frames/s", "cores": threads if kind == "reference" else 1,
-            "kind": kind,
-            "sample": f"{frames} orbit views of the 6M-Gaussian scene after 1 warm-up, median "
-                      f"{med * 1e3:.0f} ms/frame (SH eval + render_full, 16x16 tiles)"}
+    log(f"cpu baseline ({sample}): {med * 1e3:.0f} ms/frame on {threads} threads")
+    return {"value": round(1.0 / med, 4), "unit": "frames/s",
+            "cores": threads if kind == "reference" else 1, "kind": kind,
+            "nproc": info["nproc"], "os_cpu_count": info["os_cpu_count"],
+            "cpu_model": info["model"],
+            "sample": f"{sample}: median {med * 1e3:.1f} ms/frame (SH colour + render_full, "
+                      f"16x16 tiles, {threads} threads; the box's share of one GPU is "
+                      f"{BOX_CPU_SHARE} threads)"}
 
 
 def main():
@@ -394,19 +543,10 @@ def main():
         sequential_frames(args)
         return
     ctx, scene, cov, cams, stats, dt = bench_frames(args)
-    st, avg, blend_flops = stage_summary(scene, stats)
+    tiles = ((cams[0].width + 15) // 16) * ((cams[0].height + 15) // 16)
+    st = stage_summary(scene.n, 3, tiles, stats)
     fps = args.steps / dt
     log(f"{fps:.1f} frames/s; stages {st['ms']}")
-    blend_ms = avg["ms_blend"]
-    # The blend kernel: the stage the metric prices against FP32 peak. It runs on
-    # the FP32 vector ALUs (no MFMA); "mfma" marks the compute roof, priced at
-    # MI355X's FP32 peak.
-    roof = {"kernel": "k_blend", "bound": "mfma", "pipe": "fp32 VALU",
-            "achieved": round(blend_flops / (blend_ms * 1e-3) / 1e12, 3),
-            "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(blend_flops / (blend_ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4),
-            "traffic": pmc_traffic("k_blend"),
-            "flops_per_launch": round(blend_flops), "ms_per_launch": round(blend_ms, 4)}
     res = {
         "metric": "frames/sec @6M Gaussians 1237x822; sort Gkeys/s; blend frac of FP32 peak",
         "value": round(fps, 3), "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
@@ -420,23 +560,38 @@ def main():
                    "frames_in_flight": FRAMES_IN_FLIGHT,
                    "stage_times": "16 frames one at a time with per-stage hipEvents"},
         "stages": st,
-        "roofline": roof,
+        "roofline": dominant_roofline(st),
+        "blend": {"ms": st["roofline"]["blend"]["ms"],
+                  "achieved_tflops": st["roofline"]["blend"]["achieved_tflops"],
+                  "frac_fp32": st["roofline"]["blend"]["frac_fp32"]},
     }
     res["host_out"] = bench_host_out(ctx, cams, min(args.steps, 64))
     log(f"host_out: {res['host_out']}")
     if not args.no_morton:
         res["morton_chunk_cull"] = bench_morton(scene, cov, cams, args.steps, args.warmup)
         log(f"morton_chunk_cull: {res['morton_chunk_cull']}")
+    cpu_c3 = None
+    if not args.no_cpu:
+        cpu_c3 = cpu_baseline(scene, cov, cams, args.cpu_frames, args.cpu_threads,
+                              f"{args.cpu_frames} orbit views of the 6M-Gaussian scene after 1 "
+                              "warm-up")
+    del scene, cov
+    if not args.no_views:
+        from gsplat_tt_amd import scenes
+        s1, c1 = scenes.config1()
+        res["c1_100k"] = bench_view(ctx, "100K", s1, c1[0], args.view_steps, 8,
+                                    0 if args.no_cpu else 5, args.cpu_threads, out="f32")
+        s2, c2 = scenes.config2()
+        res["c2_1m"] = bench_view(ctx, "1M SH3", s2, c2[0], args.view_steps, 8,
+                                  0 if args.no_cpu else 3, args.cpu_threads, out="bf16")
+        del s1, s2
     if not args.no_sort:
         res["sort"] = bench_sort(ctx, args.sort_keys)
         log(f"sort: {res['sort']}")
     if not args.no_train:
         res["train"] = bench_train(ctx, args.train_n, args.train_steps)
         log(f"train: {res['train']}")
-    if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(scene, cov, cams, args.cpu_frames, args.cpu_threads)
-    else:
-        res["cpu_baseline"] = None
+    res["cpu_baseline"] = cpu_c3
     ctx.close()
     print(json.dumps(res), flush=True)
 
