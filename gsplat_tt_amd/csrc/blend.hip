@@ -10,14 +10,17 @@
 //   1. loads the 48-byte records (lane q and lane q+32 hold entry q),
 //   2. evaluates the constrained-minimum microblock cull for (entry, own
 //      microblock) -> a 64-bit ballot = both halves' kept masks,
-//   3. walks the union of the two kept masks in depth order: the entry's
-//      parameters are read into SGPRs (v_readlane), the halves that keep it
-//      blend it, transmittance and colour stay in VGPRs.
-// Full microblocks follow the reference's AVX2 arithmetic exactly (degree-4
-// exp, power clamp [-30,0], T -= alpha*T, early-out test every 4 kept entries);
-// image-edge microblocks follow its scalar rule (exp, T *= 1-alpha, test after
-// every entry) (cull_and_blend.cpp:506-670, simd_exp_avx2.h:12-32). A half
-// whose microblock is done stops issuing; the wave exits when both are done.
+//   3. stages the entries in LDS and walks the union of the two kept masks in
+//      depth order; transmittance and colour stay in VGPRs.
+// Bands whose two microblocks are fully inside the image (all but the image
+// edge) follow the reference's AVX2 arithmetic exactly (degree-4 exp, power
+// clamp [-30,0], T -= alpha*T, early-out test every 4 kept entries): per entry,
+// the terms that depend on the pixel row or column only are staged once and
+// every lane evaluates the entry, its half's opacity being 0 where that half
+// drops it. Edge bands follow the scalar rule for edge microblocks (exp,
+// T *= 1-alpha, test after every entry) (cull_and_blend.cpp:506-670,
+// simd_exp_avx2.h:12-32), a lane evaluating only what its half keeps. The wave
+// exits when both microblocks are done.
 #include <algorithm>
 
 #include "gs_common.h"
@@ -73,6 +76,7 @@ struct Band {
     int tile, tile_x, tile_y, mbx, mby;
     int px_start, py0;
     float tx_tile, ty_tile, pxs, offx, pxc, pyc, mb_ox, mb_oy;
+    float pxsA, pyr0;  // band: microblock A's first column, first row centre (+0.5)
     bool emptyA, emptyB, fullA, fullB, full, pix_valid;
 };
 
@@ -111,6 +115,8 @@ __device__ __forceinline__ Band make_band(const BlendParams& bp, int lane) {
     g.offx = (float)pj + 0.5f;
     g.pxc = (float)(g.px_start + pj) + 0.5f;    // scalar path pixel centre
     g.pyc = (float)(g.py0 + pi) + 0.5f;
+    g.pxsA = (float)pxA;
+    g.pyr0 = (float)g.py0 + 0.5f;
     // microblock cull rectangle (cull_and_blend.cpp:447-498)
     g.mb_oy = g.ty_tile + (float)(g.mby * 4);
     g.mb_ox = g.tx_tile + (float)(g.mbx * 8);
@@ -157,24 +163,173 @@ __device__ __forceinline__ bool mb_keep(const Band& g, float4 r0, float4 r1, int
     return m2_min <= -2.0f * lt;
 }
 
-// The batch loop of one band. INTERIOR: both microblocks lie fully inside the
-// image (AVX2 rule only, every pixel valid). Per-half state lives in VGPRs
-// (uniform within the half): `mine` = the half's kept entries of the batch
-// (cleared once the half is done), `cnt` = entries the half has blended; the
-// scalar unit only walks the union of both halves' masks.
-// The batch loop of one band. INTERIOR: both microblocks lie fully inside the
-// image (AVX2 rule only, every pixel valid). Per-half state lives in VGPRs
-// (uniform within the half): `mine` = the half's kept entries of the batch
-// (cleared once the half is done), `cnt` = entries the half has blended; the
-// scalar unit only walks the union of both halves' masks. The batch's entry
-// parameters are staged in LDS (mx, my, op | -ci_a/2, -ci_b, -ci_c/2 | r, g, b)
-// and read back with wave-uniform addresses (a broadcast, on the LDS pipe).
+// Entry parameters of an image-edge band's batch, staged in LDS (mx, my, op |
+// -ci_a/2, -ci_b, -ci_c/2 | r, g, b) and read back with wave-uniform addresses
+// (a broadcast, on the LDS pipe).
 struct BatchRec {
     float4 p0, p1, p2;
 };
 
-template <bool INTERIOR>
-__device__ __forceinline__ void blend_band(const Band& g, const float4* __restrict__ brec,
+// LDS staging of an interior band's batch: per entry, the terms of the AVX2
+// power that depend on the pixel row (y_term = C dy dy, xy_coef = B dy for the
+// band's 4 rows) and on the pixel column (dx = (px0 - mx) + (c + 0.5) for the
+// 16 columns of the two microblocks), the quadratic coefficient with each
+// half's opacity (zero where that half's microblock drops the entry), and the
+// colour: each computed once per entry instead of once per pixel. 4 KiB, so
+// eight one-wave workgroups per SIMD still fit in the CU's LDS.
+struct BandStage {
+    float4 rows[32][2];   // rows 2k, 2k+1: (y_term, xy_coef, y_term, xy_coef)
+    float4 dx[32][4];     // columns 4k .. 4k+3
+    float2 aop[32][2];    // (-ci_a/2, op or 0) per half
+    float4 rgb[32];
+};
+union BlendLds {
+    BatchRec rec[32];     // image-edge bands
+    BandStage band;       // interior bands
+};
+
+// The batch loop of an interior band (both microblocks fully inside the
+// image: AVX2 rule, every pixel valid). Costs are per (entry, wave), and a
+// scalar instruction costs about two vector ones (one scalar unit serves the
+// CU's four SIMDs), so the bookkeeping is vector and per lane, uniform within
+// each half: `mine` = the half's kept entries of the batch, `cnt` = entries
+// the half has blended. The entries where a half tests for its early-out
+// (its count reaches a multiple of 4, cull_and_blend.cpp:578-616) are found
+// once per batch, lane-parallel (lane q marks entry q). The 32 entries of a
+// batch are then walked in a loop unrolled at compile time: each entry is
+// evaluated for every lane (about 92 % of the batch's entries are kept by one
+// half or the other, so no scalar walk of the union pays off), staged terms
+// are read at immediate LDS offsets, and a lane whose half drops the entry
+// sees opacity 0: alpha 0 leaves T and the colour exactly as they are
+// (fma(0, c, x) = x, x - 0 = x), so no per-entry select. A half that retires
+// inside a batch keeps evaluating that batch's entries it had kept, so its
+// colour is saved at the retirement and restored at the end.
+__device__ __forceinline__ void blend_band_interior(const Band& g, const float4* __restrict__ brec,
+                                                    const uint32_t* __restrict__ sid,
+                                                    uint32_t start, uint32_t end,
+                                                    const BlendParams& bp, int lane,
+                                                    BandStage* st, float& cr, float& cg,
+                                                    float& cb, uint32_t& cnt,
+                                                    uint32_t& n_batch, uint32_t& n_iter,
+                                                    uint32_t& n_kept) {
+    const int h = lane >> 5, q = lane & 31;
+    const int pi = q >> 3, col = h * 8 + (q & 7);  // the lane's pixel in the band
+    const int half = (int)(blockDim.x >> 1);  // 32 lanes per microblock
+    const uint32_t below = (1u << q) - 1u;    // lanes of the half before this one
+    const float thr = bp.thr;
+    float T = 1.0f;
+    float sr = 0.0f, sg = 0.0f, sb = 0.0f;  // colour at the half's retirement
+    bool alive = true;  // this lane's half has not retired
+    for (uint32_t base = start; base < end; base += 32) {
+        const uint32_t idx = base + q;
+        const bool has = idx < end;
+        float4 r0 = make_float4(0, 0, 0, 0), r1 = r0, r2 = r0;
+        if (has) {
+            const uint32_t gi = sid[idx];
+            r0 = brec[3 * (size_t)gi + 0];
+            r1 = brec[3 * (size_t)gi + 1];
+            r2 = brec[3 * (size_t)gi + 2];
+        }
+        const bool keep = has && alive && mb_keep(g, r0, r1, bp.cull_disabled);
+        const uint64_t mask = __ballot(keep);
+        ++n_batch;
+        uint32_t mlo = (uint32_t)mask, mhi = (uint32_t)(mask >> half);
+        n_kept += (uint32_t)(__builtin_popcount(mlo) + __builtin_popcount(mhi));
+        const uint32_t mine = h ? mhi : mlo;
+        uint32_t uni = mlo | mhi;  // uniform: entries either half keeps
+        n_iter += (uint32_t)__builtin_popcount(uni);
+        // early-out test points of this batch: lane q marks entry q
+        const bool pt = ((mine >> q) & 1u) &&
+                        ((cnt + (uint32_t)__builtin_popcount(mine & below) + 1u) & 3u) == 0u;
+        const uint64_t pts = __ballot(pt);
+        uint32_t plo = (uint32_t)pts, phi = (uint32_t)(pts >> half);
+        uint32_t pany = plo | phi;  // uniform: entries after which a half tests
+        cnt += (uint32_t)__builtin_popcount(mine);
+        // stage entry q (both halves hold its record): half h its rows 2h, 2h+1,
+        // its columns 8h .. 8h+7 and its own opacity, half 1 the colour (the
+        // AVX2 rule's operations, cull_and_blend.cpp:194-279: px_base = px0 - mx,
+        // dx = px_base + (c + 0.5), dy = py + 0.5 - my, y_term = C dy dy,
+        // xy_coef = B dy)
+        {
+            const float Bq = -r1.y, Cq = -0.5f * r1.z;
+            const float dy0 = g.pyr0 + (float)(2 * h) - r0.y;
+            const float dy1 = g.pyr0 + (float)(2 * h + 1) - r0.y;
+            st->rows[q][h] = make_float4(Cq * dy0 * dy0, Bq * dy0, Cq * dy1 * dy1, Bq * dy1);
+            const float pb = g.pxs - r0.x;
+            st->dx[q][2 * h] = make_float4(pb + 0.5f, pb + 1.5f, pb + 2.5f, pb + 3.5f);
+            st->dx[q][2 * h + 1] = make_float4(pb + 4.5f, pb + 5.5f, pb + 6.5f, pb + 7.5f);
+            st->aop[q][h] = make_float2(-0.5f * r1.x, keep ? r2.x : 0.0f);
+            if (h) st->rgb[q] = make_float4(r2.y, r2.z, r2.w, 0.0f);
+        }
+        __syncthreads();  // one wave per workgroup: orders the LDS writes and reads
+        const float* rowp = &st->rows[0][pi >> 1].x + 2 * (pi & 1);
+        const float* dxp = &st->dx[0][0].x + col;
+        bool retired = false;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            if (((uni >> j) & 1u) == 0u) continue;  // neither half keeps entry j
+            // AVX2 rule for the lane's pixel: power clamp [-30, 0], degree-4
+            // exp, alpha <= 0.99 (the staged terms are the same fp32 values)
+            const float2 rt = *reinterpret_cast<const float2*>(rowp + 8 * j);
+            const float dx = dxp[16 * j];
+            const float2 ao = st->aop[j][h];
+            float pwr = __builtin_fmaf(rt.y, dx, rt.x);
+            pwr = __builtin_fmaf(ao.x, dx * dx, pwr);
+            pwr = __builtin_amdgcn_fmed3f(pwr, -30.0f, 0.0f);
+            float al = ao.y * exp4(pwr);
+            al = (al < 0.99f) ? al : 0.99f;
+            const float4 e2 = st->rgb[j];
+            const float at = al * T;
+            cr = __builtin_fmaf(at, e2.x, cr);
+            cg = __builtin_fmaf(at, e2.y, cg);
+            cb = __builtin_fmaf(at, e2.z, cb);
+            T = T - at;
+            if ((pany >> j) & 1u) {
+                // max over the microblock's pixels < thr <=> no pixel has T >= thr
+                const uint64_t live = __ballot(!(T < thr));
+                const bool deadA = ((plo >> j) & 1u) && (uint32_t)live == 0u;
+                const bool deadB = ((phi >> j) & 1u) && (uint32_t)(live >> half) == 0u;
+                if (deadA || deadB) {
+                    // a retired half blends nothing more: its later kept entries
+                    // are dropped (from its count too, which the statistics
+                    // report) and it has no later test points
+                    const bool me = h ? deadB : deadA;
+                    if (me) {
+                        cnt -= (uint32_t)__builtin_popcount((mine >> j) >> 1);
+                        alive = false;
+                        sr = cr;
+                        sg = cg;
+                        sb = cb;
+                    }
+                    if (deadA) mlo = plo = 0u;
+                    if (deadB) mhi = phi = 0u;
+                    const uint32_t later = uni & ~(mlo | mhi);
+                    n_iter -= (uint32_t)__builtin_popcount((later >> j) >> 1);
+                    uni = mlo | mhi;
+                    pany = plo | phi;
+                    if (__ballot(alive) == 0ull) {
+                        retired = true;
+                        break;
+                    }
+                }
+            }
+        }
+        if (retired) break;
+        __syncthreads();  // the next batch overwrites the staged records
+    }
+    if (!alive) {
+        cr = sr;
+        cg = sg;
+        cb = sb;
+    }
+}
+
+// The batch loop of a band that the image edge cuts: per-half state in VGPRs
+// (uniform within the half: `mine` = the half's kept entries of the batch,
+// cleared once the half is done; `cnt` = entries the half has blended), the
+// scalar unit walks the union of both halves' masks, and a lane evaluates an
+// entry only when its half keeps it and its pixel is inside the image.
+__device__ __forceinline__ void blend_band_edge(const Band& g, const float4* __restrict__ brec,
                                            const uint32_t* __restrict__ sid, uint32_t start,
                                            uint32_t end, const BlendParams& bp, int lane,
                                            BatchRec* s_rec, float& T, float& cr, float& cg,
@@ -208,70 +363,6 @@ __device__ __forceinline__ void blend_band(const Band& g, const float4* __restri
         }
         __syncthreads();  // one wave per workgroup: orders the LDS writes and reads
         uint32_t uni = mA | mB;
-        if (INTERIOR) {
-            // two union entries per step: their alpha chains are independent
-            // (only T and the colour are carried from one to the next), so the
-            // two evaluations interleave; each entry keeps its own early-out test
-            auto alpha_of = [&](int j) {
-                const float4 e0 = s_rec[j].p0, e1 = s_rec[j].p1;
-                const float px_base = g.pxs - e0.x;
-                const float dx = px_base + g.offx;
-                const float dx_sq = dx * dx;
-                const float dy = g.pyc - e0.y;
-                const float y_term = e1.z * dy * dy;
-                const float xy_coef = e1.y * dy;
-                float pwr = __builtin_fmaf(xy_coef, dx, y_term);
-                pwr = __builtin_fmaf(e1.x, dx_sq, pwr);
-                pwr = (pwr < 0.0f) ? pwr : 0.0f;
-                pwr = (pwr > -30.0f) ? pwr : -30.0f;
-                const float gw = exp4(pwr);
-                float al = e0.z * gw;
-                return (al < 0.99f) ? al : 0.99f;
-            };
-            bool all_done = false;
-            auto apply = [&](int j, float al) {
-                const float4 e2 = s_rec[j].p2;
-                const bool run = (mine >> j) & 1u;
-                // a lane whose half does not keep the entry adds nothing
-                const float at = run ? al * T : 0.0f;
-                cr = __builtin_fmaf(at, e2.x, cr);
-                cg = __builtin_fmaf(at, e2.y, cg);
-                cb = __builtin_fmaf(at, e2.z, cb);
-                T = T - at;
-                cnt += run ? 1u : 0u;
-                // early-out test every 4 kept entries (cull_and_blend.cpp:578-616)
-                const uint64_t chkm = __ballot(run && (cnt & 3u) == 0u);
-                if (chkm != 0) {
-                    const uint64_t live = __ballot(!(T < bp.thr));
-                    const bool deadA = (uint32_t)chkm != 0u && (uint32_t)live == 0u;
-                    const bool deadB = (uint32_t)(chkm >> 32) != 0u && (uint32_t)(live >> 32) == 0u;
-                    if (deadA) doneA = true;
-                    if (deadB) doneB = true;
-                    const uint32_t keepA = doneA ? 0u : mA, keepB = doneB ? 0u : mB;
-                    uni &= keepA | keepB;
-                    mine = h ? keepB : keepA;
-                    all_done = doneA && doneB;
-                }
-            };
-            while (uni) {
-                const int j1 = __builtin_ctz(uni);
-                uni &= uni - 1;
-                const bool two = uni != 0u;
-                const int j2 = two ? __builtin_ctz(uni) : j1;
-                if (two) uni &= uni - 1;
-                n_iter += two ? 2u : 1u;
-                const float al1 = alpha_of(j1);
-                const float al2 = alpha_of(j2);
-                apply(j1, al1);
-                if (all_done) return;
-                // the test after the first entry may have retired a half: the
-                // second entry then adds nothing for it (mine is updated)
-                if (two) {
-                    apply(j2, al2);
-                    if (all_done) return;
-                }
-            }
-        } else {
         while (uni) {
             const int j = __builtin_ctz(uni);
             uni &= uni - 1;
@@ -280,30 +371,7 @@ __device__ __forceinline__ void blend_band(const Band& g, const float4* __restri
             const float mx = e0.x, my = e0.y, op = e0.z;
             const float A = e1.x, B = e1.y, C = e1.z;
             const bool run = (mine >> j) & 1u;
-            if (INTERIOR) {
-                // both halves evaluate the entry and a lane whose half does not
-                // keep it adds nothing (at = 0 leaves T and the colour exactly
-                // as they are): no divergent branch per entry
-                const float px_base = g.pxs - mx;
-                const float dx = px_base + g.offx;
-                const float dx_sq = dx * dx;
-                const float dy = g.pyc - my;
-                const float y_term = C * dy * dy;
-                const float xy_coef = B * dy;
-                float pwr = __builtin_fmaf(xy_coef, dx, y_term);
-                pwr = __builtin_fmaf(A, dx_sq, pwr);
-                pwr = (pwr < 0.0f) ? pwr : 0.0f;
-                pwr = (pwr > -30.0f) ? pwr : -30.0f;
-                const float gw = exp4(pwr);
-                float al = op * gw;
-                al = (al < 0.99f) ? al : 0.99f;
-                const float at = run ? al * T : 0.0f;
-                cr = __builtin_fmaf(at, e2.x, cr);
-                cg = __builtin_fmaf(at, e2.y, cg);
-                cb = __builtin_fmaf(at, e2.z, cb);
-                T = T - at;
-                cnt += run ? 1u : 0u;
-            } else if (run) {
+            if (run) {
                 if (g.full) {
                     const float px_base = g.pxs - mx;
                     const float dx = px_base + g.offx;
@@ -341,12 +409,12 @@ __device__ __forceinline__ void blend_band(const Band& g, const float4* __restri
             }
             // early-out test: every 4 kept entries of a full microblock, after
             // every entry of an image-edge one (cull_and_blend.cpp:578-616)
-            const bool chk = run && (INTERIOR ? ((cnt & 3u) == 0u) : (!g.full || (cnt & 3u) == 0u));
+            const bool chk = run && (!g.full || (cnt & 3u) == 0u);
             const uint64_t chkm = __ballot(chk);
             if (chkm != 0) {
                 // max over the microblock's pixels < thr  <=>  no pixel has T >= thr
                 // (T is never NaN; edge pixels outside the image do not vote)
-                const uint64_t live = __ballot((INTERIOR || g.pix_valid) && !(T < bp.thr));
+                const uint64_t live = __ballot(g.pix_valid && !(T < bp.thr));
                 const bool deadA = (uint32_t)chkm != 0u && (uint32_t)live == 0u;
                 const bool deadB = (uint32_t)(chkm >> 32) != 0u && (uint32_t)(live >> 32) == 0u;
                 if (deadA) doneA = true;
@@ -356,7 +424,6 @@ __device__ __forceinline__ void blend_band(const Band& g, const float4* __restri
                 mine = h ? keepB : keepA;
                 if (doneA && doneB) return;
             }
-        }
         }
         __syncthreads();  // the next batch overwrites the staged records
     }
@@ -374,13 +441,13 @@ __global__ __launch_bounds__(GS_WAVE) void k_blend(const float4* __restrict__ br
     float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
     uint32_t cnt = 0, n_batch = 0, n_iter = 0, n_kept = 0;
     const uint32_t start = ranges[2 * g.tile], end = ranges[2 * g.tile + 1];
-    __shared__ BatchRec s_rec[32];
+    __shared__ BlendLds lds;
     if (g.fullA && g.fullB)
-        blend_band<true>(g, brec, sid, start, end, bp, lane, s_rec, T, cr, cg, cb, cnt, n_batch,
-                         n_iter, n_kept);
+        blend_band_interior(g, brec, sid, start, end, bp, lane, &lds.band, cr, cg, cb, cnt,
+                            n_batch, n_iter, n_kept);
     else
-        blend_band<false>(g, brec, sid, start, end, bp, lane, s_rec, T, cr, cg, cb, cnt, n_batch,
-                          n_iter, n_kept);
+        blend_band_edge(g, brec, sid, start, end, bp, lane, lds.rec, T, cr, cg, cb, cnt,
+                        n_batch, n_iter, n_kept);
 
     if (bp.evals != nullptr) {
         // pixel-Gaussian evaluations = sum over valid pixels of entries blended
