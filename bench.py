@@ -58,6 +58,8 @@ def parse():
     ap.add_argument("--no-views", action="store_true",
                     help="skip the 100K and 1M single-view legs")
     ap.add_argument("--view-steps", type=int, default=64)
+    ap.add_argument("--workload", choices=("c1", "c2", "c3"), default="c3",
+                    help="the workload of --sequential-frames")
     ap.add_argument("--sequential-frames", type=int, default=0, metavar="K",
                     help="only render K orbit views one at a time (device output, no frames "
                          "in flight): the per-kernel split of a frame under a kernel trace")
@@ -238,23 +240,33 @@ def bench_morton(scene, cov, cams, steps, warmup):
 
 
 def sequential_frames(args):
-    """Config 3's orbit views rendered one at a time (gs_render, device output),
-    nothing else: what a kernel trace splits into per-kernel frame times."""
+    """Frames of one workload rendered one at a time (gs_render, device output),
+    nothing else: what a kernel trace splits into per-kernel frame times.
+    --workload c3: the 6M-Gaussian orbit views; c1: the 100K-Gaussian view
+    (f32 out); c2: the 1M-Gaussian SH3 view (bf16 out)."""
     from gsplat_tt_amd import _lib as L
     from gsplat_tt_amd import scenes
 
-    scene, cams = scenes.config3(n=args.n, views=args.views)
+    if args.workload == "c1":
+        scene, cams = scenes.config1()
+        sh, deg, fmt = scene.colors, -1, "f32"
+    elif args.workload == "c2":
+        scene, cams = scenes.config2()
+        sh, deg, fmt = scene.sh, 3, "bf16"
+    else:
+        scene, cams = scenes.config3(n=args.n, views=args.views)
+        sh, deg, fmt = scene.sh, 3, "bf16"
     cov = scenes.cov3d(scene.scales, scene.quats)
     ctx = L.Context(0, timing=True)
-    ctx.set_scene(scene.means, cov, scene.opacities, scene.sh, sh_degree=3)
+    ctx.set_scene(scene.means, cov, scene.opacities, sh, sh_degree=deg)
     H, W = cams[0].height, cams[0].width
-    out = ctx.dev_alloc(H * W * 6)
-    sts = [ctx.render_dev(L.make_view(c.w2c, c.K, H, W, tile_size=16, output="bf16"), out)
+    out = ctx.dev_alloc(H * W * 12)
+    sts = [ctx.render_dev(L.make_view(c.w2c, c.K, H, W, tile_size=16, output=fmt), out)
            for c in (cams[i % len(cams)] for i in range(args.sequential_frames))]
     ctx.dev_free(out)
     ctx.close()
     keys = ("ms_project", "ms_depth_sort", "ms_tile_assign", "ms_tile_sort", "ms_blend")
-    print(json.dumps({"sequential_frames": len(sts),
+    print(json.dumps({"workload": args.workload, "sequential_frames": len(sts),
                       "ms": {k[3:]: round(float(np.mean([s[k] for s in sts[4:]])), 4) for k in keys}}),
           flush=True)
 

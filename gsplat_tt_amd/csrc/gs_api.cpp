@@ -1722,8 +1722,18 @@ static void sort_u64_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n,
     int passes = 0;
     void* kf = nullptr;
     uint32_t* vf = nullptr;
-    HIPCHK(gs::radix_sort_pairs(keys, vals, n, 8, begin_bit, end_bit, ctx->sort, ctx->h_pin + 64,
-                                ctx->st, &passes, false, &kf, &vf));
+    if (ranges != nullptr) {
+        // the tile/depth sort: no host round trip, every pass runs, each pass
+        // counting the next one's digits
+        HIPCHK(gs::launch_fill_u32(ctx->sort.hist, 0u, gs::sort_hist_words(), ctx->st));
+        HIPCHK(gs::radix_sort_pairs_dev_chain(keys, vals, n, begin_bit, end_bit, ctx->sort.hist,
+                                              ctx->sort.hist + 8 * 256, ctx->sort, ctx->st, &kf,
+                                              &vf));
+        passes = n > 0 ? (end_bit - begin_bit + 7) / 8 : 0;
+    } else {
+        HIPCHK(gs::radix_sort_pairs(keys, vals, n, 8, begin_bit, end_bit, ctx->sort,
+                                    ctx->h_pin + 64, ctx->st, &passes, false, &kf, &vf));
+    }
     if (kf != keys) {
         HIPCHK(hipMemcpyAsync(keys, kf, (size_t)n * 8, hipMemcpyDeviceToDevice, ctx->st));
         HIPCHK(hipMemcpyAsync(vals, vf, (size_t)n * 4, hipMemcpyDeviceToDevice, ctx->st));

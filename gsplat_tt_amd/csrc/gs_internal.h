@@ -138,6 +138,15 @@ hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const
                                 void** keys_final, uint32_t** vals_final,
                                 const uint32_t* n_kept_dev = nullptr);
 
+// The 64-bit-key sort of radix_sort_pairs_dev over exactly n keys, with no
+// producer histogram: a histogram kernel counts the first pass's digits and
+// each pass adds the next pass's digit counts from the keys it holds, into
+// `hist` ([pass][256], cleared by the caller). Every pass runs.
+hipError_t radix_sort_pairs_dev_chain(uint64_t* keys, uint32_t* vals, int64_t n, int begin_bit,
+                                      int end_bit, uint32_t* hist, uint32_t* tickets,
+                                      SortTemp& tmp, hipStream_t st, void** keys_final,
+                                      uint32_t** vals_final);
+
 // Device and stream of a context (gs_api.cpp), for entry points in other units.
 struct CtxInfo {
     int device;

@@ -118,12 +118,11 @@ extern "C" int gs_sort_tile_depth_noalloc(gs_ctx* ctx, uint64_t* keys, uint32_t*
     // memset, so the call can sit in a captured graph)
     e = launch_fill_u32(tmp.hist, 0u, kHistWords, st);
     if (e == hipSuccess) e = launch_fill_u32(tmp.ctl, 0u, 2, st);
-    if (e == hipSuccess) e = launch_digit_hist_u64(keys, n, 0, end_bit, tmp.hist, st);
     void* kf = keys;
     uint32_t* vf = vals;
     if (e == hipSuccess && n > 0)
-        e = radix_sort_pairs_dev(keys, vals, n, nullptr, 8, 0, end_bit, tmp.hist, tickets, tmp,
-                                 st, false, &kf, &vf);
+        e = radix_sort_pairs_dev_chain(keys, vals, n, 0, end_bit, tmp.hist, tickets, tmp, st,
+                                       &kf, &vf);
     if (e == hipSuccess && kf != keys) {
         e = hipMemcpyAsync(keys, kf, (size_t)n * 8, hipMemcpyDeviceToDevice, st);
         if (e == hipSuccess)

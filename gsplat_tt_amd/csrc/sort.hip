@@ -202,7 +202,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     uint32_t* __restrict__ vout, int64_t n_cap, const uint32_t* __restrict__ n_dev, int shift,
     int bits, const uint32_t* __restrict__ g_hist_pass, void* __restrict__ state_raw,
     uint32_t* __restrict__ ticket, uint32_t epoch, uint32_t* __restrict__ clear_next,
-    uint32_t* ctl) {
+    uint32_t* ctl, uint32_t* __restrict__ next_hist, int next_shift, int next_bits) {
     using D = Desc<D32>;
     using DT = typename D::T;
     DT* state = static_cast<DT*>(state_raw);
@@ -219,6 +219,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     __shared__ uint32_t s_loff[256];
     __shared__ uint32_t s_gpos[256];
     __shared__ uint32_t s_tmp[2][4];
+    __shared__ uint32_t s_nh[256];  // next pass's digit counts (next_hist given)
     __shared__ K s_keys[PART];
     __shared__ uint32_t s_vals_own[SPLIT ? 1 : PART];
     uint32_t* const s_vals = SPLIT ? reinterpret_cast<uint32_t*>(s_keys) : s_vals_own;
@@ -232,6 +233,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     // this workgroup's row of the descriptors that the next pass uses
     if (clear_next != nullptr && tid < 256) clear_next[(size_t)blockIdx.x * 256 + tid] = 0u;
     for (int i = tid; i < WAVES * 256; i += THREADS) (&s_wcnt[0][0])[i] = 0;
+    if (next_hist != nullptr && tid < 256) s_nh[tid] = 0u;
     __syncthreads();
     const uint32_t vid = s_vid;
     const int64_t part_base = (int64_t)vid * PART;
@@ -264,16 +266,26 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         rank[it] = 0;
         if (idx < n && !(DROP && key[it] == (K)kPairDrop)) {
             const uint32_t d = digit_of(key[it], shift, mask);
-            uint64_t peers = __ballot(1);
-            for (int b = 0; b < bits; ++b) {
-                const bool bit = (d >> b) & 1u;
-                const uint64_t bb = __ballot(bit);
-                peers &= bit ? bb : ~bb;
+            // all 8 bit planes, unrolled: a narrower last digit has zeros
+            // above its width in every lane, whose planes change nothing.
+            // x = the lane's bit b as 0 / all-ones; the lanes whose bit b
+            // differs from this lane's are ballot ^ x, collected in `diff` by
+            // one three-input op per half (diff | (ballot ^ x): truth table
+            // 0xF6 over the inputs' 0xF0 / 0xCC / 0xAA planes).
+            uint32_t diff_lo = 0u, diff_hi = 0u;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const uint32_t x = (uint32_t)__builtin_amdgcn_sbfe((int32_t)d, b, 1);
+                const uint64_t bb = __ballot(x != 0u);
+                diff_lo = __builtin_amdgcn_bitop3_b32(diff_lo, (uint32_t)bb, x, 0xF6);
+                diff_hi = __builtin_amdgcn_bitop3_b32(diff_hi, (uint32_t)(bb >> 32), x, 0xF6);
             }
+            const uint64_t peers =
+                __ballot(1) & ~(((uint64_t)diff_hi << 32) | (uint64_t)diff_lo);
             const uint32_t before = s_wcnt[w][d];
             rank[it] = before + (uint32_t)__popcll(peers & lt);
-            const int leader = __ffsll((unsigned long long)peers) - 1;
-            if (lane == leader) s_wcnt[w][d] = (WC)(before + (uint32_t)__popcll(peers));
+            // every peer stores the same new count (no leader election)
+            s_wcnt[w][d] = (WC)(before + (uint32_t)__popcll(peers));
         }
     }
     __syncthreads();
@@ -335,7 +347,19 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         const uint32_t excl = has_digit ? digit_walk<D, DT>(state, vid, tid, tot, epoch, ctl) : 0u;
         s_gpos[tid] = gbase + excl - loff;
     }
+    if (next_hist != nullptr) {
+        // the next pass's digit histogram from the keys in registers: the
+        // waves that do not walk count while the first four walk
+        const uint32_t nmask = (1u << next_bits) - 1u;
+#pragma unroll
+        for (int it = 0; it < ITEMS; ++it) {
+            const int64_t idx = wave_base + it * GS_WAVE + lane;
+            const bool on = idx < n && !(DROP && key[it] == (K)kPairDrop);
+            hist_add_wave(s_nh, digit_of(key[it], next_shift, nmask), on);
+        }
+    }
     __syncthreads();
+    if (next_hist != nullptr && tid < 256 && s_nh[tid] != 0u) atomicAdd(&next_hist[tid], s_nh[tid]);
     const int64_t cnt64 = n - part_base;
     const int count = DROP ? (int)min(s_count, (uint32_t)PART) : (cnt64 < PART ? (int)cnt64 : PART);
     if constexpr (!SPLIT) {
@@ -407,7 +431,7 @@ template <typename K, typename CFG>
 hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uint32_t* vout,
                       int64_t n_cap, const uint32_t* n_dev, int shift, int bits,
                       const uint32_t* hist_pass, SortTemp& tmp, uint32_t* ticket, hipStream_t st,
-                      bool drop) {
+                      bool drop, uint32_t* next_hist, int next_shift, int next_bits) {
     constexpr int T = CFG::T, I = CFG::I;
     constexpr bool SP = CFG::SPLIT;
     const unsigned grid = (unsigned)((n_cap + T * I - 1) / (T * I));
@@ -436,7 +460,8 @@ hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uin
 #define GS_OS(IO, DD, DR)                                                                         \
     k_onesweep<K, IO, T, I, DD, DR, SP><<<grid, T, 0, st>>>(kin, vin, kout, vout, n_cap, n_dev,  \
                                                             shift, bits, hist_pass, state,       \
-                                                            ticket, epoch, clear_next, tmp.ctl)
+                                                            ticket, epoch, clear_next, tmp.ctl,  \
+                                                            next_hist, next_shift, next_bits)
     if (drop) {
         if (iota || sizeof(K) != 4) return hipErrorInvalidValue;
         if (d32) GS_OS(false, true, true); else GS_OS(false, false, true);
@@ -451,16 +476,21 @@ hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uin
 
 // One digit pass: clears the look-back descriptors of its partitions (32-bit
 // ones below 2^30 keys, else 64-bit), then runs the onesweep kernel.
+// next_hist (optional): the pass also adds the digit histogram of bits
+// [next_shift, next_shift + next_bits) of its keys there (for the next pass).
 template <typename K>
 hipError_t launch_pass(bool iota, const K* kin, const uint32_t* vin, K* kout, uint32_t* vout,
                        int64_t n_cap, const uint32_t* n_dev, int shift, int bits,
                        const uint32_t* hist_pass, SortTemp& tmp, uint32_t* ticket,
-                       hipStream_t st, bool drop = false) {
+                       hipStream_t st, bool drop = false, uint32_t* next_hist = nullptr,
+                       int next_shift = 0, int next_bits = 0) {
     if constexpr (sizeof(K) == 8)
         return launch_cfg<K, Sweep64>(iota, kin, vin, kout, vout, n_cap, n_dev, shift, bits,
-                                      hist_pass, tmp, ticket, st, drop);
+                                      hist_pass, tmp, ticket, st, drop, next_hist, next_shift,
+                                      next_bits);
     return launch_cfg<K, Sweep32>(iota, kin, vin, kout, vout, n_cap, n_dev, shift, bits,
-                                  hist_pass, tmp, ticket, st, drop);
+                                  hist_pass, tmp, ticket, st, drop, next_hist, next_shift,
+                                  next_bits);
 }
 
 template <typename K>
@@ -526,11 +556,15 @@ hipError_t sort_impl(K* keys, uint32_t* vals, int64_t n, int begin_bit, int end_
 // histogram); n is min(n_cap, *n_dev), read on the device. The key bits are
 // spread evenly over the passes (sort_digit_width), and `hist` holds 256 words
 // per pass for digits of that width.
+// chain_hist (optional, the same buffer as hist): only the first pass's
+// histogram is given; each pass adds the next one's. pass_events: record the
+// SortTemp's per-pass events (when it has them).
 template <typename K>
 hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t* n_dev,
                          int begin_bit, int end_bit, const uint32_t* hist, uint32_t* tickets,
                          SortTemp& tmp, hipStream_t st, bool vals_iota, K** keys_final,
-                         uint32_t** vals_final, const uint32_t* n_kept_dev) {
+                         uint32_t** vals_final, const uint32_t* n_kept_dev,
+                         uint32_t* chain_hist = nullptr, bool pass_events = false) {
     *keys_final = keys;
     *vals_final = vals;
     if (n_cap <= 0) return hipSuccess;
@@ -547,8 +581,15 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
         const int bits = std::min(dw, end_bit - shift);
         const bool drop = p == 0 && n_kept_dev != nullptr;
         const uint32_t* cnt = (p > 0 && n_kept_dev != nullptr) ? n_kept_dev : n_dev;
+        const bool chain = chain_hist != nullptr && p + 1 < npass;
+        const int nshift = shift + dw;
+        const bool timed = pass_events && tmp.pass_events != nullptr && p < tmp.max_timed_passes;
+        if (timed) (void)hipEventRecord(tmp.pass_events[2 * p], st);
         hipError_t e = launch_pass<K>(p == 0 && vals_iota, kin, vin, kalt, valt, n_cap, cnt,
-                                      shift, bits, hist + p * 256, tmp, tickets + p, st, drop);
+                                      shift, bits, hist + p * 256, tmp, tickets + p, st, drop,
+                                      chain ? chain_hist + (p + 1) * 256 : nullptr, nshift,
+                                      chain ? std::min(dw, end_bit - nshift) : 0);
+        if (timed) (void)hipEventRecord(tmp.pass_events[2 * p + 1], st);
         if (e != hipSuccess) return e;
         std::swap(kin, kalt);
         std::swap(vin, valt);
@@ -583,6 +624,32 @@ hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const
         return e;
     }
     return hipErrorInvalidValue;
+}
+
+hipError_t radix_sort_pairs_dev_chain(uint64_t* keys, uint32_t* vals, int64_t n, int begin_bit,
+                                      int end_bit, uint32_t* hist, uint32_t* tickets,
+                                      SortTemp& tmp, hipStream_t st, void** keys_final,
+                                      uint32_t** vals_final) {
+    *keys_final = keys;
+    *vals_final = vals;
+    if (n <= 0) return hipSuccess;
+    if (n >= (int64_t)1 << 32) return hipErrorInvalidValue;
+    const int npass = (end_bit - begin_bit + 7) / 8;
+    if (npass <= 0 || npass > kMaxPasses) return hipErrorInvalidValue;
+    const int dw = sort_digit_width(end_bit - begin_bit);
+    // the first pass's histogram only; the passes chain the others
+    const unsigned grid = (unsigned)std::min<int64_t>(
+        (n + kHistThreads * kHistItems - 1) / (kHistThreads * kHistItems), 2048);
+    k_hist<uint64_t><<<grid, kHistThreads, 0, st>>>(keys, n, begin_bit,
+                                                    std::min(end_bit, begin_bit + dw), 1, dw,
+                                                    hist);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    uint64_t* kf = nullptr;
+    e = sort_dev_impl<uint64_t>(keys, vals, n, nullptr, begin_bit, end_bit, hist, tickets, tmp,
+                                st, false, &kf, vals_final, nullptr, hist, true);
+    *keys_final = kf;
+    return e;
 }
 
 size_t sort_partitions(int64_t n) { return (size_t)((n + kMinPart - 1) / kMinPart); }

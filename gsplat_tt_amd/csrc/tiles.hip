@@ -18,8 +18,6 @@
 namespace gs {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / GS_WAVE;
 // The count scan's partitions are chained by a decoupled look-back: 2048 ranks
 // per 512-thread workgroup halve the chain of 1024-rank ones (measured: the
 // tile-assign stage 0.41 -> 0.38 ms; 4096 per workgroup is slower again).
@@ -52,13 +50,32 @@ __device__ __forceinline__ void divmod_small(uint32_t j, uint32_t w, uint32_t& q
     r = (uint32_t)(ri - fix * (int)w);
 }
 
-__device__ __forceinline__ Rect tile_rect(float4 r, const TileParams& tp) {
-    const float ts = (float)tp.tile_size;
+// x / tile_size as the reference computes it (a float division). For a
+// power-of-two tile size the quotient is an exact scaling by 2^-k, which the
+// product with the (exact) reciprocal reproduces bit for bit, denormals
+// included; other sizes divide.
+struct TsDiv {
+    float ts, inv;
+    bool pow2;
+};
+__device__ __forceinline__ TsDiv ts_div(const TileParams& tp) {
+    TsDiv d;
+    d.ts = (float)tp.tile_size;
+    d.pow2 = tp.tile_size > 0 && (tp.tile_size & (tp.tile_size - 1)) == 0;
+    d.inv = d.pow2 ? 1.0f / d.ts : 0.0f;
+    return d;
+}
+__device__ __forceinline__ float div_ts(float x, const TsDiv& d) {
+    if (d.pow2) return x * d.inv;
+    return x / d.ts;
+}
+
+__device__ __forceinline__ Rect tile_rect(float4 r, const TileParams& tp, const TsDiv& d) {
     Rect o;
-    o.x0 = max(0, min((int)((r.x - r.z) / ts), tp.tiles_x - 1));
-    o.x1 = max(0, min((int)((r.x + r.z) / ts), tp.tiles_x - 1));
-    o.y0 = max(0, min((int)((r.y - r.w) / ts), tp.tiles_y - 1));
-    o.y1 = max(0, min((int)((r.y + r.w) / ts), tp.tiles_y - 1));
+    o.x0 = max(0, min((int)div_ts(r.x - r.z, d), tp.tiles_x - 1));
+    o.x1 = max(0, min((int)div_ts(r.x + r.z, d), tp.tiles_x - 1));
+    o.y0 = max(0, min((int)div_ts(r.y - r.w, d), tp.tiles_y - 1));
+    o.y1 = max(0, min((int)div_ts(r.y + r.w, d), tp.tiles_y - 1));
     return o;
 }
 
@@ -135,6 +152,7 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
     // gathers of a thread are in flight together
     const bool gather = rect_r != nullptr;
     const bool want_cov = gather && tp.cull;
+    const TsDiv tsd = ts_div(tp);
     // (indices past m are clamped to m - 1: unconditional loads, no branches
     // whose joins would wait for each load in turn)
     uint32_t gid[kCountItems];
@@ -158,7 +176,7 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
         const int64_t r = base + it * kCountThreads + tid;
         uint32_t c = 0;
         if (r < m) {
-            const Rect q = tile_rect(rr[it], tp);
+            const Rect q = tile_rect(rr[it], tp, tsd);
             c = (uint32_t)((q.x1 - q.x0 + 1) * (q.y1 - q.y0 + 1));
             if (gather) {
                 rect_r[r] = rr[it];
@@ -260,10 +278,11 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     const int64_t rend = (c1 < (uint64_t)p_pre) ? (int64_t)bstart[vid + 1] + 1 : m;
     // every rank owns >= 1 candidate, so nr <= kEmitPart + 1; clamp defensively
     const int64_t nr = min(rend - rlo, (int64_t)kEmitPart + 1);
+    const TsDiv tsd = ts_div(tp);
     for (int64_t k = tid; k < nr; k += kEmitThreads) {
         const int64_t r = rlo + k;
         const float4 rr = rect_r[r];
-        const Rect q = tile_rect(rr, tp);
+        const Rect q = tile_rect(rr, tp, tsd);
         const uint32_t o = offs[r];
         if (k < kRankCache) {
             s_pc[k] = make_float2(rr.x, rr.y);
