@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--n", type=int, default=6_000_000)
     ap.add_argument("--sort-keys", type=int, default=50_000_000)
     ap.add_argument("--no-sort", action="store_true")
+    ap.add_argument("--sort-only", action="store_true",
+                    help="only the 50M-key tile/depth sort leg (for profiling)")
     ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--train-steps", type=int, default=20)
     ap.add_argument("--train-n", type=int, default=1_000_000)
@@ -351,15 +353,25 @@ def bench_sort(ctx, n, tiles=5000):
     dk, dv, dr = ctx.dev_alloc(n * 8), ctx.dev_alloc(n * 4), ctx.dev_alloc(tiles * 8)
     L = ctx._L
     times, passes, pass_ms, ranges_ms = [], 0, [], []
-    for rep in range(5):
-        ctx.h2d(dk, keys)   # restore the unsorted input, outside the timed region
-        ctx.h2d(dv, vals)
-        L.gs_sync(ctx.handle)
-        t0 = time.perf_counter()
-        passes = ctx.sort_tile_depth_dev(dk, dv, n, tiles, dr)
-        times.append(time.perf_counter() - t0)
-        pass_ms.append(ctx.last_sort_pass_ms())
-        ranges_ms.append(ctx.last_ranges_ms())
+    # wall times with the per-pass events off (events between passes add
+    # gaps), then the same calls with them on for the per-pass split
+    from gsplat_tt_amd import _lib as Lm
+    for timed in (0, 1):
+        Lm._check(L.gs_set_timing(ctx.handle, timed))
+        for rep in range(5):
+            ctx.h2d(dk, keys)   # restore the unsorted input, outside the timed region
+            ctx.h2d(dv, vals)
+            L.gs_sync(ctx.handle)
+            t0 = time.perf_counter()
+            passes = ctx.sort_tile_depth_dev(dk, dv, n, tiles, dr)
+            dt = time.perf_counter() - t0
+            if timed:
+                if rep > 0:
+                    pass_ms.append(ctx.last_sort_pass_ms())
+                    ranges_ms.append(ctx.last_ranges_ms())
+            else:
+                times.append(dt)
+    Lm._check(L.gs_set_timing(ctx.handle, 0))
     # spot-check: sortedness, permutation checksum, a prefix against the input
     ko = np.empty(n, np.uint64)
     vo = np.empty(n, np.uint32)
@@ -373,15 +385,15 @@ def bench_sort(ctx, n, tiles=5000):
     for p in (dk, dv, dr):
         ctx.dev_free(p)
     best = min(times[1:])
-    kernel_ms = float(np.mean([sum(p) for p in pass_ms[1:]]))
-    per_pass_ms = float(np.mean([np.mean(p) for p in pass_ms[1:] if p]))
+    kernel_ms = float(np.mean([sum(p) for p in pass_ms]))
+    per_pass_ms = float(np.mean([np.mean(p) for p in pass_ms if p]))
     bytes_total = n * (24 * passes + 8)
     traffic = pmc_traffic("sort_50M")
     ach = bytes_total / best / 1e9
     return {
         "keys": n, "tiles": tiles, "zipf_s": 1.1, "passes": passes, "ok": ok,
         "wall_ms": round(best * 1e3, 3), "passes_ms": round(kernel_ms, 3),
-        "ranges_ms": round(float(np.mean(ranges_ms[1:])), 4),
+        "ranges_ms": round(float(np.mean(ranges_ms)), 4),
         "gkeys_per_s": round(n / best / 1e9, 3),
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
@@ -553,6 +565,12 @@ def main():
         return
     if args.sequential_frames:
         sequential_frames(args)
+        return
+    if args.sort_only:
+        from gsplat_tt_amd import _lib as L
+        ctx = L.Context(0, timing=False)
+        print(json.dumps({"sort": bench_sort(ctx, args.sort_keys)}), flush=True)
+        ctx.close()
         return
     ctx, scene, cov, cams, stats, dt = bench_frames(args)
     tiles = ((cams[0].width + 15) // 16) * ((cams[0].height + 15) // 16)
