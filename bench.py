@@ -371,7 +371,7 @@ def bench_sort(ctx, n, tiles=5000):
                     ranges_ms.append(ctx.last_ranges_ms())
             else:
                 times.append(dt)
-    Lm._check(L.gs_set_timing(ctx.handle, 0))
+    # the later legs (training) report stage times: leave the events on
     # spot-check: sortedness, permutation checksum, a prefix against the input
     ko = np.empty(n, np.uint64)
     vo = np.empty(n, np.uint32)
@@ -417,6 +417,7 @@ def bench_train(ctx, n, steps):
     from gsplat_tt_amd import _lib as L
     from gsplat_tt_amd import scenes
 
+    L._check(ctx._L.gs_set_timing(ctx.handle, 1))  # per-phase events for the rooflines
     t = time.time()
     scene, tgt_scene, cams = scenes.config5(n=n)
     cam = cams[0]
