@@ -159,36 +159,56 @@ def stage_summary(n, sh_degree, tiles, stats):
     }
 
 
-def dominant_roofline(st):
+def dominant_roofline(st, tag, deg, out):
     """The roofline object of the frame's dominant kernel: k_project (the project
     stage is that one kernel plus a small histogram reduction, HBM-bound) or
-    k_blend (FP32 VALU-bound; no MFMA on this path), whichever takes longer."""
+    k_blend (FP32 VALU-bound; no MFMA on this path), whichever takes longer.
+    `traffic` is the kernel's PMC-measured HBM bytes per dispatch for this
+    workload (profiles/frame_<tag>_pmc_traffic.md), for the kernel instance the
+    workload runs (k_project<sh degree>, k_blend<tile, output format>)."""
+    proj_k = f"k_project<{deg}>"
+    blend_k = f"k_blend<16, {ORDER_OUT.index(out)}>"
     r = st["roofline"]
     proj_ms, blend_ms = r["project"]["ms"], r["blend"]["ms"]
     if blend_ms >= proj_ms:
         b = r["blend"]
         return {"kernel": "k_blend", "bound": "valu", "pipe": "fp32 VALU (no MFMA issued)",
                 "achieved": b["achieved_tflops"], "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": b["frac_fp32"], "traffic": pmc_traffic("k_blend"),
+                "frac": b["frac_fp32"], "traffic": pmc_traffic(blend_k, tag),
                 "flops_per_launch": b["flops"], "ms_per_launch": b["ms"],
                 "work_model": "20 FP32 flops per pixel-Gaussian evaluation"}
     p = r["project"]
     return {"kernel": "k_project", "bound": "hbm", "achieved": p["achieved_gbs"],
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": p["frac_hbm"],
-            "traffic": pmc_traffic("k_project"), "bytes_per_launch": p["bytes"],
+            "traffic": pmc_traffic(proj_k, tag), "bytes_per_launch": p["bytes"],
             "ms_per_launch": p["ms"],
             "work_model": "N*(12+24+4+12*(d+1)^2) B read + M*48 B written"}
 
 
-def pmc_traffic(kernel):
-    """HBM bytes per dispatch of `kernel` from the committed rocprofv3 PMC summary
-    (FETCH_SIZE and WRITE_SIZE scaled by a copy-kernel calibration), or None."""
+ORDER_OUT = ("u8", "bf16", "f32")  # k_blend's output-format template argument
+
+
+def pmc_traffic(kernel, tag):
+    """HBM bytes per dispatch of `kernel` in workload `tag` from the committed
+    rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE scaled by a copy-kernel
+    calibration), or None when no summary holds it."""
     import re
-    path = os.path.join(ROOT, "profiles", f"{kernel}_pmc_traffic.md")
+    path = os.path.join(ROOT, "profiles", f"frame_{tag}_pmc_traffic.md")
     if not os.path.exists(path):
         return None
-    m = re.search(r"traffic_bytes_per_dispatch\s*=\s*([0-9_,]+)", open(path).read())
-    return int(m.group(1).replace(",", "").replace("_", "")) if m else None
+    m = re.search(r"traffic_bytes_per_dispatch\[" + re.escape(kernel) + r"\]\s*=\s*([0-9]+)",
+                  open(path).read())
+    return int(m.group(1)) if m else None
+
+
+def sort_traffic():
+    """HBM bytes of one 50M-key tile/depth sort call from its PMC summary, or None."""
+    import re
+    path = os.path.join(ROOT, "profiles", "sort_50M_pmc_traffic.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_call\s*=\s*([0-9]+)", open(path).read())
+    return int(m.group(1)) if m else None
 
 
 def copy_calibration(nbytes):
@@ -300,7 +320,7 @@ def bench_host_out(ctx, cams, frames):
     return res
 
 
-def bench_view(ctx, name, scene, cam, steps, warmup, cpu_frames, cpu_threads, out="bf16"):
+def bench_view(ctx, name, tag, scene, cam, steps, warmup, cpu_frames, cpu_threads, out="bf16"):
     """One workload's single view, rendered `steps` times through gs_render_batch
     (three frames in flight), then 8 frames one at a time with per-stage events;
     the reference's CPU renderer on the same view for the CPU figure."""
@@ -331,7 +351,7 @@ def bench_view(ctx, name, scene, cam, steps, warmup, cpu_frames, cpu_threads, ou
                        f"{'SH degree %d' % deg if deg >= 0 else 'RGB'}, 16x16 tiles, {out} out, "
                        "one view", "frames": steps, "frames_per_s": round(steps / dt, 1),
            "ms_per_frame": round(dt / steps * 1e3, 4), "stages": st,
-           "roofline": dominant_roofline(st)}
+           "roofline": dominant_roofline(st, tag, deg, out)}
     if cpu_frames > 0:
         res["cpu_baseline"] = cpu_baseline(scene, cov, [cam], cpu_frames, cpu_threads,
                                            f"{cpu_frames} renders of the {name} view after 1 "
@@ -388,7 +408,7 @@ def bench_sort(ctx, n, tiles=5000):
     kernel_ms = float(np.mean([sum(p) for p in pass_ms]))
     per_pass_ms = float(np.mean([np.mean(p) for p in pass_ms if p]))
     bytes_total = n * (24 * passes + 8)
-    traffic = pmc_traffic("sort_50M")
+    traffic = sort_traffic() if n == 50_000_000 else None
     ach = bytes_total / best / 1e9
     return {
         "keys": n, "tiles": tiles, "zipf_s": 1.1, "passes": passes, "ok": ok,
@@ -591,7 +611,7 @@ def main():
                    "frames_in_flight": FRAMES_IN_FLIGHT,
                    "stage_times": "16 frames one at a time with per-stage hipEvents"},
         "stages": st,
-        "roofline": dominant_roofline(st),
+        "roofline": dominant_roofline(st, "6M", 3, "bf16"),
         "blend": {"ms": st["roofline"]["blend"]["ms"],
                   "achieved_tflops": st["roofline"]["blend"]["achieved_tflops"],
                   "frac_fp32": st["roofline"]["blend"]["frac_fp32"]},
@@ -610,10 +630,10 @@ def main():
     if not args.no_views:
         from gsplat_tt_amd import scenes
         s1, c1 = scenes.config1()
-        res["c1_100k"] = bench_view(ctx, "100K", s1, c1[0], args.view_steps, 8,
+        res["c1_100k"] = bench_view(ctx, "100K", "100K", s1, c1[0], args.view_steps, 8,
                                     0 if args.no_cpu else 5, args.cpu_threads, out="f32")
         s2, c2 = scenes.config2()
-        res["c2_1m"] = bench_view(ctx, "1M SH3", s2, c2[0], args.view_steps, 8,
+        res["c2_1m"] = bench_view(ctx, "1M SH3", "1M", s2, c2[0], args.view_steps, 8,
                                   0 if args.no_cpu else 3, args.cpu_threads, out="bf16")
         del s1, s2
     if not args.no_sort:
