@@ -27,7 +27,7 @@ FP32_PEAK_TFLOPS = 157.3     # MI355X FP32 peak (packed FP32 VALU issue)
 # clamp, exp, alpha (mul + min), alpha*T, 3 colour FMA, T update; FMA = 2 flops
 BLEND_FLOPS_PER_EVAL = 20
 # frame slots of gs_render_batch; one output buffer per slot
-FRAMES_IN_FLIGHT = 3
+FRAMES_IN_FLIGHT = 4
 # host threads of one GPU's share of the box (its worker pools are sized to it)
 BOX_CPU_SHARE = 16
 
@@ -72,7 +72,7 @@ def parse():
 
 def bench_frames(args):
     """The orbit: `warmup` untimed frames, then `steps` frames timed as one camera
-    path through gs_render_batch (three frames in flight on three streams), with the
+    path through gs_render_batch (four frames in flight on four streams), with the
     per-stage hipEvents off; then 16 frames one at a time with the events on,
     for the per-stage times and the blend diagnostics."""
     from gsplat_tt_amd import _lib as L
@@ -322,7 +322,7 @@ def bench_host_out(ctx, cams, frames):
 
 def bench_view(ctx, name, tag, scene, cam, steps, warmup, cpu_frames, cpu_threads, out="bf16"):
     """One workload's single view, rendered `steps` times through gs_render_batch
-    (three frames in flight), then 8 frames one at a time with per-stage events;
+    (four frames in flight), then 8 frames one at a time with per-stage events;
     the reference's CPU renderer on the same view for the CPU figure."""
     from gsplat_tt_amd import _lib as L
     from gsplat_tt_amd import scenes

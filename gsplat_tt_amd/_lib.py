@@ -332,7 +332,7 @@ class Context:
         return size.value, held.value, grows.value, replaced.value
 
     def render_batch(self, views, outs, out_on_device=True):
-        """Views rendered with up to three frames in flight; outs: device pointers (or host
+        """Views rendered with up to four frames in flight; outs: device pointers (or host
         arrays when out_on_device is False), one per view. Returns their stats."""
         n = len(views)
         varr = (GsView * n)(*views)

@@ -105,8 +105,8 @@ int gs_device_info(gs_ctx* ctx, int* num_cus, int* arch_minor);
  * out_on_device. M == 0 gives a black image. */
 int gs_scene_set(gs_ctx* ctx, const gs_scene* scene);
 int gs_render(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device, gs_stats* stats);
-/* n views of the scene (a camera path), as n gs_render calls, with up to three
- * frames in flight on three streams: a view is enqueued before the earlier ones
+/* n views of the scene (a camera path), as n gs_render calls, with up to four
+ * frames in flight on four streams: a view is enqueued before the earlier ones
  * are waited for, so one frame's last stages overlap the next frame's first
  * ones (the cross-view pipelining of render/host/xview.h and the next_extrinsics
  * argument of render/host/render.cpp:263-273, for a known list of views).

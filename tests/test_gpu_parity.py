@@ -383,7 +383,7 @@ def test_render_batch_capacity_retry():
     cov = O.cov3d(scales, quats)
     K = scenes.intrinsics(500, 500, 320, 240)
     w2cs = []
-    for k in range(3):
+    for k in range(4):  # one view per frame slot of gs_render_batch
         w2c = np.eye(4, dtype=np.float32)
         w2c[0, 3] = 0.05 * k
         w2cs.append(w2c)
