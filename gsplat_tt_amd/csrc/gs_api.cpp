@@ -211,7 +211,7 @@ struct gs_ctx {
                           &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_bstart, &b_pair_tile, &b_pair_id,
                           &b_ranges, &b_out, &b_kalt, &b_valt, &b_hist, &b_state, &b_lb, &b_cnt,
                           &b_tmp_a, &b_tmp_b, &b_tmp_c, &b_evals, &b_frame, &b_phist_proj,
-                          &b_phist_emit, &b_rect_r, &b_cov_r, &b_spec, &b_chunk_box, &b_skip})
+                          &b_phist_emit, &b_spec, &b_chunk_box, &b_skip})
             b->release();
         if (h_pin) (void)hipHostFree(h_pin);
         ring.reset();  // held images stay valid until their leases are released
@@ -347,6 +347,9 @@ struct gs_ctx {
         REQUIRE((int64_t)v->image_height * v->image_width <= ((int64_t)1 << 28),
                 "view: image too large");
         REQUIRE(v->tile_size == 16 || v->tile_size == 32, "view: tile_size must be 16 or 32");
+        REQUIRE((v->image_width + v->tile_size - 1) / v->tile_size <= 65535 &&
+                    (v->image_height + v->tile_size - 1) / v->tile_size <= 65535,
+                "view: at most 65535 tiles per row and per column");
         REQUIRE(v->out_format >= GS_OUT_U8 && v->out_format <= GS_OUT_F32, "view: bad out_format");
         REQUIRE(v->contrib_floor > 0.0f && v->mb_contrib_floor > 0.0f, "view: floors must be > 0");
     }
@@ -471,11 +474,11 @@ struct gs_ctx {
         for (int attempt = 0; attempt < 2; ++attempt) {
             HIPCHK(gs::launch_fill_u32(b_cnt.as<uint32_t>() + 8, 0u, 8, st));
             HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, rparts * 2, st));
-            HIPCHK(gs::launch_rect_count_scan(rect, cov, 1, order, m, nullptr, tpc,
+            HIPCHK(gs::launch_rect_count_scan(rect, 1, order, m, nullptr, tpc,
                                               b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(),
                                               (uint32_t)(b_bstart.cap / 4), b_lb.as<uint64_t>(),
                                               b_cnt.as<uint32_t>() + 8, b_cnt.as<uint32_t>() + 9,
-                                              nullptr, nullptr, st));
+                                              st));
             HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
             sync();
             ctl_check(h_pin[C_CTL], "tile_assign");
@@ -493,7 +496,7 @@ struct gs_ctx {
         const size_t eparts = gs::emit_partitions(p_pre);
         b_lb.ensure(eparts * 8);
         HIPCHK(gs::launch_fill_u32(b_lb.as<uint32_t>(), 0u, eparts * 2, st));
-        HIPCHK(gs::launch_pair_emit(rect, cov, order, b_offs.as<uint32_t>(),
+        HIPCHK(gs::launch_pair_emit(rect, cov, 1, false, order, b_offs.as<uint32_t>(),
                                     b_bstart.as<uint32_t>(), m, nullptr, p_pre, nullptr, tpc,
                                     b_pair_tile.as<uint32_t>(), b_pair_id.as<uint32_t>(), p_pre,
                                     b_lb.as<uint64_t>(), b_cnt.as<uint32_t>() + 10,
@@ -517,7 +520,7 @@ struct gs_ctx {
         C_MBSTAT = 40  // two u64: pairs no microblock keeps, kept (pair, microblock)
     };
     uint64_t pair_cap = 0;  // candidate-pair capacity of the frame buffers
-    DevBuf b_frame, b_phist_proj, b_phist_emit, b_rect_r, b_cov_r;
+    DevBuf b_frame, b_phist_proj, b_phist_emit;
 
     // One frame with no host synchronisation until the end: every size that
     // only the device knows (visible count, candidate and kept pairs) is read
@@ -837,8 +840,6 @@ struct gs_ctx {
         b_src.ensure((size_t)N * 4);
         b_tmp_a.ensure((size_t)N * 4);
         b_offs.ensure((size_t)N * 4);
-        b_rect_r.ensure((size_t)N * 16);
-        b_cov_r.ensure((size_t)N * 16);
         b_bstart.ensure((L.eparts + 1) * 4);
         b_pair_tile.ensure((size_t)L.pcap * 4);
         b_pair_id.ensure((size_t)L.pcap * 4);
@@ -873,12 +874,11 @@ struct gs_ctx {
                                         fr + kFrDepthHist, cnt + C_DSORT_TICKETS, sort, st, true,
                                         &kf, &order));
         record(2);
-        HIPCHK(gs::launch_rect_count_scan(b_rc.as<float4>(), b_rc.as<float4>() + 1, 2, order, N,
-                                          cnt + C_M, tp, b_offs.as<uint32_t>(),
-                                          b_bstart.as<uint32_t>(), (uint32_t)(L.eparts + 1),
-                                          L.lb_rect, cnt + C_RECT_TICKET, cnt + C_PPRE,
-                                          b_rect_r.as<float4>(), b_cov_r.as<float4>(), st));
-        HIPCHK(gs::launch_pair_emit(b_rect_r.as<float4>(), b_cov_r.as<float4>(), order,
+        HIPCHK(gs::launch_rect_count_scan(b_rc.as<float4>(), 2, order, N, cnt + C_M, tp,
+                                          b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(),
+                                          (uint32_t)(L.eparts + 1), L.lb_rect,
+                                          cnt + C_RECT_TICKET, cnt + C_PPRE, st));
+        HIPCHK(gs::launch_pair_emit(b_rc.as<float4>(), b_rc.as<float4>() + 1, 2, true, order,
                                     b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(), N, cnt + C_M,
                                     L.pcap, cnt + C_PPRE, tp, b_pair_tile.as<uint32_t>(),
                                     b_pair_id.as<uint32_t>(), L.pcap, L.lb_emit,
@@ -1537,6 +1537,9 @@ int gs_tile_assign(gs_ctx* ctx, const float* means2d, const float* radii, int64_
         REQUIRE(ctx && p_out, "null argument");
         REQUIRE(m >= 0 && m < ((int64_t)1 << 31), "m out of range");
         REQUIRE(image_height > 0 && image_width > 0 && tile_size > 0, "bad image/tile size");
+        REQUIRE(((int64_t)image_width + tile_size - 1) / tile_size <= 65535 &&
+                    ((int64_t)image_height + tile_size - 1) / tile_size <= 65535,
+                "at most 65535 tiles per row and per column");
         REQUIRE(m == 0 || (means2d && radii), "null means2d/radii");
         HIPCHK(hipSetDevice(ctx->device));
         ctx->drain_spec();

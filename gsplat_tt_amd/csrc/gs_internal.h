@@ -167,15 +167,12 @@ struct TileParams {
 // Sizes: m / p_pre / p are host capacities sizing the grids; when the *_dev
 // pointer is given the real count is read on the device (min with the
 // capacity) and partitions beyond it exit at once.
-// rect_r / cov_r (optional): rect[order[r]] / cov[order[r]] gathered into
-// rank order (cov_r only with the cull on), the inputs of launch_pair_emit.
-// stride: element stride of rect / cov in float4 (2 for interleaved records).
-hipError_t launch_rect_count_scan(const float4* rect, const float4* cov, int stride,
-                                  const uint32_t* order, int64_t m, const uint32_t* m_dev,
-                                  TileParams tp, uint32_t* offs,
+// Rank r's rectangle is rect[order[r] * stride] (order null: rect[r * stride]);
+// stride is in float4 (2 for the interleaved rectangle + conic records).
+hipError_t launch_rect_count_scan(const float4* rect, int stride, const uint32_t* order,
+                                  int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
                                   uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
-                                  uint32_t* ticket, uint32_t* total_out, float4* rect_r,
-                                  float4* cov_r, hipStream_t st);
+                                  uint32_t* ticket, uint32_t* total_out, hipStream_t st);
 // Digit width of a device sort over `bits` key bits: the fewest 8-bit-or-less
 // passes, with the bits spread evenly over them (12 tile bits: two passes of 6,
 // whose 64 digits give longer runs per digit than 256 would).
@@ -187,13 +184,15 @@ inline int sort_digit_width(int bits) {
 // tile bits (rows of 512 words), three above (rows of 1024 words, the last 256
 // zero).
 inline int tile_hist_cols(int tile_bits) { return tile_bits > 16 ? 1024 : 512; }
-// rect_r / cov_r are indexed by rank (rect[order[r]], ...; the plain arrays
-// when order is null); pair ids are order[r]. part_hist (optional):
-// per-partition digit histograms of the kept pairs' tile ids, one row of
-// tile_hist_cols(tile_bits) words per emit partition: 256 words per digit of
-// sort_digit_width(tile_bits) bits, lowest digit first.
-hipError_t launch_pair_emit(const float4* rect_r, const float4* cov_r, const uint32_t* order,
-                            const uint32_t* offs, const uint32_t* bstart, int64_t m,
+// Rank r's rectangle and conic are rect / cov[e * stride] with e = order[r]
+// when by_order (records in compact order, as the projection writes them),
+// else e = r (records already in rank order); pair ids are order[r] (r when
+// order is null). part_hist (optional): per-partition digit histograms of the
+// kept pairs' tile ids, one row of tile_hist_cols(tile_bits) words per emit
+// partition: 256 words per digit of sort_digit_width(tile_bits) bits, lowest
+// digit first.
+hipError_t launch_pair_emit(const float4* rect, const float4* cov, int stride, bool by_order,
+                            const uint32_t* order, const uint32_t* offs, const uint32_t* bstart, int64_t m,
                             const uint32_t* m_dev, uint32_t p_pre, const uint32_t* p_pre_dev,
                             TileParams tp, uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
                             uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,

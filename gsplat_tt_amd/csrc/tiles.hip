@@ -118,10 +118,8 @@ __device__ __forceinline__ bool pair_keep(float px, float py, float4 cv, int til
 // Rectangle area per rank, exclusive scan -> offs[r]; last partition writes
 // the total candidate count (saturated to 0xFFFFFFFF on overflow).
 // Also records, for every emit partition b (candidates [b*kEmitPart, ...)),
-// the rank that owns its first candidate: bstart[b]. With rect_r / cov_r
-// given, the rectangles and conics are also gathered into rank order.
+// the rank that owns its first candidate: bstart[b].
 __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4* __restrict__ rect,
-                                                              const float4* __restrict__ cov,
                                                               int stride,
                                                               const uint32_t* __restrict__ order,
                                                               int64_t m_cap,
@@ -132,9 +130,7 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
                                                               uint32_t bstart_cap,
                                                               uint64_t* lb_state,
                                                               uint32_t* ticket,
-                                                              uint32_t* total_out,
-                                                              float4* __restrict__ rect_r,
-                                                              float4* __restrict__ cov_r) {
+                                                              uint32_t* total_out) {
     __shared__ uint32_t s_vid;
     __shared__ uint32_t s_wsum[kCountItems][kCountWaves];
     __shared__ uint64_t s_excl;
@@ -148,15 +144,13 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
     const uint32_t nparts = (uint32_t)((m + kCountPart - 1) / kCountPart);
     if (vid >= nparts) return;  // no later partition has work either
     const int64_t base = (int64_t)vid * kCountPart;
-    // loads in stages (all ranks' ids, then all records) so that the four
+    // loads in stages (all ranks' ids, then all rectangles) so that the four
     // gathers of a thread are in flight together
-    const bool gather = rect_r != nullptr;
-    const bool want_cov = gather && tp.cull;
     const TsDiv tsd = ts_div(tp);
     // (indices past m are clamped to m - 1: unconditional loads, no branches
     // whose joins would wait for each load in turn)
     uint32_t gid[kCountItems];
-    float4 rr[kCountItems], cv[kCountItems];
+    float4 rr[kCountItems];
 #pragma unroll
     for (int it = 0; it < kCountItems; ++it)
         gid[it] = (uint32_t)min(base + it * kCountThreads + tid, m - 1);
@@ -166,10 +160,6 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
     }
 #pragma unroll
     for (int it = 0; it < kCountItems; ++it) rr[it] = rect[(int64_t)gid[it] * stride];
-    if (want_cov) {
-#pragma unroll
-        for (int it = 0; it < kCountItems; ++it) cv[it] = cov[(int64_t)gid[it] * stride];
-    }
     uint32_t incl[kCountItems], cnt[kCountItems];
 #pragma unroll
     for (int it = 0; it < kCountItems; ++it) {
@@ -178,10 +168,6 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
         if (r < m) {
             const Rect q = tile_rect(rr[it], tp, tsd);
             c = (uint32_t)((q.x1 - q.x0 + 1) * (q.y1 - q.y0 + 1));
-            if (gather) {
-                rect_r[r] = rr[it];
-                if (want_cov) cov_r[r] = cv[it];
-            }
         }
         cnt[it] = c;
         incl[it] = wave_incl_scan(c);
@@ -225,7 +211,9 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
 // Pair-centric emission: candidate c -> (rank r, j-th tile of r's rectangle),
 // cull, stable compaction of kept pairs in candidate order. The ranks of a
 // partition are [bstart[vid], bstart[vid+1]]; each candidate finds its rank by
-// an inclusive max-scan over rank heads in LDS.
+// an inclusive max-scan over rank heads in LDS. A rank's rectangle and conic
+// are read once per partition, from its record in compact order (by_order:
+// the lines the count scan fetched just before, not a rank-ordered copy).
 // COMPACT: kept pairs are compacted (ticket-ordered partitions, look-back).
 // Otherwise every candidate slot c < cap is written, the tile id of a kept
 // pair or kPairDrop for a culled one (the pair id only for kept ones), and the
@@ -234,8 +222,8 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
 // NDIG: tile-id digit histograms made (2, or 3 above 16 tile bits).
 template <bool COMPACT, int NDIG>
 __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
-    const float4* __restrict__ rect_r, const float4* __restrict__ cov_r,
-    const uint32_t* __restrict__ order, const uint32_t* __restrict__ offs,
+    const float4* __restrict__ rect, const float4* __restrict__ cov, int stride,
+    bool by_order, const uint32_t* __restrict__ order, const uint32_t* __restrict__ offs,
     const uint32_t* __restrict__ bstart, int64_t m_cap, const uint32_t* __restrict__ m_dev,
     uint32_t p_pre_cap, const uint32_t* __restrict__ p_pre_dev, TileParams tp,
     uint32_t* __restrict__ pair_tile, uint32_t* __restrict__ pair_id, uint32_t cap,
@@ -281,12 +269,13 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     const TsDiv tsd = ts_div(tp);
     for (int64_t k = tid; k < nr; k += kEmitThreads) {
         const int64_t r = rlo + k;
-        const float4 rr = rect_r[r];
+        const int64_t e = by_order ? (int64_t)order[r] : r;  // the rank's record
+        const float4 rr = rect[e * stride];
         const Rect q = tile_rect(rr, tp, tsd);
         const uint32_t o = offs[r];
         if (k < kRankCache) {
             s_pc[k] = make_float2(rr.x, rr.y);
-            if (tp.cull) s_cv[k] = cov_r[r];
+            if (tp.cull) s_cv[k] = cov[e * stride];
         }
         s_off[k] = o;
         s_xy[k] = (uint32_t)q.x0 | ((uint32_t)q.y0 << 16);
@@ -366,8 +355,10 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
             float4 rr[kEmitItems], cv[kEmitItems];
 #pragma unroll
             for (int it = 0; it < kEmitItems; ++it) {
-                rr[it] = rect_r[rlo + lo[it]];
-                cv[it] = cov_r[rlo + lo[it]];
+                const int64_t r = rlo + lo[it];
+                const int64_t e = by_order ? (int64_t)order[r] : r;
+                rr[it] = rect[e * stride];
+                cv[it] = cov[e * stride];
             }
 #pragma unroll
             for (int it = 0; it < kEmitItems; ++it)
@@ -593,34 +584,40 @@ hipError_t launch_tile_ranges64(const uint64_t* keys, uint32_t p, uint32_t* rang
 size_t rect_scan_partitions(int64_t m) { return (size_t)((m + kCountPart - 1) / kCountPart); }
 size_t emit_partitions(uint64_t p_pre) { return (size_t)((p_pre + kEmitPart - 1) / kEmitPart); }
 
-hipError_t launch_rect_count_scan(const float4* rect, const float4* cov, int stride,
-                                  const uint32_t* order, int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
+hipError_t launch_rect_count_scan(const float4* rect, int stride, const uint32_t* order,
+                                  int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
                                   uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
-                                  uint32_t* ticket, uint32_t* total_out, float4* rect_r,
-                                  float4* cov_r, hipStream_t st) {
+                                  uint32_t* ticket, uint32_t* total_out, hipStream_t st) {
     if (m <= 0) return hipSuccess;
+    if (stride < 1) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)rect_scan_partitions(m);
-    k_rect_count_scan<<<grid, kCountThreads, 0, st>>>(rect, cov, stride, order, m, m_dev, tp, offs, bstart,
-                                                 bstart_cap, lb_state, ticket, total_out, rect_r,
-                                                 cov_r);
+    k_rect_count_scan<<<grid, kCountThreads, 0, st>>>(rect, stride, order, m, m_dev, tp, offs,
+                                                      bstart, bstart_cap, lb_state, ticket,
+                                                      total_out);
     return hipGetLastError();
 }
 
-hipError_t launch_pair_emit(const float4* rect_r, const float4* cov_r, const uint32_t* order,
+hipError_t launch_pair_emit(const float4* rect, const float4* cov, int stride, bool by_order,
+                            const uint32_t* order,
                             const uint32_t* offs, const uint32_t* bstart, int64_t m,
                             const uint32_t* m_dev, uint32_t p_pre, const uint32_t* p_pre_dev,
                             TileParams tp, uint32_t* pair_tile, uint32_t* pair_id, uint32_t cap,
                             uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
                             uint32_t* part_hist, int tile_bits, bool compact, hipStream_t st) {
     if (p_pre == 0 || m <= 0) return hipSuccess;
+    if (stride < 1 || (by_order && order == nullptr)) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)emit_partitions(p_pre);
     // at most three digits of at most 8 bits (tile ids below 2^24)
     if (tile_bits < 1 || tile_bits > 24) return hipErrorInvalidValue;
+    // a rectangle's corner is held in two 16-bit fields
+    if (tp.tiles_x < 1 || tp.tiles_x > 65535 || tp.tiles_y < 1 || tp.tiles_y > 65535)
+        return hipErrorInvalidValue;
     const int dbits = sort_digit_width(tile_bits);
     const bool three = tile_hist_cols(tile_bits) > 512;
 #define GS_EMIT(CP, ND)                                                                    \
     k_pair_emit<CP, ND><<<grid, kEmitThreads, 0, st>>>(                                    \
-        rect_r, cov_r, order, offs, bstart, m, m_dev, p_pre, p_pre_dev, tp, pair_tile, pair_id, \
+        rect, cov, stride, by_order, order, offs, bstart, m, m_dev, p_pre, p_pre_dev, tp,    \
+        pair_tile, pair_id,                                                                \
         cap, lb_state, ticket, total_out, part_hist, dbits)
     if (compact) {
         if (three) GS_EMIT(true, 3); else GS_EMIT(true, 2);

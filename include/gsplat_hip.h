@@ -187,7 +187,8 @@ int gs_project(gs_ctx* ctx, const gs_scene* scene, const gs_view* view,
 /* gs_tile_assign: tile_assign, src/gsplat_cpu/tile_assign.cpp:26-368.
  * covs2d (m,4) and opac (m) may be NULL (no per-pair cull). Pairs are
  * Gaussian-major. Writes at most `cap` pairs; *p_out = P, *p_pre_out =
- * pairs before the cull (cap < P -> GS_E_CAPACITY, nothing written). */
+ * pairs before the cull (cap < P -> GS_E_CAPACITY, nothing written).
+ * At most 65535 tiles per row and per column (also for views). */
 int gs_tile_assign(gs_ctx* ctx, const float* means2d, const float* radii, int64_t m,
                    int image_height, int image_width, int tile_size, const float* covs2d,
                    const float* opac, float contrib_floor, int64_t* gids, int64_t* tids,

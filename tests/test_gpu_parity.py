@@ -206,6 +206,9 @@ def test_render_edge_cases(gpu_ctx):
     assert np.abs(img - ref).max() <= 1e-5
     with pytest.raises(ValueError):
         gpu_ctx.render(L.make_view(cam.w2c, cam.K, 64, 80, tile_size=24))
+    # a tile grid wider than 65535 tiles is refused before anything is launched
+    with pytest.raises(ValueError):
+        gpu_ctx.render(L.make_view(cam.w2c, cam.K, 1, 65535 * 16 + 1, output="u8"))
 
 
 def test_render_degenerate_inputs(gpu_ctx):
