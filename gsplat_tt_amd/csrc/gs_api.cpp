@@ -136,6 +136,13 @@ int tile_bits(int64_t num_tiles) {
     return std::max(b, 1);
 }
 
+// Index bits of the frame's packed depth-sort values over n Gaussians (the
+// tile count takes the rest of the word), 0 when too few bits would be left.
+int dval_idx_bits(int64_t n) {
+    const int b = tile_bits(n);
+    return b <= 28 ? b : 0;
+}
+
 }  // namespace
 
 struct gs_ctx {
@@ -868,11 +875,13 @@ struct gs_ctx {
         uint32_t* cnt = L.cnt;
         sort.ctl = cnt + C_CTL;
         // depth order of the visible Gaussians (stable: ties keep index order)
+        // (values: the projection's packed ones when tp.idx_bits is set, else
+        // the compact indices 0..M-1)
         void* kf = nullptr;
         uint32_t* order = nullptr;
         HIPCHK(gs::radix_sort_pairs_dev(b_dkey.p, b_tmp_a.as<uint32_t>(), N, cnt + C_M, 4, 0, 32,
-                                        fr + kFrDepthHist, cnt + C_DSORT_TICKETS, sort, st, true,
-                                        &kf, &order));
+                                        fr + kFrDepthHist, cnt + C_DSORT_TICKETS, sort, st,
+                                        tp.idx_bits == 0, &kf, &order));
         record(2);
         HIPCHK(gs::launch_rect_count_scan(b_rc.as<float4>(), 2, order, N, cnt + C_M, tp,
                                           b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(),
@@ -886,7 +895,8 @@ struct gs_ctx {
                                     tile_bits(T), false, st));
         HIPCHK(gs::launch_reduce_rows(b_phist_emit.as<uint32_t>(),
                                       gs::tile_hist_cols(tile_bits(T)), (uint32_t)L.eparts,
-                                      cnt + C_PPRE, L.pcap, gs::kEmitPartition, fr + kFrTileHist,
+                                      cnt + C_PPRE, L.pcap, gs::kEmitPartition,
+                                      gs::sort_digit_width(tile_bits(T)), fr + kFrTileHist,
                                       st));
         record(3);
         // stable tile sort of the depth-ordered candidate slots; its first pass
@@ -914,6 +924,12 @@ struct gs_ctx {
         if (timing) HIPCHK(gs::launch_fill_u32(b_evals.as<uint32_t>(), 0u, 64 * 8 * 2, st));
         gs::ProjParams p = proj_params(v);
         p.ctl = L.cnt + C_CTL;
+        // depth-sort values carry each Gaussian's tile count
+        p.tiles_x = tiles_x;
+        p.tiles_y = tiles_y;
+        p.tile_size = v->tile_size;
+        p.idx_bits = dval_idx_bits(N);
+        p.dvals = p.idx_bits ? b_tmp_a.as<uint32_t>() : nullptr;
         // the boxes bound three standard deviations: no skipping for wider k
         if (sd.chunk_box != nullptr && v->k_cap <= 3.0f) {
             b_skip.ensure(gs::project_partitions(N));
@@ -926,10 +942,10 @@ struct gs_ctx {
         HIPCHK(gs::launch_project(sd, p, c, nullptr, L.lb_proj, L.cnt + C_PROJ_TICKET,
                                   L.cnt + C_M, b_phist_proj.as<uint32_t>(), st));
         HIPCHK(gs::launch_reduce_rows(b_phist_proj.as<uint32_t>(), 1024, (uint32_t)L.pparts,
-                                      nullptr, 0, 0, L.fr + kFrDepthHist, st));
+                                      nullptr, 0, 0, 0, L.fr + kFrDepthHist, st));
         record(1);
         gs::TileParams tp{tiles_x, tiles_y, v->tile_size, v->cull_disabled ? 0 : 1,
-                          L.cnt + C_CTL};
+                          L.cnt + C_CTL, p.idx_bits};
         uint32_t* tiles_sorted = nullptr;
         uint32_t* ids_sorted = frame_tiles(L, N, T, tp, &tiles_sorted);
         record(4);
@@ -1141,7 +1157,7 @@ struct gs_ctx {
                                         L.cnt + C_PROJ_TICKET, L.cnt + C_M,
                                         b_phist_proj.as<uint32_t>(), dbg, st));
         HIPCHK(gs::launch_reduce_rows(b_phist_proj.as<uint32_t>(), 1024, (uint32_t)L.pparts,
-                                      nullptr, 0, 0, L.fr + kFrDepthHist, st));
+                                      nullptr, 0, 0, 0, L.fr + kFrDepthHist, st));
         gs::TileParams tp{tr.tiles_x, tr.tiles_y, 16, 1, L.cnt + C_CTL};
         tr.ids = frame_tiles(L, std::max<int64_t>(N, 1), T, tp, nullptr);
         gs::TrainFwdParams fp{};

@@ -66,6 +66,59 @@ __device__ __forceinline__ void hist_add_wave(uint32_t* hist, uint32_t bin, bool
 }
 
 // ---------------------------------------------------------------------------
+// Tile rectangle of a projected Gaussian (src/gsplat_cpu/tile_assign.cpp:60-102):
+// (centre -+ radius) / tile_size as a float division, truncated toward zero,
+// clamped to the tile grid. For a power-of-two tile size the quotient is an
+// exact scaling by 2^-k, which the product with the (exact) reciprocal
+// reproduces bit for bit, denormals included; other sizes divide.
+// ---------------------------------------------------------------------------
+struct TsDiv {
+    float ts, inv;
+    bool pow2;
+};
+__device__ __forceinline__ TsDiv ts_div(int tile_size) {
+    TsDiv d;
+    d.ts = (float)tile_size;
+    d.pow2 = tile_size > 0 && (tile_size & (tile_size - 1)) == 0;
+    d.inv = d.pow2 ? 1.0f / d.ts : 0.0f;
+    return d;
+}
+__device__ __forceinline__ float div_ts(float x, const TsDiv& d) {
+    if (d.pow2) return x * d.inv;
+    return x / d.ts;
+}
+
+struct Rect {
+    int x0, x1, y0, y1;
+};
+// r = (px, py, rx, ry)
+__device__ __forceinline__ Rect tile_rect(float4 r, int tiles_x, int tiles_y, const TsDiv& d) {
+    Rect o;
+    o.x0 = max(0, min((int)div_ts(r.x - r.z, d), tiles_x - 1));
+    o.x1 = max(0, min((int)div_ts(r.x + r.z, d), tiles_x - 1));
+    o.y0 = max(0, min((int)div_ts(r.y - r.w, d), tiles_y - 1));
+    o.y1 = max(0, min((int)div_ts(r.y + r.w, d), tiles_y - 1));
+    return o;
+}
+
+// Depth-sort values of the frame: compact index in the low idx_bits bits, the
+// Gaussian's tile count above them, saturated at the field's largest value
+// (which, like a zero field, means "not held: read the rectangle").
+// idx_bits 0: plain compact indices.
+__device__ __forceinline__ uint32_t dval_index(uint32_t v, int idx_bits) {
+    return idx_bits ? (v & ((1u << idx_bits) - 1u)) : v;
+}
+__device__ __forceinline__ uint32_t dval_count(uint32_t v, int idx_bits) {
+    if (idx_bits == 0) return 0u;
+    const uint32_t c = v >> idx_bits;
+    return c == (0xFFFFFFFFu >> idx_bits) ? 0u : c;
+}
+__device__ __forceinline__ uint32_t dval_pack(uint32_t m, uint32_t count, int idx_bits) {
+    const uint32_t sat = 0xFFFFFFFFu >> idx_bits;
+    return m | ((count < sat ? count : sat) << idx_bits);
+}
+
+// ---------------------------------------------------------------------------
 // Control words of a launch (ctl, may be null): ctl[0] collects error flags
 // (kErrLookback: a bounded look-back wait gave up, so a prefix may be wrong),
 // ctl[1] is the wait's spin limit (0: kLbMaxSpins). The host clears ctl[0]

@@ -52,6 +52,10 @@ struct ProjParams {
     int has_opac;
     int sh_clamp_hi;
     int write_src;             // also write compact->source index
+    // depth-sort values (dval_pack: compact index | tile count << idx_bits) of
+    // the frame's tile grid, written when dvals is set (idx_bits > 0)
+    int tiles_x, tiles_y, tile_size, idx_bits;
+    uint32_t* dvals;
     // per projection partition: nonzero = no Gaussian of it can reach the image
     // (its loads are skipped); nullptr = no partition is skipped
     const uint8_t* skip;
@@ -161,6 +165,9 @@ struct TileParams {
     int tiles_x, tiles_y, tile_size;
     int cull;          // per-pair Mahalanobis cull on
     uint32_t* ctl;     // control words (gs_common.h), may be null
+    // the rank order holds packed depth-sort values (dval_pack) with this many
+    // index bits; 0: plain compact indices
+    int idx_bits;
 };
 // offs: exclusive scan of rectangle areas in `order`; bstart[b]: rank owning
 // candidate b*emit_part (b < bstart_cap).
@@ -180,17 +187,20 @@ inline int sort_digit_width(int bits) {
     const int passes = (bits + 7) / 8;
     return passes > 0 ? (bits + passes - 1) / passes : 8;
 }
-// Tile-id digit histograms that the pair emission produces: two for up to 16
-// tile bits (rows of 512 words), three above (rows of 1024 words, the last 256
-// zero).
-inline int tile_hist_cols(int tile_bits) { return tile_bits > 16 ? 1024 : 512; }
+// Tile-id digit histograms that the pair emission produces, one row per emit
+// partition: two digits for up to 16 tile bits, three above, each of
+// 2^sort_digit_width(tile_bits) words, the row padded with zeros to a power of
+// two (12 tile bits: 2 x 64 = 128 words).
+inline int tile_hist_cols(int tile_bits) {
+    return (tile_bits > 16 ? 4 : 2) << sort_digit_width(tile_bits);
+}
 // Rank r's rectangle and conic are rect / cov[e * stride] with e = order[r]
 // when by_order (records in compact order, as the projection writes them),
 // else e = r (records already in rank order); pair ids are order[r] (r when
 // order is null). part_hist (optional): per-partition digit histograms of the
 // kept pairs' tile ids, one row of tile_hist_cols(tile_bits) words per emit
-// partition: 256 words per digit of sort_digit_width(tile_bits) bits, lowest
-// digit first.
+// partition: 2^w words per digit of w = sort_digit_width(tile_bits) bits, lowest
+// digit first (launch_reduce_rows with dig_w = w spreads them to 256-word rows).
 hipError_t launch_pair_emit(const float4* rect, const float4* cov, int stride, bool by_order,
                             const uint32_t* order, const uint32_t* offs, const uint32_t* bstart, int64_t m,
                             const uint32_t* m_dev, uint32_t p_pre, const uint32_t* p_pre_dev,
@@ -207,10 +217,12 @@ hipError_t launch_tile_bounds(const uint32_t* sorted_tile, uint32_t p_cap, const
 // id >= num_tiles is flagged kErrKeyRange in ctl[0] (its keys get no range).
 hipError_t launch_tile_bounds64(const uint64_t* sorted_keys, uint32_t p, uint32_t* ranges,
                                 int64_t num_tiles, uint32_t* ctl, hipStream_t st);
-// out[c] += sum over rows of part[r][c] (out must be cleared by the caller).
+// out[c] += sum over rows of part[r][c] (out must be cleared by the caller);
+// with dig_w > 0 the columns are digit rows of 2^dig_w words and column c adds
+// into out[(c >> dig_w) * 256 + (c & (2^dig_w - 1))].
 hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,
                               const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
-                              uint32_t* out, hipStream_t st);
+                              int dig_w, uint32_t* out, hipStream_t st);
 constexpr uint32_t kEmitPartition = 2048;   // candidates per emit partition
 constexpr uint32_t kProjPartition = 2048;   // Gaussians per project partition
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t st);

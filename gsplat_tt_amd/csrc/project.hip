@@ -245,6 +245,13 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
         out.rc[2 * m + 0] = make_float4(vmx[it], vmy[it], vrx[it], vry[it]);
         out.rc[2 * m + 1] = make_float4(a, b, c, s.m2thr[i]);
         out.dkey[m] = __float_as_uint(vtz[it]);
+        if (p.dvals != nullptr) {
+            // the tile count that the candidate scan would read the rectangle for
+            const Rect q = tile_rect(make_float4(vmx[it], vmy[it], vrx[it], vry[it]), p.tiles_x,
+                                     p.tiles_y, ts_div(p.tile_size));
+            const uint32_t cnt = (uint32_t)(q.x1 - q.x0 + 1) * (uint32_t)(q.y1 - q.y0 + 1);
+            p.dvals[m] = dval_pack((uint32_t)m, cnt, p.idx_bits);
+        }
         // Microblock cull / blend record (cull_and_blend.cpp:723-777).
         const float det = fmax_std(a * c - b * b, 1e-6f);
         const float ci_a = c / det;

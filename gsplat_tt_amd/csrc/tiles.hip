@@ -36,10 +36,6 @@ static_assert(kEmitPart + 1 <= 65535, "a partition's ranks are held as 16-bit in
 __device__ __forceinline__ float fmin_std(float a, float b) { return (b < a) ? b : a; }
 __device__ __forceinline__ float fmax_std(float a, float b) { return (a < b) ? b : a; }
 
-struct Rect {
-    int x0, x1, y0, y1;
-};
-
 // q = j / w, r = j % w for j < 2^24 and a quotient below 2^16 (a tile row of a
 // Gaussian's rectangle): float reciprocal estimate, then one exact correction.
 __device__ __forceinline__ void divmod_small(uint32_t j, uint32_t w, uint32_t& q, uint32_t& r) {
@@ -48,35 +44,6 @@ __device__ __forceinline__ void divmod_small(uint32_t j, uint32_t w, uint32_t& q
     const int fix = (ri < 0) ? -1 : ((ri >= (int)w) ? 1 : 0);
     q = (uint32_t)(qi + fix);
     r = (uint32_t)(ri - fix * (int)w);
-}
-
-// x / tile_size as the reference computes it (a float division). For a
-// power-of-two tile size the quotient is an exact scaling by 2^-k, which the
-// product with the (exact) reciprocal reproduces bit for bit, denormals
-// included; other sizes divide.
-struct TsDiv {
-    float ts, inv;
-    bool pow2;
-};
-__device__ __forceinline__ TsDiv ts_div(const TileParams& tp) {
-    TsDiv d;
-    d.ts = (float)tp.tile_size;
-    d.pow2 = tp.tile_size > 0 && (tp.tile_size & (tp.tile_size - 1)) == 0;
-    d.inv = d.pow2 ? 1.0f / d.ts : 0.0f;
-    return d;
-}
-__device__ __forceinline__ float div_ts(float x, const TsDiv& d) {
-    if (d.pow2) return x * d.inv;
-    return x / d.ts;
-}
-
-__device__ __forceinline__ Rect tile_rect(float4 r, const TileParams& tp, const TsDiv& d) {
-    Rect o;
-    o.x0 = max(0, min((int)div_ts(r.x - r.z, d), tp.tiles_x - 1));
-    o.x1 = max(0, min((int)div_ts(r.x + r.z, d), tp.tiles_x - 1));
-    o.y0 = max(0, min((int)div_ts(r.y - r.w, d), tp.tiles_y - 1));
-    o.y1 = max(0, min((int)div_ts(r.y + r.w, d), tp.tiles_y - 1));
-    return o;
 }
 
 // tile_assign.cpp:151-290, one (Gaussian, tile) pair. Both edge distances are
@@ -146,10 +113,13 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
     const int64_t base = (int64_t)vid * kCountPart;
     // loads in stages (all ranks' ids, then all rectangles) so that the four
     // gathers of a thread are in flight together
-    const TsDiv tsd = ts_div(tp);
+    const TsDiv tsd = ts_div(tp.tile_size);
     // (indices past m are clamped to m - 1: unconditional loads, no branches
     // whose joins would wait for each load in turn)
-    uint32_t gid[kCountItems];
+    // A packed rank order carries each Gaussian's tile count (the projection
+    // computed it): only ranks whose count field is saturated read their
+    // rectangle, a 16-byte gather in depth order.
+    uint32_t gid[kCountItems], held[kCountItems];
     float4 rr[kCountItems];
 #pragma unroll
     for (int it = 0; it < kCountItems; ++it)
@@ -159,15 +129,25 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
         for (int it = 0; it < kCountItems; ++it) gid[it] = order[gid[it]];
     }
 #pragma unroll
-    for (int it = 0; it < kCountItems; ++it) rr[it] = rect[(int64_t)gid[it] * stride];
+    for (int it = 0; it < kCountItems; ++it) {
+        held[it] = dval_count(gid[it], tp.idx_bits);
+        gid[it] = dval_index(gid[it], tp.idx_bits);
+    }
+#pragma unroll
+    for (int it = 0; it < kCountItems; ++it)
+        if (held[it] == 0u) rr[it] = rect[(int64_t)gid[it] * stride];
     uint32_t incl[kCountItems], cnt[kCountItems];
 #pragma unroll
     for (int it = 0; it < kCountItems; ++it) {
         const int64_t r = base + it * kCountThreads + tid;
         uint32_t c = 0;
         if (r < m) {
-            const Rect q = tile_rect(rr[it], tp, tsd);
-            c = (uint32_t)((q.x1 - q.x0 + 1) * (q.y1 - q.y0 + 1));
+            if (held[it] != 0u) {
+                c = held[it];
+            } else {
+                const Rect q = tile_rect(rr[it], tp.tiles_x, tp.tiles_y, tsd);
+                c = (uint32_t)((q.x1 - q.x0 + 1) * (q.y1 - q.y0 + 1));
+            }
         }
         cnt[it] = c;
         incl[it] = wave_incl_scan(c);
@@ -229,7 +209,6 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     uint32_t* __restrict__ pair_tile, uint32_t* __restrict__ pair_id, uint32_t cap,
     uint64_t* lb_state, uint32_t* ticket, uint32_t* total_out,
     uint32_t* __restrict__ part_hist, int dig_bits) {
-    constexpr int kHistCols = NDIG == 2 ? 512 : 1024;  // tile_hist_cols
     __shared__ uint32_t s_vid;
     __shared__ uint32_t s_off[kEmitPart + 1];
     __shared__ uint32_t s_xy[kEmitPart + 1];
@@ -266,12 +245,12 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     const int64_t rend = (c1 < (uint64_t)p_pre) ? (int64_t)bstart[vid + 1] + 1 : m;
     // every rank owns >= 1 candidate, so nr <= kEmitPart + 1; clamp defensively
     const int64_t nr = min(rend - rlo, (int64_t)kEmitPart + 1);
-    const TsDiv tsd = ts_div(tp);
+    const TsDiv tsd = ts_div(tp.tile_size);
     for (int64_t k = tid; k < nr; k += kEmitThreads) {
         const int64_t r = rlo + k;
-        const int64_t e = by_order ? (int64_t)order[r] : r;  // the rank's record
+        const int64_t e = by_order ? (int64_t)dval_index(order[r], tp.idx_bits) : r;  // its record
         const float4 rr = rect[e * stride];
-        const Rect q = tile_rect(rr, tp, tsd);
+        const Rect q = tile_rect(rr, tp.tiles_x, tp.tiles_y, tsd);
         const uint32_t o = offs[r];
         if (k < kRankCache) {
             s_pc[k] = make_float2(rr.x, rr.y);
@@ -325,7 +304,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
         xy[it] = s_xy[lo[it]];
         // the Gaussian id from the rank order itself (an L2-resident read; a
         // table of it in LDS would cost a quarter of the workgroup's LDS)
-        gid[it] = order ? order[rlo + lo[it]] : (uint32_t)(rlo + lo[it]);
+        gid[it] = order ? dval_index(order[rlo + lo[it]], tp.idx_bits) : (uint32_t)(rlo + lo[it]);
     }
 #pragma unroll
     for (int it = 0; it < kEmitItems; ++it) {
@@ -356,7 +335,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
 #pragma unroll
             for (int it = 0; it < kEmitItems; ++it) {
                 const int64_t r = rlo + lo[it];
-                const int64_t e = by_order ? (int64_t)order[r] : r;
+                const int64_t e = by_order ? (int64_t)dval_index(order[r], tp.idx_bits) : r;
                 rr[it] = rect[e * stride];
                 cv[it] = cov[e * stride];
             }
@@ -381,8 +360,12 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     }
     __syncthreads();
     if (part_hist != nullptr) {
-        for (int i = tid; i < kHistCols; i += kEmitThreads)
-            part_hist[(size_t)vid * kHistCols + i] = i < NDIG * 256 ? (&s_th[0][0])[i] : 0u;
+        // the row holds digit q's 2^dig_bits counts at [q << dig_bits], then zeros
+        // up to tile_hist_cols(tile bits) words
+        const int cols = (NDIG == 2 ? 2 : 4) << dig_bits;
+        const uint32_t dm = (1u << dig_bits) - 1u;
+        for (int i = tid; i < cols; i += kEmitThreads)
+            part_hist[(size_t)vid * cols + i] = (i >> dig_bits) < NDIG ? s_th[i >> dig_bits][i & dm] : 0u;
     }
     if (!COMPACT) {
 #pragma unroll
@@ -504,7 +487,7 @@ constexpr int kRedThreads = 1024;
 constexpr uint32_t kRedBlocks = 96;  // workgroups for the largest row count
 __global__ __launch_bounds__(kRedThreads) void k_reduce_rows(
     const uint32_t* __restrict__ part, int cols, uint32_t rows_cap, uint32_t span,
-    const uint32_t* __restrict__ count_dev, uint32_t count_cap, uint32_t per_row,
+    const uint32_t* __restrict__ count_dev, uint32_t count_cap, uint32_t per_row, int dig_w,
     uint32_t* __restrict__ out) {
     __shared__ uint4 s_acc[kRedThreads];
     uint32_t rows = rows_cap;
@@ -538,11 +521,15 @@ __global__ __launch_bounds__(kRedThreads) void k_reduce_rows(
             acc.z += v.z;
             acc.w += v.w;
         }
-        uint32_t* o = out + q * 4;
-        if (acc.x) atomicAdd(o + 0, acc.x);
-        if (acc.y) atomicAdd(o + 1, acc.y);
-        if (acc.z) atomicAdd(o + 2, acc.z);
-        if (acc.w) atomicAdd(o + 3, acc.w);
+        // column c -> out[c], or with digit rows of 2^dig_w words -> the digit's
+        // row of 256 words
+        const uint32_t a[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t c = (uint32_t)(q * 4 + j);
+            const uint32_t o = dig_w ? ((c >> dig_w) << 8) | (c & ((1u << dig_w) - 1u)) : c;
+            if (a[j]) atomicAdd(out + o, a[j]);
+        }
     }
 }
 
@@ -613,7 +600,7 @@ hipError_t launch_pair_emit(const float4* rect, const float4* cov, int stride, b
     if (tp.tiles_x < 1 || tp.tiles_x > 65535 || tp.tiles_y < 1 || tp.tiles_y > 65535)
         return hipErrorInvalidValue;
     const int dbits = sort_digit_width(tile_bits);
-    const bool three = tile_hist_cols(tile_bits) > 512;
+    const bool three = tile_bits > 16;
 #define GS_EMIT(CP, ND)                                                                    \
     k_pair_emit<CP, ND><<<grid, kEmitThreads, 0, st>>>(                                    \
         rect, cov, stride, by_order, order, offs, bstart, m, m_dev, p_pre, p_pre_dev, tp,    \
@@ -657,13 +644,14 @@ hipError_t launch_tile_bounds64(const uint64_t* sorted_keys, uint32_t p, uint32_
 
 hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,
                               const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
-                              uint32_t* out, hipStream_t st) {
+                              int dig_w, uint32_t* out, hipStream_t st) {
     if (rows_cap == 0) return hipSuccess;
     if (cols <= 0 || cols % 4 != 0 || kRedThreads % (cols / 4) != 0) return hipErrorInvalidValue;
     const uint32_t span = std::max<uint32_t>(32, (rows_cap + kRedBlocks - 1) / kRedBlocks);
     const unsigned grid = (rows_cap + span - 1) / span;
+    if (dig_w < 0 || dig_w > 8) return hipErrorInvalidValue;
     k_reduce_rows<<<grid, kRedThreads, 0, st>>>(part, cols, rows_cap, span, count_dev,
-                                                count_cap, per_row, out);
+                                                count_cap, per_row, dig_w, out);
     return hipGetLastError();
 }
 

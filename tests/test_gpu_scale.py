@@ -54,6 +54,56 @@ def test_c2_1m_1280x720_sh3_frame(gpu_ctx):
     F.check_frame(gpu_ctx, view, ref, img, st, bf16=True, label="C2")
 
 
+def test_frame_tile_counts_past_the_packed_field(gpu_ctx):
+    """The frame's depth-sort values carry each Gaussian's tile count above its
+    compact index; with more than 2^22 Gaussians the index takes 23 bits and the
+    count field saturates at 511 tiles, past which the candidate scan reads the
+    rectangle itself. A view whose few hundred visible Gaussians cover 1 to ~2000
+    tiles each (the rest lie behind the camera) crosses that boundary many times;
+    the frame must still equal the reference id for id."""
+    print("packed tile counts: 4.2M Gaussians, counts around 511", flush=True)
+    rng = np.random.default_rng(21)
+    n = (1 << 22) + 4096
+    nv = 600
+    means = np.empty((n, 3), np.float32)
+    means[:, :2] = rng.uniform(-2, 2, (n, 2))
+    means[:, 2] = rng.uniform(-5, -1, n)          # behind the camera
+    vis = rng.choice(n, nv, replace=False)
+    means[vis, 0] = rng.uniform(-2.5, 2.5, nv)
+    means[vis, 1] = rng.uniform(-1.5, 1.5, nv)
+    means[vis, 2] = rng.uniform(3, 8, nv)
+    scales = np.full((n, 3), 0.01, np.float32)
+    scales[vis] = np.exp(rng.uniform(np.log(0.002), np.log(0.6), (nv, 1))) * \
+        rng.uniform(0.6, 1.0, (nv, 3))
+    quats = np.zeros((n, 4), np.float32)
+    quats[:, 0] = 1.0
+    quats[vis] = scenes._unit_quats(rng, nv)
+    opac = scenes._sigmoid(rng.normal(0, 1.5, n)).astype(np.float32)
+    rgb = rng.uniform(0, 1, (n, 3)).astype(np.float32)
+    cov = O.cov3d(scales.astype(np.float32), quats)
+    H, W = 720, 1280
+    cam = scenes.Camera(np.eye(4, dtype=np.float32), scenes.intrinsics(1000, 1000, W / 2, H / 2),
+                        H, W)
+    ref = F.frame(means, cov, opac, rgb, cam, 16)
+    pr = ref["project"]
+    m2, rad = pr["means2d"], pr["radii"]
+    tx, ty = W // 16, (H + 15) // 16
+    x0 = np.clip(((m2[:, 0] - rad[:, 0]) / 16).astype(np.int64), 0, tx - 1)
+    x1 = np.clip(((m2[:, 0] + rad[:, 0]) / 16).astype(np.int64), 0, tx - 1)
+    y0 = np.clip(((m2[:, 1] - rad[:, 1]) / 16).astype(np.int64), 0, ty - 1)
+    y1 = np.clip(((m2[:, 1] + rad[:, 1]) / 16).astype(np.int64), 0, ty - 1)
+    counts = (x1 - x0 + 1) * (y1 - y0 + 1)
+    sat = int((counts >= 511).sum())
+    print(f"M={ref['M']} counts {counts.min()}..{counts.max()}, {sat} at or past 511",
+          flush=True)
+    assert int(counts.sum()) == ref["pairs_pre"]
+    assert 20 <= sat <= ref["M"] - 20
+    gpu_ctx.set_scene(means, cov, opac, rgb)
+    view = L.make_view(cam.w2c, cam.K, H, W, tile_size=16, output="f32")
+    img, st = gpu_ctx.render(view)
+    F.check_frame(gpu_ctx, view, ref, img, st, bf16=False, label="packed counts")
+
+
 @pytest.fixture(scope="module")
 def c3_scene():
     scene, cams = scenes.config3()
