@@ -208,7 +208,6 @@ struct gs_ctx {
     // next call that reuses them.
     bool rb_valid = false, rb_empty = false;
     uint32_t* rb_ids = nullptr;
-    uint32_t* rb_tiles = nullptr;
     int64_t rb_T = 0, rb_M = 0, rb_ppre = 0, rb_P = 0;
 
     ~gs_ctx() {
@@ -250,6 +249,12 @@ struct gs_ctx {
         drain_spec();  // an announced frame reads the buffers about to change
         const int64_t n = s->n;
         sync();
+        if (n != sd.n) {
+            // the frame's launch grids follow the pair capacity: a scene of another
+            // size starts again from its own default (buffers keep their memory)
+            pair_cap = 0;
+            for (gs_ctx* p : peers) p->pair_cap = 0;
+        }
         const int K = s->sh_degree < 0 ? 1 : (s->sh_degree + 1) * (s->sh_degree + 1);
         const int col_planes = 3 * K;
         b_mean.ensure(std::max<int64_t>(n, 1) * 3 * 4);
@@ -832,6 +837,7 @@ struct gs_ctx {
         uint32_t* fr;
         uint32_t* cnt;
         uint64_t *lb_proj, *lb_rect, *lb_emit;
+        uint32_t* tcnt;  // pairs per tile (the tile sort's last pass counts them)
         size_t fwords, pparts, rparts, eparts;
         uint32_t pcap;
     };
@@ -853,7 +859,8 @@ struct gs_ctx {
         b_ranges.ensure((size_t)T * 8);
         b_phist_proj.ensure(L.pparts * 1024 * 4);
         b_phist_emit.ensure(L.eparts * gs::tile_hist_cols(tile_bits(T)) * 4);
-        L.fwords = kFrLb + 2 * (L.pparts + L.rparts + L.eparts);
+        const size_t lb_words = 2 * (L.pparts + L.rparts + L.eparts);
+        L.fwords = kFrLb + lb_words + (size_t)T;
         b_frame.ensure(L.fwords * 4);
         ensure_sort(std::max<int64_t>(N, L.pcap), 4);
         if (timing) b_evals.ensure(64 * 8 * 8);
@@ -861,6 +868,7 @@ struct gs_ctx {
         L.lb_proj = reinterpret_cast<uint64_t*>(L.fr + kFrLb);
         L.lb_rect = L.lb_proj + L.pparts;
         L.lb_emit = L.lb_rect + L.rparts;
+        L.tcnt = L.fr + kFrLb + lb_words;
         L.cnt = L.fr + kFrCnt;
         return L;
     }
@@ -871,6 +879,10 @@ struct gs_ctx {
     // tile bounds. Returns the sorted compact ids.
     uint32_t* frame_tiles(const FrameLayout& L, int64_t N, int64_t T, const gs::TileParams& tp,
                           uint32_t** tiles_out) {
+        // without a caller for the tile-sorted keys, the tile sort's last pass
+        // counts the pairs per tile instead of writing them, and the ranges come
+        // from the counts
+        const bool want_keys = tiles_out != nullptr;
         uint32_t* fr = L.fr;
         uint32_t* cnt = L.cnt;
         sort.ctl = cnt + C_CTL;
@@ -906,10 +918,14 @@ struct gs_ctx {
         HIPCHK(gs::radix_sort_pairs_dev(b_pair_tile.p, b_pair_id.as<uint32_t>(), L.pcap,
                                         cnt + C_PPRE, 4, 0, tile_bits(T), fr + kFrTileHist,
                                         cnt + C_TSORT_TICKETS, sort, st, false, &tiles_sorted,
-                                        &ids_sorted, cnt + C_P));
-        HIPCHK(gs::launch_tile_bounds(static_cast<uint32_t*>(tiles_sorted), L.pcap, cnt + C_P,
-                                      b_ranges.as<uint32_t>(), T, st));
-        if (tiles_out) *tiles_out = static_cast<uint32_t*>(tiles_sorted);
+                                        &ids_sorted, cnt + C_P, want_keys ? nullptr : L.tcnt));
+        if (want_keys) {
+            HIPCHK(gs::launch_tile_bounds(static_cast<uint32_t*>(tiles_sorted), L.pcap, cnt + C_P,
+                                          b_ranges.as<uint32_t>(), T, st));
+            *tiles_out = static_cast<uint32_t*>(tiles_sorted);
+        } else {
+            HIPCHK(gs::launch_ranges_from_counts(L.tcnt, T, b_ranges.as<uint32_t>(), st));
+        }
         return ids_sorted;
     }
 
@@ -947,7 +963,7 @@ struct gs_ctx {
         gs::TileParams tp{tiles_x, tiles_y, v->tile_size, v->cull_disabled ? 0 : 1,
                           L.cnt + C_CTL, p.idx_bits};
         uint32_t* tiles_sorted = nullptr;
-        uint32_t* ids_sorted = frame_tiles(L, N, T, tp, &tiles_sorted);
+        uint32_t* ids_sorted = frame_tiles(L, N, T, tp, cull_stats ? &tiles_sorted : nullptr);
         record(4);
         gs::BlendParams bp{tiles_x, tiles_y, v->tile_size, v->image_height, v->image_width,
                            v->cull_disabled ? 1 : 0, v->transmittance_threshold, v->out_format,
@@ -961,7 +977,6 @@ struct gs_ctx {
                                        reinterpret_cast<unsigned long long*>(L.cnt + C_MBSTAT),
                                        L.cnt + C_CTL, st));
         rb_ids = ids_sorted;
-        rb_tiles = tiles_sorted;
     }
 
     // ------------------------------------------------------------ training

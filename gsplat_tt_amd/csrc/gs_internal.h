@@ -135,12 +135,15 @@ hipError_t radix_sort_pairs(void* keys, uint32_t* vals, int64_t n, int key_bytes
 // n_kept_dev (u32 keys only, optional): the first pass drops every key equal
 // to kPairDrop (its value is not read) and stably compacts the rest; later
 // passes sort min(n_cap, *n_kept_dev) keys, and `hist` counts kept keys only.
+// run_cnt (u32 keys only, optional): the sorted keys are not written (*keys_final = nullptr); run_cnt[k] (cleared by the caller) gains
+// the number of keys equal to k, for launch_ranges_from_counts.
 constexpr uint32_t kPairDrop = 0xFFFFFFFFu;
 hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const uint32_t* n_dev,
                                 int key_bytes, int begin_bit, int end_bit, const uint32_t* hist,
                                 uint32_t* tickets, SortTemp& tmp, hipStream_t st, bool vals_iota,
                                 void** keys_final, uint32_t** vals_final,
-                                const uint32_t* n_kept_dev = nullptr);
+                                const uint32_t* n_kept_dev = nullptr,
+                                uint32_t* run_cnt = nullptr);
 
 // The 64-bit-key sort of radix_sort_pairs_dev over exactly n keys, with no
 // producer histogram: a histogram kernel counts the first pass's digits and
@@ -209,6 +212,10 @@ hipError_t launch_pair_emit(const float4* rect, const float4* cov, int stride, b
                             uint32_t* part_hist, int tile_bits, bool compact, hipStream_t st);
 hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, const uint32_t* p_dev,
                               uint32_t* ranges, int64_t num_tiles, hipStream_t st);
+// ranges[t] = [start, end) from per-tile pair counts (an exclusive scan in tile
+// order; (0, 0) for an empty tile), one workgroup.
+hipError_t launch_ranges_from_counts(const uint32_t* counts, int64_t num_tiles, uint32_t* ranges,
+                                     hipStream_t st);
 // Same ranges by per-tile binary search over the sorted tile keys (reads
 // O(tiles * log p) keys instead of all p; no clearing pass).
 hipError_t launch_tile_bounds(const uint32_t* sorted_tile, uint32_t p_cap, const uint32_t* p_dev,

@@ -196,13 +196,19 @@ __device__ __forceinline__ uint32_t digit_walk(DT* state, uint32_t vid, int digi
 // SPLIT: the keys are re-ordered in LDS and written out first, then the values
 // in the same LDS space, so a partition holds only its keys in LDS (larger
 // partitions, fewer look-back links).
-template <typename K, bool IOTA, int THREADS, int ITEMS, bool D32, bool DROP, bool SPLIT>
+// RUNS (the last pass of a sort of 32-bit keys that index run_cnt): the sorted
+// keys are not written; instead every run of equal keys in the partition (the
+// last pass leaves a partition sorted by all the key bits in LDS) adds its
+// length to run_cnt[key], with at most two atomics per run.
+template <typename K, bool IOTA, int THREADS, int ITEMS, bool D32, bool DROP, bool SPLIT,
+          bool RUNS>
 __global__ __launch_bounds__(THREADS) void k_onesweep(
     const K* __restrict__ kin, const uint32_t* __restrict__ vin, K* __restrict__ kout,
     uint32_t* __restrict__ vout, int64_t n_cap, const uint32_t* __restrict__ n_dev, int shift,
     int bits, const uint32_t* __restrict__ g_hist_pass, void* __restrict__ state_raw,
     uint32_t* __restrict__ ticket, uint32_t epoch, uint32_t* __restrict__ clear_next,
-    uint32_t* ctl, uint32_t* __restrict__ next_hist, int next_shift, int next_bits) {
+    uint32_t* ctl, uint32_t* __restrict__ next_hist, int next_shift, int next_bits,
+    uint32_t* __restrict__ run_cnt) {
     using D = Desc<D32>;
     using DT = typename D::T;
     DT* state = static_cast<DT*>(state_raw);
@@ -368,8 +374,16 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
             const uint32_t d = digit_of(k, shift, mask);
             const uint32_t g = s_gpos[d] + (uint32_t)j;
             if ((int64_t)g < n) {
-                kout[g] = k;
+                if (!RUNS) kout[g] = k;
                 vout[g] = s_vals[j];
+            }
+            if (RUNS) {
+                // run [a, b) of key k: + b at its last key, - a at its first
+                // (modulo 2^32; a run of one adds 1)
+                const bool first = j == 0 || s_keys[j - 1] != k;
+                const bool last = j == count - 1 || s_keys[j + 1] != k;
+                const uint32_t delta = (last ? (uint32_t)j + 1u : 0u) - (first ? (uint32_t)j : 0u);
+                if (first || last) atomicAdd(&run_cnt[(uint32_t)k], delta);
             }
         }
     } else {
@@ -431,7 +445,8 @@ template <typename K, typename CFG>
 hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uint32_t* vout,
                       int64_t n_cap, const uint32_t* n_dev, int shift, int bits,
                       const uint32_t* hist_pass, SortTemp& tmp, uint32_t* ticket, hipStream_t st,
-                      bool drop, uint32_t* next_hist, int next_shift, int next_bits) {
+                      bool drop, uint32_t* next_hist, int next_shift, int next_bits,
+                      uint32_t* run_cnt) {
     constexpr int T = CFG::T, I = CFG::I;
     constexpr bool SP = CFG::SPLIT;
     const unsigned grid = (unsigned)((n_cap + T * I - 1) / (T * I));
@@ -457,18 +472,26 @@ hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uin
         tmp.dirty[0] = tmp.dirty[1] = (uint32_t)std::min<size_t>(tmp.state_parts, 0xFFFFFFFFu);
     }
     const uint32_t epoch = ++tmp.epoch;
-#define GS_OS(IO, DD, DR)                                                                         \
-    k_onesweep<K, IO, T, I, DD, DR, SP><<<grid, T, 0, st>>>(kin, vin, kout, vout, n_cap, n_dev,  \
-                                                            shift, bits, hist_pass, state,       \
-                                                            ticket, epoch, clear_next, tmp.ctl,  \
-                                                            next_hist, next_shift, next_bits)
-    if (drop) {
+#define GS_OS(IO, DD, DR, RU)                                                                    \
+    k_onesweep<K, IO, T, I, DD, DR, SP, RU><<<grid, T, 0, st>>>(kin, vin, kout, vout, n_cap,     \
+                                                                n_dev, shift, bits, hist_pass,   \
+                                                                state, ticket, epoch, clear_next,\
+                                                                tmp.ctl, next_hist, next_shift,  \
+                                                                next_bits, run_cnt)
+    if (run_cnt != nullptr) {
+        if (iota || sizeof(K) != 4 || SP) return hipErrorInvalidValue;
+        if (drop) {  // a one-pass sort: it drops and counts
+            if (d32) GS_OS(false, true, true, true); else GS_OS(false, false, true, true);
+        } else {
+            if (d32) GS_OS(false, true, false, true); else GS_OS(false, false, false, true);
+        }
+    } else if (drop) {
         if (iota || sizeof(K) != 4) return hipErrorInvalidValue;
-        if (d32) GS_OS(false, true, true); else GS_OS(false, false, true);
+        if (d32) GS_OS(false, true, true, false); else GS_OS(false, false, true, false);
     } else if (iota) {
-        if (d32) GS_OS(true, true, false); else GS_OS(true, false, false);
+        if (d32) GS_OS(true, true, false, false); else GS_OS(true, false, false, false);
     } else {
-        if (d32) GS_OS(false, true, false); else GS_OS(false, false, false);
+        if (d32) GS_OS(false, true, false, false); else GS_OS(false, false, false, false);
     }
 #undef GS_OS
     return hipGetLastError();
@@ -483,14 +506,14 @@ hipError_t launch_pass(bool iota, const K* kin, const uint32_t* vin, K* kout, ui
                        int64_t n_cap, const uint32_t* n_dev, int shift, int bits,
                        const uint32_t* hist_pass, SortTemp& tmp, uint32_t* ticket,
                        hipStream_t st, bool drop = false, uint32_t* next_hist = nullptr,
-                       int next_shift = 0, int next_bits = 0) {
+                       int next_shift = 0, int next_bits = 0, uint32_t* run_cnt = nullptr) {
     if constexpr (sizeof(K) == 8)
         return launch_cfg<K, Sweep64>(iota, kin, vin, kout, vout, n_cap, n_dev, shift, bits,
                                       hist_pass, tmp, ticket, st, drop, next_hist, next_shift,
-                                      next_bits);
+                                      next_bits, run_cnt);
     return launch_cfg<K, Sweep32>(iota, kin, vin, kout, vout, n_cap, n_dev, shift, bits,
                                   hist_pass, tmp, ticket, st, drop, next_hist, next_shift,
-                                  next_bits);
+                                  next_bits, run_cnt);
 }
 
 template <typename K>
@@ -564,7 +587,8 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
                          int begin_bit, int end_bit, const uint32_t* hist, uint32_t* tickets,
                          SortTemp& tmp, hipStream_t st, bool vals_iota, K** keys_final,
                          uint32_t** vals_final, const uint32_t* n_kept_dev,
-                         uint32_t* chain_hist = nullptr, bool pass_events = false) {
+                         uint32_t* chain_hist = nullptr, bool pass_events = false,
+                         uint32_t* run_cnt = nullptr) {
     *keys_final = keys;
     *vals_final = vals;
     if (n_cap <= 0) return hipSuccess;
@@ -588,7 +612,8 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
         hipError_t e = launch_pass<K>(p == 0 && vals_iota, kin, vin, kalt, valt, n_cap, cnt,
                                       shift, bits, hist + p * 256, tmp, tickets + p, st, drop,
                                       chain ? chain_hist + (p + 1) * 256 : nullptr, nshift,
-                                      chain ? std::min(dw, end_bit - nshift) : 0);
+                                      chain ? std::min(dw, end_bit - nshift) : 0,
+                                      p + 1 == npass ? run_cnt : nullptr);
         if (timed) (void)hipEventRecord(tmp.pass_events[2 * p + 1], st);
         if (e != hipSuccess) return e;
         std::swap(kin, kalt);
@@ -605,17 +630,18 @@ hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const
                                 int key_bytes, int begin_bit, int end_bit, const uint32_t* hist,
                                 uint32_t* tickets, SortTemp& tmp, hipStream_t st, bool vals_iota,
                                 void** keys_final, uint32_t** vals_final,
-                                const uint32_t* n_kept_dev) {
+                                const uint32_t* n_kept_dev, uint32_t* run_cnt) {
     if (key_bytes == 4) {
         uint32_t* kf = nullptr;
         hipError_t e = sort_dev_impl<uint32_t>(static_cast<uint32_t*>(keys), vals, n_cap, n_dev,
                                                begin_bit, end_bit, hist, tickets, tmp, st,
-                                               vals_iota, &kf, vals_final, n_kept_dev);
-        *keys_final = kf;
+                                               vals_iota, &kf, vals_final, n_kept_dev, nullptr,
+                                               false, run_cnt);
+        *keys_final = run_cnt != nullptr ? nullptr : kf;
         return e;
     }
     if (key_bytes == 8) {
-        if (n_kept_dev != nullptr) return hipErrorInvalidValue;
+        if (n_kept_dev != nullptr || run_cnt != nullptr) return hipErrorInvalidValue;
         uint64_t* kf = nullptr;
         hipError_t e = sort_dev_impl<uint64_t>(static_cast<uint64_t*>(keys), vals, n_cap, n_dev,
                                                begin_bit, end_bit, hist, tickets, tmp, st,

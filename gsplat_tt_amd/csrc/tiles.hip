@@ -297,14 +297,19 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     int tx[kEmitItems], ty[kEmitItems];
 #pragma unroll
     for (int it = 0; it < kEmitItems; ++it) lo[it] = s_own[it * kEmitThreads + tid];
+    // The Gaussian id from the rank order itself (an L2-resident read; a table
+    // of it in LDS would cost a quarter of the workgroup's LDS). The raw words
+    // are loaded here and decoded only where the pairs are written, so the four
+    // loads stay in flight through the evaluation.
+    if (order != nullptr) {
+#pragma unroll
+        for (int it = 0; it < kEmitItems; ++it) gid[it] = order[rlo + lo[it]];
+    }
 #pragma unroll
     for (int it = 0; it < kEmitItems; ++it) {
         off[it] = s_off[lo[it]];
         wdt[it] = s_w[lo[it]];
         xy[it] = s_xy[lo[it]];
-        // the Gaussian id from the rank order itself (an L2-resident read; a
-        // table of it in LDS would cost a quarter of the workgroup's LDS)
-        gid[it] = order ? dval_index(order[rlo + lo[it]], tp.idx_bits) : (uint32_t)(rlo + lo[it]);
     }
 #pragma unroll
     for (int it = 0; it < kEmitItems; ++it) {
@@ -331,11 +336,12 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
             for (int it = 0; it < kEmitItems; ++it)
                 keep[it] = keep[it] & pair_keep(pc[it].x, pc[it].y, cv[it], tx[it], ty[it], tp);
         } else {
+            // records through the order words already loaded
             float4 rr[kEmitItems], cv[kEmitItems];
 #pragma unroll
             for (int it = 0; it < kEmitItems; ++it) {
-                const int64_t r = rlo + lo[it];
-                const int64_t e = by_order ? (int64_t)dval_index(order[r], tp.idx_bits) : r;
+                const int64_t e = by_order ? (int64_t)dval_index(gid[it], tp.idx_bits)
+                                           : rlo + lo[it];
                 rr[it] = rect[e * stride];
                 cv[it] = cov[e * stride];
             }
@@ -350,14 +356,18 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     for (int it = 0; it < kEmitItems; ++it) {
         bal[it] = __ballot(keep[it]);
         if (lane == 0) s_cnt[it][w] = (uint32_t)__popcll(bal[it]);
-        if (part_hist != nullptr) {
-            // digit histograms of the tile keys, for the tile sort's passes
+        if (part_hist != nullptr && keep[it]) {
+            // digit histograms of the tile keys, for the tile sort's passes: a
+            // partition's kept tiles spread over the digits, so one LDS atomic
+            // per lane (no aggregation of equal digits)
             const uint32_t dm = (1u << dig_bits) - 1u;
 #pragma unroll
-            for (int q = 0; q < NDIG; ++q)
-                hist_add_wave(s_th[q], (tile[it] >> (q * dig_bits)) & dm, keep[it]);
+            for (int q = 0; q < NDIG; ++q) atomicAdd(&s_th[q][(tile[it] >> (q * dig_bits)) & dm], 1u);
         }
     }
+#pragma unroll
+    for (int it = 0; it < kEmitItems; ++it)
+        gid[it] = order != nullptr ? dval_index(gid[it], tp.idx_bits) : (uint32_t)(rlo + lo[it]);
     __syncthreads();
     if (part_hist != nullptr) {
         // the row holds digit q's 2^dig_bits counts at [q << dig_bits], then zeros
@@ -533,6 +543,32 @@ __global__ __launch_bounds__(kRedThreads) void k_reduce_rows(
     }
 }
 
+// Tile ranges from per-tile pair counts in one workgroup: each thread sums a
+// block of consecutive tiles, the block sums are scanned, and each thread
+// writes its tiles' [start, end) (sort.cpp:146-165: (0, 0) for an empty tile).
+constexpr int kRangeThreads = 1024;
+__global__ __launch_bounds__(kRangeThreads) void k_ranges_from_counts(
+    const uint32_t* __restrict__ counts, uint32_t ntiles, uint32_t* __restrict__ ranges) {
+    __shared__ uint32_t s_w[kRangeThreads / GS_WAVE];
+    const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
+    const uint32_t per = (ntiles + kRangeThreads - 1) / kRangeThreads;
+    const uint32_t t0 = min(ntiles, (uint32_t)tid * per), t1 = min(ntiles, t0 + per);
+    uint32_t sum = 0;
+    for (uint32_t t = t0; t < t1; ++t) sum += counts[t];
+    const uint32_t inc = wave_incl_scan(sum);
+    if (lane == GS_WAVE - 1) s_w[w] = inc;
+    __syncthreads();
+    uint32_t pre = 0;
+    for (int i = 0; i < w; ++i) pre += s_w[i];
+    uint32_t start = pre + inc - sum;
+    for (uint32_t t = t0; t < t1; ++t) {
+        const uint32_t c = counts[t];
+        ranges[2 * (size_t)t] = c ? start : 0u;
+        ranges[2 * (size_t)t + 1] = c ? start + c : 0u;
+        start += c;
+    }
+}
+
 // key = (tile << 32) | fp32 depth bits of the pair's Gaussian (sort.cpp:180-205).
 __global__ void k_make_keys64(const uint32_t* __restrict__ gid, const uint32_t* __restrict__ tid,
                               const float* __restrict__ depths, uint32_t p,
@@ -621,6 +657,14 @@ hipError_t launch_tile_ranges(const uint32_t* sorted_tile, uint32_t p, const uin
     if (e != hipSuccess || p == 0) return e;
     const unsigned grid = std::min<unsigned>((p + 255) / 256, 4096u);
     k_tile_ranges<<<grid, 256, 0, st>>>(sorted_tile, p, p_dev, ranges);
+    return hipGetLastError();
+}
+
+hipError_t launch_ranges_from_counts(const uint32_t* counts, int64_t num_tiles, uint32_t* ranges,
+                                     hipStream_t st) {
+    if (num_tiles <= 0) return hipSuccess;
+    if (num_tiles > ((int64_t)1 << 24)) return hipErrorInvalidValue;
+    k_ranges_from_counts<<<1, kRangeThreads, 0, st>>>(counts, (uint32_t)num_tiles, ranges);
     return hipGetLastError();
 }
 
