@@ -16,6 +16,9 @@ namespace gs {
 // raised flag into an error status.
 constexpr uint32_t kErrLookback = 1u;  // a look-back wait gave up: a prefix may be wrong
 constexpr uint32_t kErrKeyRange = 2u;  // a sorted key's tile id is past the tile count
+// the frame's candidate pairs exceed its pair capacity: the later kernels skip
+// their work and the host runs the frame again with a larger capacity
+constexpr uint32_t kErrCapacity = 4u;
 
 // Scene resident in HBM, structure-of-arrays (one coalesced dword stream per
 // attribute). `sh` holds (d+1)^2*3 planes of n floats, plane index k*3+c.
@@ -179,10 +182,12 @@ struct TileParams {
 // capacity) and partitions beyond it exit at once.
 // Rank r's rectangle is rect[order[r] * stride] (order null: rect[r * stride]);
 // stride is in float4 (2 for the interleaved rectangle + conic records).
+// cap (0: none): a total above it raises kErrCapacity in tp.ctl.
 hipError_t launch_rect_count_scan(const float4* rect, int stride, const uint32_t* order,
                                   int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
                                   uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
-                                  uint32_t* ticket, uint32_t* total_out, hipStream_t st);
+                                  uint32_t* ticket, uint32_t* total_out, uint32_t cap,
+                                  hipStream_t st);
 // Digit width of a device sort over `bits` key bits: the fewest 8-bit-or-less
 // passes, with the bits spread evenly over them (12 tile bits: two passes of 6,
 // whose 64 digits give longer runs per digit than 256 would).

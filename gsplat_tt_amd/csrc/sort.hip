@@ -242,6 +242,10 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     if (next_hist != nullptr && tid < 256) s_nh[tid] = 0u;
     __syncthreads();
     const uint32_t vid = s_vid;
+    // after an earlier give-up or a capacity overflow the keys may be partial:
+    // sort nothing (this workgroup's row of the next pass's descriptors is
+    // cleared above all the same)
+    if (__builtin_amdgcn_readfirstlane(upstream_failed(ctl) ? 1 : 0)) return;
     const int64_t part_base = (int64_t)vid * PART;
     // grid sized for a capacity; the key count may be known only on the device
     const int64_t n = n_dev ? min(n_cap, (int64_t)*n_dev) : n_cap;

@@ -97,7 +97,8 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
                                                               uint32_t bstart_cap,
                                                               uint64_t* lb_state,
                                                               uint32_t* ticket,
-                                                              uint32_t* total_out) {
+                                                              uint32_t* total_out,
+                                                              uint32_t cap) {
     __shared__ uint32_t s_vid;
     __shared__ uint32_t s_wsum[kCountItems][kCountWaves];
     __shared__ uint64_t s_excl;
@@ -170,6 +171,9 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
             if (vid == nparts - 1) {
                 const uint64_t t = ex + total;
                 *total_out = t > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)t;
+                // the frame is run again with room for them: the kernels after
+                // this one skip their work
+                if (cap != 0u && t > cap) report_error(tp.ctl, kErrCapacity);
             }
         }
     }
@@ -610,13 +614,14 @@ size_t emit_partitions(uint64_t p_pre) { return (size_t)((p_pre + kEmitPart - 1)
 hipError_t launch_rect_count_scan(const float4* rect, int stride, const uint32_t* order,
                                   int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
                                   uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
-                                  uint32_t* ticket, uint32_t* total_out, hipStream_t st) {
+                                  uint32_t* ticket, uint32_t* total_out, uint32_t cap,
+                                  hipStream_t st) {
     if (m <= 0) return hipSuccess;
     if (stride < 1) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)rect_scan_partitions(m);
     k_rect_count_scan<<<grid, kCountThreads, 0, st>>>(rect, stride, order, m, m_dev, tp, offs,
                                                       bstart, bstart_cap, lb_state, ticket,
-                                                      total_out);
+                                                      total_out, cap);
     return hipGetLastError();
 }
 
