@@ -136,6 +136,13 @@ int tile_bits(int64_t num_tiles) {
     return std::max(b, 1);
 }
 
+// Candidate-pair capacity a scene of n Gaussians starts with: 8 per Gaussian
+// (scene-scale views reach 6-7: 35-40M at 6M Gaussians), so a camera path does
+// not stall mid-way to grow its buffers and re-run a frame; at most 2^29.
+uint64_t default_pair_cap(int64_t n) {
+    return std::min<uint64_t>((uint64_t)1 << 29, std::max<uint64_t>(1u << 20, (uint64_t)n * 8));
+}
+
 // Index bits of the frame's packed depth-sort values over n Gaussians (the
 // tile count takes the rest of the word), 0 when too few bits would be left.
 int dval_idx_bits(int64_t n) {
@@ -613,7 +620,7 @@ struct gs_ctx {
             if (!out_dev) HIPCHK(hipMemcpyAsync(out, pend.dout, pend.bytes, hipMemcpyDeviceToHost, st));
             return;
         }
-        if (pair_cap == 0) pair_cap = std::max<uint64_t>(1u << 20, (uint64_t)sd.n * 4);
+        if (pair_cap == 0) pair_cap = default_pair_cap(sd.n);
         enqueue_attempt();
     }
 
@@ -1220,7 +1227,7 @@ struct gs_ctx {
         tr.fwd_valid = false;
         tr.grads_valid = false;
         rb_valid = false;
-        if (pair_cap == 0) pair_cap = std::max<uint64_t>(1u << 20, (uint64_t)tr.n * 4);
+        if (pair_cap == 0) pair_cap = default_pair_cap(tr.n);
         for (int attempt = 0;; ++attempt) {
             train_forward_enqueue(v, c, tgt, dbg);
             HIPCHK(hipMemcpyAsync(h_pin, b_frame.p, 64 * 4, hipMemcpyDeviceToHost, st));

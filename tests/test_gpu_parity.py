@@ -156,7 +156,7 @@ def test_render_frame_three_tile_digits(gpu_ctx):
 
 
 def test_render_pair_capacity_retry():
-    """A fresh context starts with room for max(2^20, 4N) candidate pairs; 4200
+    """A fresh context starts with room for max(2^20, 8N) candidate pairs; 4200
     large Gaussians make 1.3M pairs, so the first frame overflows, is detected
     after the fact and re-run with a larger capacity. Both that frame and the
     next (no overflow) must equal the oracle's."""
