@@ -124,7 +124,12 @@ __device__ __forceinline__ uint32_t dval_pack(uint32_t m, uint32_t count, int id
 // ctl[1] is the wait's spin limit (0: kLbMaxSpins). The host clears ctl[0]
 // before the launches and turns a nonzero value into an error status.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kLbMaxSpins = 1u << 24;
+constexpr uint32_t kLbMaxSpins = 1u << 20;  // about 0.45 s of polls (kLbSleep below)
+// Back-off between polls of an unpublished predecessor (s_sleep units of 64
+// clocks). With frames in flight the waiting waves share their SIMDs with
+// other frames' kernels; polling every ~0.4 us instead of every ~27 ns gives
+// those kernels the issue slots (orbit 997 -> 1007 frames/s; 4: 1006, 64: 993).
+constexpr int kLbSleep = 16;
 
 // Read only when a wait happens, with a plain load (the host wrote it before
 // the launch): an atomic load of one address by every wave would serialise.
@@ -194,7 +199,7 @@ __device__ __forceinline__ uint64_t lookback_exclusive(uint64_t* state, uint32_t
             // a broken chain or a host-set tiny limit: report, never hang
             if (limit == 0) limit = spin_limit(ctl);
             if (++spins < limit) {
-                __builtin_amdgcn_s_sleep(1);
+                __builtin_amdgcn_s_sleep(kLbSleep);
                 continue;
             }
             gave_up = true;

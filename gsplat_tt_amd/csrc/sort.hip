@@ -180,7 +180,7 @@ __device__ __forceinline__ uint32_t digit_walk(DT* state, uint32_t vid, int digi
             // give-up is reported to the host through ctl
             if (limit == 0) limit = spin_limit(ctl);
             if (++spins < limit) {
-                __builtin_amdgcn_s_sleep(1);
+                __builtin_amdgcn_s_sleep(kLbSleep);
             } else {
                 report_error(ctl, kErrLookback);
                 done = true;

@@ -139,7 +139,7 @@ int gs_frame_readback(gs_ctx* ctx, int64_t* counts, int64_t* sorted_ids, int64_t
  * frame's pairs after the blend, off by default. */
 int gs_set_cull_stats(gs_ctx* ctx, int on);
 /* Spin limit of every bounded look-back wait of this context's kernels (0: the
- * default, 2^24 rounds). A wait that reaches it goes on without the missing
+ * default, 2^20 polls, about 0.45 s). A wait that reaches it goes on without the missing
  * prefix and the call returns GS_E_DEVICE ("look-back wait gave up") instead of
  * results; every kernel still exits normally. A tiny limit is for tests of that
  * error path only. */
