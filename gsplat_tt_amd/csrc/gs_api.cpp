@@ -499,7 +499,7 @@ struct gs_ctx {
                                               b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(),
                                               (uint32_t)(b_bstart.cap / 4), b_lb.as<uint64_t>(),
                                               b_cnt.as<uint32_t>() + 8, b_cnt.as<uint32_t>() + 9,
-                                              0u, st));
+                                              0u, false, st));
             HIPCHK(hipMemcpyAsync(h_pin, b_cnt.p, 64 * 4, hipMemcpyDeviceToHost, st));
             sync();
             ctl_check(h_pin[C_CTL], "tile_assign");
@@ -907,7 +907,7 @@ struct gs_ctx {
         HIPCHK(gs::launch_rect_count_scan(b_rc.as<float4>(), 2, order, N, cnt + C_M, tp,
                                           b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(),
                                           (uint32_t)(L.eparts + 1), L.lb_rect,
-                                          cnt + C_RECT_TICKET, cnt + C_PPRE, L.pcap, st));
+                                          cnt + C_RECT_TICKET, cnt + C_PPRE, L.pcap, true, st));
         HIPCHK(gs::launch_pair_emit(b_rc.as<float4>(), b_rc.as<float4>() + 1, 2, true, order,
                                     b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(), N, cnt + C_M,
                                     L.pcap, cnt + C_PPRE, tp, b_pair_tile.as<uint32_t>(),

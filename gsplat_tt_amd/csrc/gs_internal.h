@@ -183,11 +183,14 @@ struct TileParams {
 // Rank r's rectangle is rect[order[r] * stride] (order null: rect[r * stride]);
 // stride is in float4 (2 for the interleaved rectangle + conic records).
 // cap (0: none): a total above it raises kErrCapacity in tp.ctl.
+// reduce_scan: three kernels that never wait on each other's partitions
+// (lb_state then holds rect_scan_partitions(m) partition sums) instead of one
+// kernel chained by a look-back (lb_state: its cleared descriptors, ticket).
 hipError_t launch_rect_count_scan(const float4* rect, int stride, const uint32_t* order,
                                   int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
                                   uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
                                   uint32_t* ticket, uint32_t* total_out, uint32_t cap,
-                                  hipStream_t st);
+                                  bool reduce_scan, hipStream_t st);
 // Digit width of a device sort over `bits` key bits: the fewest 8-bit-or-less
 // passes, with the bits spread evenly over them (12 tile bits: two passes of 6,
 // whose 64 digits give longer runs per digit than 256 would).

@@ -82,10 +82,19 @@ __device__ __forceinline__ bool pair_keep(float px, float py, float4 cv, int til
     return (m2thr >= 0.0f) & ((x_in & y_in) | (fmin_std(m2_v, m2_h) <= scaled));
 }
 
-// Rectangle area per rank, exclusive scan -> offs[r]; last partition writes
-// the total candidate count (saturated to 0xFFFFFFFF on overflow).
-// Also records, for every emit partition b (candidates [b*kEmitPart, ...)),
-// the rank that owns its first candidate: bstart[b].
+// Rectangle area per rank, exclusive scan -> offs[r]; the total candidate
+// count goes to *total_out (saturated to 0xFFFFFFFF on overflow). Also
+// records, for every emit partition b (candidates [b*kEmitPart, ...)), the
+// rank that owns its first candidate: bstart[b].
+//   kScanLookback: one kernel, partitions chained by a decoupled look-back.
+//   kScanReduce / kScanFinal: reduce-then-scan without waits, for a frame with
+//     other frames in flight (a look-back chain advances only as fast as its
+//     slowest partition, and other frames' kernels slow its partitions): the
+//     reduce kernel writes each partition's sum to part[vid], a one-workgroup
+//     kernel turns them into exclusive bases (k_scan_part_sums), and the final
+//     kernel re-reads the counts and writes the offsets from its base.
+constexpr int kScanLookback = 0, kScanReduce = 1, kScanFinal = 2;
+template <int PHASE>
 __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4* __restrict__ rect,
                                                               int stride,
                                                               const uint32_t* __restrict__ order,
@@ -103,7 +112,10 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
     __shared__ uint32_t s_wsum[kCountItems][kCountWaves];
     __shared__ uint64_t s_excl;
     const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
-    if (tid == 0) s_vid = upstream_failed(tp.ctl) ? 0xFFFFFFFFu : atomicAdd(ticket, 1u);
+    if (tid == 0) {
+        const bool failed = upstream_failed(tp.ctl);
+        s_vid = failed ? 0xFFFFFFFFu : (PHASE == kScanLookback ? atomicAdd(ticket, 1u) : blockIdx.x);
+    }
     __syncthreads();
     const uint32_t vid = s_vid;
     if (vid == 0xFFFFFFFFu) return;  // the depth order may be wrong: touch nothing
@@ -164,7 +176,14 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
             if (ww == w) my_off[it] = total;
             total += s_wsum[it][ww];
         }
-    if (w == 0) {
+    if (PHASE == kScanReduce) {
+        // lb_state[vid]: this partition's sum, for k_scan_part_sums
+        if (tid == 0) lb_state[vid] = total;
+        return;
+    }
+    if (PHASE == kScanFinal) {
+        if (tid == 0) s_excl = lb_state[vid];  // the exclusive base
+    } else if (w == 0) {
         const uint64_t ex = lookback_exclusive(lb_state, vid, total, tp.ctl);
         if (lane == 0) {
             s_excl = ex;
@@ -189,6 +208,42 @@ __global__ __launch_bounds__(kCountThreads) void k_rect_count_scan(const float4*
             uint64_t b = (o + kEmitPart - 1) / kEmitPart;
             for (; b * kEmitPart < o + cnt[it] && b < bstart_cap; ++b) bstart[b] = (uint32_t)r;
         }
+    }
+}
+
+// Exclusive scan of the count scan's partition sums in place (one workgroup:
+// each thread a run of consecutive partitions), the total candidate count to
+// *total_out (saturated to 0xFFFFFFFF) and kErrCapacity when it exceeds cap.
+constexpr int kSumThreads = 1024;
+__global__ __launch_bounds__(kSumThreads) void k_scan_part_sums(uint64_t* __restrict__ part,
+                                                               int64_t m_cap,
+                                                               const uint32_t* __restrict__ m_dev,
+                                                               uint32_t* total_out, uint32_t cap,
+                                                               uint32_t* ctl) {
+    __shared__ uint64_t s_w[kSumThreads / GS_WAVE];
+    if (upstream_failed(ctl)) return;  // uniform over the workgroup
+    const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
+    const int64_t m = m_dev ? min(m_cap, (int64_t)*m_dev) : m_cap;
+    const uint32_t nparts = (uint32_t)((m + kCountPart - 1) / kCountPart);
+    const uint32_t per = (nparts + kSumThreads - 1) / kSumThreads;
+    const uint32_t p0 = min(nparts, (uint32_t)tid * per), p1 = min(nparts, p0 + per);
+    uint64_t sum = 0;
+    for (uint32_t q = p0; q < p1; ++q) sum += part[q];
+    const uint64_t inc = wave_incl_scan64(sum);
+    if (lane == GS_WAVE - 1) s_w[w] = inc;
+    __syncthreads();
+    uint64_t run = inc - sum;
+    for (int i = 0; i < w; ++i) run += s_w[i];
+    for (uint32_t q = p0; q < p1; ++q) {
+        const uint64_t v = part[q];
+        part[q] = run;
+        run += v;
+    }
+    if (tid == kSumThreads - 1) {
+        *total_out = run > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)run;
+        // the frame is run again with room for them: the kernels after this
+        // one skip their work
+        if (cap != 0u && run > cap) report_error(ctl, kErrCapacity);
     }
 }
 
@@ -615,13 +670,23 @@ hipError_t launch_rect_count_scan(const float4* rect, int stride, const uint32_t
                                   int64_t m, const uint32_t* m_dev, TileParams tp, uint32_t* offs,
                                   uint32_t* bstart, uint32_t bstart_cap, uint64_t* lb_state,
                                   uint32_t* ticket, uint32_t* total_out, uint32_t cap,
-                                  hipStream_t st) {
+                                  bool reduce_scan, hipStream_t st) {
     if (m <= 0) return hipSuccess;
     if (stride < 1) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)rect_scan_partitions(m);
-    k_rect_count_scan<<<grid, kCountThreads, 0, st>>>(rect, stride, order, m, m_dev, tp, offs,
-                                                      bstart, bstart_cap, lb_state, ticket,
-                                                      total_out, cap);
+    if (!reduce_scan) {
+        k_rect_count_scan<kScanLookback><<<grid, kCountThreads, 0, st>>>(
+            rect, stride, order, m, m_dev, tp, offs, bstart, bstart_cap, lb_state, ticket,
+            total_out, cap);
+        return hipGetLastError();
+    }
+    k_rect_count_scan<kScanReduce><<<grid, kCountThreads, 0, st>>>(
+        rect, stride, order, m, m_dev, tp, offs, bstart, bstart_cap, lb_state, ticket, total_out,
+        cap);
+    k_scan_part_sums<<<1, kSumThreads, 0, st>>>(lb_state, m, m_dev, total_out, cap, tp.ctl);
+    k_rect_count_scan<kScanFinal><<<grid, kCountThreads, 0, st>>>(
+        rect, stride, order, m, m_dev, tp, offs, bstart, bstart_cap, lb_state, ticket, total_out,
+        cap);
     return hipGetLastError();
 }
 
