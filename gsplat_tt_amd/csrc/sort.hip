@@ -401,7 +401,15 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
                 const K k = s_keys[j];
                 const uint32_t g = s_gpos[digit_of(k, shift, mask)] + (uint32_t)j;
                 gq[q] = g;
-                if ((int64_t)g < n) kout[g] = k;
+                if (!RUNS && (int64_t)g < n) kout[g] = k;
+                if (RUNS) {
+                    // run [a, b) of key k: + b at its last key, - a at its first
+                    const bool first = j == 0 || s_keys[j - 1] != k;
+                    const bool last = j == count - 1 || s_keys[j + 1] != k;
+                    const uint32_t delta =
+                        (last ? (uint32_t)j + 1u : 0u) - (first ? (uint32_t)j : 0u);
+                    if (first || last) atomicAdd(&run_cnt[(uint32_t)k], delta);
+                }
             }
         }
         __syncthreads();  // the keys are out: their LDS space takes the values
@@ -483,7 +491,7 @@ hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uin
                                                                 tmp.ctl, next_hist, next_shift,  \
                                                                 next_bits, run_cnt)
     if (run_cnt != nullptr) {
-        if (iota || sizeof(K) != 4 || SP) return hipErrorInvalidValue;
+        if (iota || sizeof(K) != 4) return hipErrorInvalidValue;
         if (drop) {  // a one-pass sort: it drops and counts
             if (d32) GS_OS(false, true, true, true); else GS_OS(false, false, true, true);
         } else {
