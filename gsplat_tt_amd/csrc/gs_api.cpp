@@ -226,7 +226,8 @@ struct gs_ctx {
                           &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_bstart, &b_pair_tile, &b_pair_id,
                           &b_ranges, &b_out, &b_kalt, &b_valt, &b_hist, &b_state, &b_lb, &b_cnt,
                           &b_tmp_a, &b_tmp_b, &b_tmp_c, &b_evals, &b_frame, &b_phist_proj,
-                          &b_phist_emit, &b_spec, &b_chunk_box, &b_skip})
+                          &b_phist_emit, &b_pchunk, &b_poffs, &b_spec, &b_chunk_box,
+                          &b_skip})
             b->release();
         if (h_pin) (void)hipHostFree(h_pin);
         ring.reset();  // held images stay valid until their leases are released
@@ -542,6 +543,10 @@ struct gs_ctx {
     };
     uint64_t pair_cap = 0;  // candidate-pair capacity of the frame buffers
     DevBuf b_frame, b_phist_proj, b_phist_emit;
+    DevBuf b_pchunk, b_poffs;  // tile sort's first pass: emit row chunk sums, offsets
+    static constexpr size_t kEmitPerSort = gs::kSortPartition32 / gs::kEmitPartition;
+    static_assert(gs::kSortPartition32 % gs::kEmitPartition == 0,
+                  "a sort partition is whole emit partitions");
 
     // One frame with no host synchronisation until the end: every size that
     // only the device knows (visible count, candidate and kept pairs) is read
@@ -868,6 +873,11 @@ struct gs_ctx {
         b_ranges.ensure((size_t)T * 8);
         b_phist_proj.ensure(L.pparts * 1024 * 4);
         b_phist_emit.ensure(L.eparts * gs::tile_hist_cols(tile_bits(T)) * 4);
+        b_pchunk.ensure(gs::reduce_chunks((uint32_t)L.eparts) * gs::tile_hist_cols(tile_bits(T)) *
+                        4);
+        b_poffs.ensure(((L.eparts + kEmitPerSort - 1) / kEmitPerSort)
+                       << gs::sort_digit_width(tile_bits(T))
+                       << 2);
         const size_t lb_words = 2 * (L.pparts + L.rparts + L.eparts);
         L.fwords = kFrLb + lb_words + (size_t)T;
         b_frame.ensure(L.fwords * 4);
@@ -914,11 +924,17 @@ struct gs_ctx {
                                     b_pair_id.as<uint32_t>(), L.pcap, L.lb_emit,
                                     cnt + C_EMIT_TICKET, cnt + C_P, b_phist_emit.as<uint32_t>(),
                                     tile_bits(T), false, st));
-        HIPCHK(gs::launch_reduce_rows(b_phist_emit.as<uint32_t>(),
-                                      gs::tile_hist_cols(tile_bits(T)), (uint32_t)L.eparts,
-                                      cnt + C_PPRE, L.pcap, gs::kEmitPartition,
-                                      gs::sort_digit_width(tile_bits(T)), fr + kFrTileHist,
-                                      st));
+        const int hcols = gs::tile_hist_cols(tile_bits(T));
+        const int dw = gs::sort_digit_width(tile_bits(T));
+        HIPCHK(gs::launch_reduce_rows(b_phist_emit.as<uint32_t>(), hcols, (uint32_t)L.eparts,
+                                      cnt + C_PPRE, L.pcap, gs::kEmitPartition, dw,
+                                      fr + kFrTileHist, st, b_pchunk.as<uint32_t>()));
+        // the first tile pass's output positions per partition, from the emit
+        // rows (four emit partitions per sort partition): no look-back
+        HIPCHK(gs::launch_part_offsets(b_phist_emit.as<uint32_t>(), hcols, (uint32_t)L.eparts,
+                                       cnt + C_PPRE, L.pcap, gs::kEmitPartition, kEmitPerSort,
+                                       dw, b_pchunk.as<uint32_t>(), fr + kFrTileHist,
+                                       b_poffs.as<uint32_t>(), st));
         record(3);
         // stable tile sort of the depth-ordered candidate slots; its first pass
         // drops the culled ones (kPairDrop), so the kept pairs come out compact
@@ -927,7 +943,8 @@ struct gs_ctx {
         HIPCHK(gs::radix_sort_pairs_dev(b_pair_tile.p, b_pair_id.as<uint32_t>(), L.pcap,
                                         cnt + C_PPRE, 4, 0, tile_bits(T), fr + kFrTileHist,
                                         cnt + C_TSORT_TICKETS, sort, st, false, &tiles_sorted,
-                                        &ids_sorted, cnt + C_P, want_keys ? nullptr : L.tcnt));
+                                        &ids_sorted, cnt + C_P, want_keys ? nullptr : L.tcnt,
+                                        b_poffs.as<uint32_t>()));
         if (want_keys) {
             HIPCHK(gs::launch_tile_bounds(static_cast<uint32_t*>(tiles_sorted), L.pcap, cnt + C_P,
                                           b_ranges.as<uint32_t>(), T, st));

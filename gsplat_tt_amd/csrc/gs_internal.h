@@ -140,13 +140,18 @@ hipError_t radix_sort_pairs(void* keys, uint32_t* vals, int64_t n, int key_bytes
 // passes sort min(n_cap, *n_kept_dev) keys, and `hist` counts kept keys only.
 // run_cnt (u32 keys only, optional): the sorted keys are not written (*keys_final = nullptr); run_cnt[k] (cleared by the caller) gains
 // the number of keys equal to k, for launch_ranges_from_counts.
+// first_offs (u32 keys only, optional): the first pass's output positions per
+// partition of kSortPartition32 keys and digit (2^w words per partition, w the
+// pass's digit width; launch_part_offsets): that pass needs no look-back.
 constexpr uint32_t kPairDrop = 0xFFFFFFFFu;
+constexpr uint32_t kSortPartition32 = 8192;  // keys per partition of a 32-bit-key pass
 hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const uint32_t* n_dev,
                                 int key_bytes, int begin_bit, int end_bit, const uint32_t* hist,
                                 uint32_t* tickets, SortTemp& tmp, hipStream_t st, bool vals_iota,
                                 void** keys_final, uint32_t** vals_final,
                                 const uint32_t* n_kept_dev = nullptr,
-                                uint32_t* run_cnt = nullptr);
+                                uint32_t* run_cnt = nullptr,
+                                const uint32_t* first_offs = nullptr);
 
 // The 64-bit-key sort of radix_sort_pairs_dev over exactly n keys, with no
 // producer histogram: a histogram kernel counts the first pass's digits and
@@ -235,9 +240,23 @@ hipError_t launch_tile_bounds64(const uint64_t* sorted_keys, uint32_t p, uint32_
 // out[c] += sum over rows of part[r][c] (out must be cleared by the caller);
 // with dig_w > 0 the columns are digit rows of 2^dig_w words and column c adds
 // into out[(c >> dig_w) * 256 + (c & (2^dig_w - 1))].
+// chunk_out (optional, reduce_chunks(rows_cap) x cols words): the column sums
+// of each workgroup's rows, for launch_part_offsets.
 hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,
                               const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
-                              int dig_w, uint32_t* out, hipStream_t st);
+                              int dig_w, uint32_t* out, hipStream_t st,
+                              uint32_t* chunk_out = nullptr);
+size_t reduce_chunks(uint32_t rows_cap);
+// After launch_reduce_rows with chunk_out over the same rows: per partition of
+// rows_per_part rows and per digit d < 2^dig_w (columns 0 .. 2^dig_w - 1 of a
+// row), offs[s << dig_w | d] = (sum of hist[d'] over d' < d) + (sum of
+// part[e][d] over rows e < s * rows_per_part): the output position of the
+// partition's first key of digit d in a sort pass over those keys (hist: that
+// pass's digit histogram). ceil(rows in use / rows_per_part) << dig_w words.
+hipError_t launch_part_offsets(const uint32_t* part, int cols, uint32_t rows_cap,
+                               const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
+                               int rows_per_part, int dig_w, const uint32_t* chunks,
+                               const uint32_t* hist, uint32_t* offs, hipStream_t st);
 constexpr uint32_t kEmitPartition = 2048;   // candidates per emit partition
 constexpr uint32_t kProjPartition = 2048;   // Gaussians per project partition
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t st);

@@ -200,6 +200,10 @@ __device__ __forceinline__ uint32_t digit_walk(DT* state, uint32_t vid, int digi
 // keys are not written; instead every run of equal keys in the partition (the
 // last pass leaves a partition sorted by all the key bits in LDS) adds its
 // length to run_cnt[key], with at most two atomics per run.
+// part_offs (optional, 2^bits words per partition): partition vid's keys of
+// digit d start at part_offs[vid << bits | d] of the output (the digit's base
+// plus the kept keys of that digit in all earlier partitions, counted by the
+// keys' producer): the partition neither publishes nor walks back.
 template <typename K, bool IOTA, int THREADS, int ITEMS, bool D32, bool DROP, bool SPLIT,
           bool RUNS>
 __global__ __launch_bounds__(THREADS) void k_onesweep(
@@ -208,7 +212,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     int bits, const uint32_t* __restrict__ g_hist_pass, void* __restrict__ state_raw,
     uint32_t* __restrict__ ticket, uint32_t epoch, uint32_t* __restrict__ clear_next,
     uint32_t* ctl, uint32_t* __restrict__ next_hist, int next_shift, int next_bits,
-    uint32_t* __restrict__ run_cnt) {
+    uint32_t* __restrict__ run_cnt, const uint32_t* __restrict__ part_offs) {
     using D = Desc<D32>;
     using DT = typename D::T;
     DT* state = static_cast<DT*>(state_raw);
@@ -305,7 +309,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     // A digit absent from the whole pass publishes nothing and looks back at
     // nothing (all partitions agree: the histogram is global).
     uint32_t tot = 0;
-    const bool has_digit = tid < 256 && g_hist_pass[tid] != 0u;
+    const bool has_digit = part_offs == nullptr && tid < 256 && g_hist_pass[tid] != 0u;
     if (tid < 256) {
 #pragma unroll
         for (int ww = 0; ww < WAVES; ++ww) {
@@ -354,8 +358,13 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         }
     }
     if (tid < 256) {
-        const uint32_t excl = has_digit ? digit_walk<D, DT>(state, vid, tid, tot, epoch, ctl) : 0u;
-        s_gpos[tid] = gbase + excl - loff;
+        if (part_offs != nullptr) {
+            s_gpos[tid] = tid <= (int)mask ? part_offs[((size_t)vid << bits) | tid] - loff : 0u;
+        } else {
+            const uint32_t excl =
+                has_digit ? digit_walk<D, DT>(state, vid, tid, tot, epoch, ctl) : 0u;
+            s_gpos[tid] = gbase + excl - loff;
+        }
     }
     if (next_hist != nullptr) {
         // the next pass's digit histogram from the keys in registers: the
@@ -440,6 +449,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
 struct Sweep64 { static constexpr int T = 1024, I = 8; static constexpr bool SPLIT = true; };
 struct Sweep32 { static constexpr int T = 1024, I = 8; static constexpr bool SPLIT = false; };
 constexpr int kMinPart = Sweep32::T * Sweep32::I;  // the smallest partition of all shapes
+static_assert(kMinPart == (int)kSortPartition32, "first-pass offsets index these partitions");
 static_assert(kMinPart <= Sweep64::T * Sweep64::I, "kMinPart sizes the look-back state");
 
 __global__ void k_fill_u32(uint32_t* p, uint32_t v, size_t n) {
@@ -458,7 +468,7 @@ hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uin
                       int64_t n_cap, const uint32_t* n_dev, int shift, int bits,
                       const uint32_t* hist_pass, SortTemp& tmp, uint32_t* ticket, hipStream_t st,
                       bool drop, uint32_t* next_hist, int next_shift, int next_bits,
-                      uint32_t* run_cnt) {
+                      uint32_t* run_cnt, const uint32_t* part_offs) {
     constexpr int T = CFG::T, I = CFG::I;
     constexpr bool SP = CFG::SPLIT;
     const unsigned grid = (unsigned)((n_cap + T * I - 1) / (T * I));
@@ -489,7 +499,7 @@ hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uin
                                                                 n_dev, shift, bits, hist_pass,   \
                                                                 state, ticket, epoch, clear_next,\
                                                                 tmp.ctl, next_hist, next_shift,  \
-                                                                next_bits, run_cnt)
+                                                                next_bits, run_cnt, part_offs)
     if (run_cnt != nullptr) {
         if (iota || sizeof(K) != 4) return hipErrorInvalidValue;
         if (drop) {  // a one-pass sort: it drops and counts
@@ -518,14 +528,15 @@ hipError_t launch_pass(bool iota, const K* kin, const uint32_t* vin, K* kout, ui
                        int64_t n_cap, const uint32_t* n_dev, int shift, int bits,
                        const uint32_t* hist_pass, SortTemp& tmp, uint32_t* ticket,
                        hipStream_t st, bool drop = false, uint32_t* next_hist = nullptr,
-                       int next_shift = 0, int next_bits = 0, uint32_t* run_cnt = nullptr) {
+                       int next_shift = 0, int next_bits = 0, uint32_t* run_cnt = nullptr,
+                       const uint32_t* part_offs = nullptr) {
     if constexpr (sizeof(K) == 8)
         return launch_cfg<K, Sweep64>(iota, kin, vin, kout, vout, n_cap, n_dev, shift, bits,
                                       hist_pass, tmp, ticket, st, drop, next_hist, next_shift,
-                                      next_bits, run_cnt);
+                                      next_bits, run_cnt, part_offs);
     return launch_cfg<K, Sweep32>(iota, kin, vin, kout, vout, n_cap, n_dev, shift, bits,
                                   hist_pass, tmp, ticket, st, drop, next_hist, next_shift,
-                                  next_bits, run_cnt);
+                                  next_bits, run_cnt, part_offs);
 }
 
 template <typename K>
@@ -600,7 +611,7 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
                          SortTemp& tmp, hipStream_t st, bool vals_iota, K** keys_final,
                          uint32_t** vals_final, const uint32_t* n_kept_dev,
                          uint32_t* chain_hist = nullptr, bool pass_events = false,
-                         uint32_t* run_cnt = nullptr) {
+                         uint32_t* run_cnt = nullptr, const uint32_t* first_offs = nullptr) {
     *keys_final = keys;
     *vals_final = vals;
     if (n_cap <= 0) return hipSuccess;
@@ -625,7 +636,8 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
                                       shift, bits, hist + p * 256, tmp, tickets + p, st, drop,
                                       chain ? chain_hist + (p + 1) * 256 : nullptr, nshift,
                                       chain ? std::min(dw, end_bit - nshift) : 0,
-                                      p + 1 == npass ? run_cnt : nullptr);
+                                      p + 1 == npass ? run_cnt : nullptr,
+                                      p == 0 ? first_offs : nullptr);
         if (timed) (void)hipEventRecord(tmp.pass_events[2 * p + 1], st);
         if (e != hipSuccess) return e;
         std::swap(kin, kalt);
@@ -642,18 +654,20 @@ hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const
                                 int key_bytes, int begin_bit, int end_bit, const uint32_t* hist,
                                 uint32_t* tickets, SortTemp& tmp, hipStream_t st, bool vals_iota,
                                 void** keys_final, uint32_t** vals_final,
-                                const uint32_t* n_kept_dev, uint32_t* run_cnt) {
+                                const uint32_t* n_kept_dev, uint32_t* run_cnt,
+                                const uint32_t* first_offs) {
     if (key_bytes == 4) {
         uint32_t* kf = nullptr;
         hipError_t e = sort_dev_impl<uint32_t>(static_cast<uint32_t*>(keys), vals, n_cap, n_dev,
                                                begin_bit, end_bit, hist, tickets, tmp, st,
                                                vals_iota, &kf, vals_final, n_kept_dev, nullptr,
-                                               false, run_cnt);
+                                               false, run_cnt, first_offs);
         *keys_final = run_cnt != nullptr ? nullptr : kf;
         return e;
     }
     if (key_bytes == 8) {
-        if (n_kept_dev != nullptr || run_cnt != nullptr) return hipErrorInvalidValue;
+        if (n_kept_dev != nullptr || run_cnt != nullptr || first_offs != nullptr)
+            return hipErrorInvalidValue;
         uint64_t* kf = nullptr;
         hipError_t e = sort_dev_impl<uint64_t>(static_cast<uint64_t*>(keys), vals, n_cap, n_dev,
                                                begin_bit, end_bit, hist, tickets, tmp, st,

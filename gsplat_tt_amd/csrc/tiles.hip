@@ -546,24 +546,31 @@ __global__ __launch_bounds__(256) void k_tile_bounds(const K* __restrict__ st, u
     }
 }
 
+// Rows of part that hold counts: ceil(min(*count_dev, count_cap) / per_row)
+// when count_dev is given, else all rows_cap.
+__device__ __forceinline__ uint32_t rows_in_use(uint32_t rows_cap, const uint32_t* count_dev,
+                                                uint32_t count_cap, uint32_t per_row) {
+    if (count_dev == nullptr) return rows_cap;
+    const uint32_t c = min(*count_dev, count_cap);
+    return min(rows_cap, (uint32_t)(((uint64_t)c + per_row - 1) / per_row));
+}
+
 // out[c] += column sums of part (rows x cols, cols / 4 dividing 1024), rows
-// bounded by ceil(min(*count_dev, count_cap) / per_row) when count_dev is
-// given. A 1024-thread workgroup takes `span` rows: cols / 4 column quads x
-// (4096 / cols) row lanes, 16-byte loads with 8 rows in flight per lane; the
-// row lanes are summed in LDS and each workgroup adds its column sums with one
-// atomic per column (few workgroups, so little contention on the atomics).
+// bounded by rows_in_use. A 1024-thread workgroup takes `span` rows: cols / 4
+// column quads x (4096 / cols) row lanes, 16-byte loads with 8 rows in flight
+// per lane; the row lanes are summed in LDS and each workgroup adds its column
+// sums with one atomic per column (few workgroups, so little contention on the
+// atomics). chunk_out (optional): workgroup b also stores its column sums at
+// chunk_out[b * cols + c], zeros included (workgroups past the rows in use
+// store nothing).
 constexpr int kRedThreads = 1024;
 constexpr uint32_t kRedBlocks = 96;  // workgroups for the largest row count
 __global__ __launch_bounds__(kRedThreads) void k_reduce_rows(
     const uint32_t* __restrict__ part, int cols, uint32_t rows_cap, uint32_t span,
     const uint32_t* __restrict__ count_dev, uint32_t count_cap, uint32_t per_row, int dig_w,
-    uint32_t* __restrict__ out) {
+    uint32_t* __restrict__ out, uint32_t* __restrict__ chunk_out) {
     __shared__ uint4 s_acc[kRedThreads];
-    uint32_t rows = rows_cap;
-    if (count_dev) {
-        const uint32_t c = min(*count_dev, count_cap);
-        rows = min(rows_cap, (uint32_t)(((uint64_t)c + per_row - 1) / per_row));
-    }
+    const uint32_t rows = rows_in_use(rows_cap, count_dev, count_cap, per_row);
     const uint32_t r0 = blockIdx.x * span;
     if (r0 >= rows) return;  // uniform over the workgroup
     const int quads = cols / 4;
@@ -590,6 +597,8 @@ __global__ __launch_bounds__(kRedThreads) void k_reduce_rows(
             acc.z += v.z;
             acc.w += v.w;
         }
+        if (chunk_out != nullptr)
+            reinterpret_cast<uint4*>(chunk_out + (size_t)blockIdx.x * cols)[q] = acc;
         // column c -> out[c], or with digit rows of 2^dig_w words -> the digit's
         // row of 256 words
         const uint32_t a[4] = {acc.x, acc.y, acc.z, acc.w};
@@ -599,6 +608,79 @@ __global__ __launch_bounds__(kRedThreads) void k_reduce_rows(
             const uint32_t o = dig_w ? ((c >> dig_w) << 8) | (c & ((1u << dig_w) - 1u)) : c;
             if (a[j]) atomicAdd(out + o, a[j]);
         }
+    }
+}
+
+// Output positions of a sort pass per partition of rows_per_part rows of
+// `part` (the per-partition digit counts of the keys' producer, the pass's
+// digit in the first 2^dig_w columns of each row) and per digit:
+// offs[s << dig_w | d] = base[d] + sum over rows e < s * rows_per_part of
+// part[e][d], base[d] = sum of hist[d'] over d' < d (the pass's histogram).
+// Workgroup b covers the rows of k_reduce_rows's workgroup b (span rows, a
+// multiple of rows_per_part) and starts from the column sums of the chunks
+// before it. Thread (d, g): digit d, g-th contiguous run of the chunk's
+// partitions; the runs' sums are scanned in LDS, then each thread writes its
+// partitions' offsets. No look-back: every workgroup reads only sums that the
+// reduce finished before this kernel started.
+constexpr int kOffsThreads = 1024;
+__global__ __launch_bounds__(kOffsThreads) void k_part_offsets(
+    const uint32_t* __restrict__ part, int cols, uint32_t rows_cap, uint32_t span,
+    const uint32_t* __restrict__ count_dev, uint32_t count_cap, uint32_t per_row,
+    int rows_per_part, int dig_w, const uint32_t* __restrict__ chunks,
+    const uint32_t* __restrict__ hist, uint32_t* __restrict__ offs) {
+    __shared__ uint32_t s_base[256];
+    __shared__ uint32_t s_run[kOffsThreads];
+    const uint32_t rows = rows_in_use(rows_cap, count_dev, count_cap, per_row);
+    const uint32_t r0 = blockIdx.x * span;
+    if (r0 >= rows) return;  // uniform over the workgroup
+    const int nd = 1 << dig_w, G = kOffsThreads / nd;
+    const int tid = threadIdx.x, d = tid % nd, g = tid / nd;
+    // digit bases: exclusive scan of the pass's histogram (one wave, four
+    // digits per lane)
+    if (tid < GS_WAVE) {
+        uint32_t h[4], sum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int dd = tid * 4 + i;
+            h[i] = dd < nd ? hist[dd] : 0u;
+            sum += h[i];
+        }
+        uint32_t ex = wave_incl_scan(sum) - sum;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (tid * 4 + i < nd) s_base[tid * 4 + i] = ex;
+            ex += h[i];
+        }
+    }
+    // counts of the chunks before this one
+    uint32_t pre = 0;
+#pragma unroll 4
+    for (uint32_t b = (uint32_t)g; b < blockIdx.x; b += (uint32_t)G)
+        pre += chunks[(size_t)b * cols + d];
+    // this thread's run of partitions inside the chunk
+    const uint32_t r1 = min(rows, r0 + span);
+    const uint32_t p0 = r0 / rows_per_part;
+    const uint32_t nparts = (r1 - r0 + rows_per_part - 1) / rows_per_part;
+    const uint32_t per = (nparts + G - 1) / G;
+    const uint32_t q0 = min(nparts, (uint32_t)g * per), q1 = min(nparts, q0 + per);
+    uint32_t run = 0;
+    const uint32_t ea = r0 + q0 * rows_per_part, eb = min(r1, r0 + q1 * rows_per_part);
+#pragma unroll 8
+    for (uint32_t e = ea; e < eb; ++e) run += part[(size_t)e * cols + d];
+    s_run[tid] = pre;
+    __syncthreads();
+    uint32_t carry = s_base[d];
+    for (int gg = 0; gg < G; ++gg) carry += s_run[gg * nd + d];  // chunks before
+    __syncthreads();
+    s_run[tid] = run;
+    __syncthreads();
+    for (int gg = 0; gg < g; ++gg) carry += s_run[gg * nd + d];  // earlier runs
+    for (uint32_t q = q0; q < q1; ++q) {
+        offs[((size_t)(p0 + q) << dig_w) | (uint32_t)d] = carry;
+        const uint32_t e0 = r0 + q * rows_per_part;
+        const uint32_t e1 = min(r1, e0 + rows_per_part);
+#pragma unroll 4
+        for (uint32_t e = e0; e < e1; ++e) carry += part[(size_t)e * cols + d];
     }
 }
 
@@ -756,16 +838,42 @@ hipError_t launch_tile_bounds64(const uint64_t* sorted_keys, uint32_t p, uint32_
     return hipGetLastError();
 }
 
+uint32_t reduce_span(uint32_t rows_cap) {
+    const uint32_t span = std::max<uint32_t>(32, (rows_cap + kRedBlocks - 1) / kRedBlocks);
+    return (span + 3u) & ~3u;
+}
+
+size_t reduce_chunks(uint32_t rows_cap) {
+    const uint32_t span = reduce_span(rows_cap);
+    return (rows_cap + span - 1) / span;
+}
+
 hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,
                               const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
-                              int dig_w, uint32_t* out, hipStream_t st) {
+                              int dig_w, uint32_t* out, hipStream_t st, uint32_t* chunk_out) {
     if (rows_cap == 0) return hipSuccess;
     if (cols <= 0 || cols % 4 != 0 || kRedThreads % (cols / 4) != 0) return hipErrorInvalidValue;
-    const uint32_t span = std::max<uint32_t>(32, (rows_cap + kRedBlocks - 1) / kRedBlocks);
+    const uint32_t span = reduce_span(rows_cap);
     const unsigned grid = (rows_cap + span - 1) / span;
     if (dig_w < 0 || dig_w > 8) return hipErrorInvalidValue;
     k_reduce_rows<<<grid, kRedThreads, 0, st>>>(part, cols, rows_cap, span, count_dev,
-                                                count_cap, per_row, dig_w, out);
+                                                count_cap, per_row, dig_w, out, chunk_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_part_offsets(const uint32_t* part, int cols, uint32_t rows_cap,
+                               const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
+                               int rows_per_part, int dig_w, const uint32_t* chunks,
+                               const uint32_t* hist, uint32_t* offs, hipStream_t st) {
+    if (rows_cap == 0) return hipSuccess;
+    const uint32_t span = reduce_span(rows_cap);
+    if (dig_w < 0 || dig_w > 8 || (1 << dig_w) > cols || rows_per_part <= 0 ||
+        span % (uint32_t)rows_per_part != 0)
+        return hipErrorInvalidValue;
+    const unsigned grid = (rows_cap + span - 1) / span;
+    k_part_offsets<<<grid, kOffsThreads, 0, st>>>(part, cols, rows_cap, span, count_dev,
+                                                  count_cap, per_row, rows_per_part, dig_w,
+                                                  chunks, hist, offs);
     return hipGetLastError();
 }
 
