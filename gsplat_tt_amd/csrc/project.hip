@@ -116,30 +116,61 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
     bool valid[kProjItems];
     uint64_t bal[kProjItems];
 
+    // loads in two stages over all items: the means and opacities, then the
+    // covariance words of the items that pass the depth and opacity tests
+    float ltx[kProjItems], lty[kProjItems], ltz[kProjItems];
+    bool lok[kProjItems];
+    {
+        float lmx[kProjItems], lmy[kProjItems], lmz[kProjItems], lop[kProjItems];
+#pragma unroll
+        for (int it = 0; it < kProjItems; ++it) {
+            const int64_t i = base + it * kProjThreads + tid;
+            const bool in = i < n && !skipped;
+            lmx[it] = in ? s.mean[0][i] : 0.0f;
+            lmy[it] = in ? s.mean[1][i] : 0.0f;
+            lmz[it] = in ? s.mean[2][i] : 0.0f;
+            lop[it] = (in && p.has_opac) ? s.opac[i] : 1.0f;
+        }
+#pragma unroll
+        for (int it = 0; it < kProjItems; ++it) {
+            const int64_t i = base + it * kProjThreads + tid;
+            const float mx = lmx[it], my = lmy[it], mz = lmz[it];
+            const float rmx = mx * p.r[0] + my * p.r[1] + mz * p.r[2];
+            const float rmy = mx * p.r[3] + my * p.r[4] + mz * p.r[5];
+            const float rmz = mx * p.r[6] + my * p.r[7] + mz * p.r[8];
+            ltx[it] = rmx + p.t[0];
+            lty[it] = rmy + p.t[1];
+            ltz[it] = rmz + p.t[2];
+            bool ok = i < n && !skipped && !(ltz[it] <= 0.2f);
+            if (p.has_opac) ok = ok && !(lop[it] < p.min_opacity);
+            lok[it] = ok;
+        }
+    }
+    float lc[6][kProjItems], lk[kProjItems];
+#pragma unroll
+    for (int it = 0; it < kProjItems; ++it) {
+        const int64_t i = base + it * kProjThreads + tid;
+#pragma unroll
+        for (int q = 0; q < 6; ++q) lc[q][it] = lok[it] ? s.cov[q][i] : 0.0f;
+        lk[it] = lok[it] ? s.kfac[i] : 0.0f;
+    }
+
 #pragma unroll
     for (int it = 0; it < kProjItems; ++it) {
         const int64_t i = base + it * kProjThreads + tid;
         valid[it] = false;
         vmx[it] = vmy[it] = vtz[it] = va[it] = vb[it] = vc[it] = vrx[it] = vry[it] = 0.0f;
-        if (i < n && !skipped) {
-            const float mx = s.mean[0][i], my = s.mean[1][i], mz = s.mean[2][i];
-            const float rmx = mx * p.r[0] + my * p.r[1] + mz * p.r[2];
-            const float rmy = mx * p.r[3] + my * p.r[4] + mz * p.r[5];
-            const float rmz = mx * p.r[6] + my * p.r[7] + mz * p.r[8];
-            const float tx = rmx + p.t[0];
-            const float ty = rmy + p.t[1];
-            const float tz = rmz + p.t[2];
-            bool ok = !(tz <= 0.2f);
-            if (ok && p.has_opac) ok = !(s.opac[i] < p.min_opacity);
-            if (ok) {
+        {
+            const float tx = ltx[it], ty = lty[it], tz = ltz[it];
+            if (lok[it]) {
                 const float inv_tz = 1.0f / tz;
                 const float mean_x = p.fx * tx * inv_tz + p.cx;
                 const float mean_y = p.fy * ty * inv_tz + p.cy;
                 const float tz2 = tz * tz;
                 const float j00 = p.fx / tz, j02 = -p.fx * tx / tz2;
                 const float j11 = p.fy / tz, j12 = -p.fy * ty / tz2;
-                const float c00 = s.cov[0][i], c01 = s.cov[1][i], c02 = s.cov[2][i];
-                const float c11 = s.cov[3][i], c12 = s.cov[4][i], c22 = s.cov[5][i];
+                const float c00 = lc[0][it], c01 = lc[1][it], c02 = lc[2][it];
+                const float c11 = lc[3][it], c12 = lc[4][it], c22 = lc[5][it];
                 const float r00 = p.r[0], r01 = p.r[1], r02 = p.r[2];
                 const float r10 = p.r[3], r11 = p.r[4], r12 = p.r[5];
                 const float r20 = p.r[6], r21 = p.r[7], r22 = p.r[8];
@@ -166,7 +197,7 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
                 const float a = m00 * j00 + m02 * j02 + 0.3f;
                 const float b = m01 * j11 + m02 * j12;
                 const float c = m11 * j11 + m12 * j12 + 0.3f;
-                const float k = s.kfac[i];
+                const float k = lk[it];
                 float rx, ry;
                 if (p.use_iso) {
                     const float trace = a + c;
