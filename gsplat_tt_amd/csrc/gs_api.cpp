@@ -570,8 +570,8 @@ struct gs_ctx {
     // further frame slots (peer contexts sharing the scene): slot 0 is this one
     std::vector<gs_ctx*> peers;
     // slots of gs_render_batch: four streams, one per hardware queue of the
-    // process (orbit 921 frames/s with three, 940 with four, 873 and 901 with
-    // five and six, whose streams share queues)
+    // process (orbit 964 frames/s with two, 1027 with three, 1047 with four,
+    // 981 with five, whose streams share queues)
     static constexpr int kFramesInFlight = 4;
 
     void render(const gs_view* v, void* out, bool out_dev, gs_stats* stats) {
