@@ -282,6 +282,18 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     __shared__ uint32_t s_th[NDIG][256];
     __shared__ uint64_t s_excl;
     const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
+    // The counts and this partition's rank bounds, loaded together (every
+    // caller's bstart holds a word past the grid's last partition, so vid + 1 is
+    // in bounds; a partition past the candidates ignores what it read). Without
+    // compaction the partition is the workgroup's, and they load alongside the
+    // error word below.
+    const int64_t m = m_dev ? min(m_cap, (int64_t)*m_dev) : m_cap;
+    const uint32_t p_pre = p_pre_dev ? min(p_pre_cap, *p_pre_dev) : p_pre_cap;
+    uint32_t b_lo = 0, b_hi = 0;
+    if constexpr (!COMPACT) {
+        b_lo = bstart[blockIdx.x];
+        b_hi = bstart[blockIdx.x + 1];
+    }
     // one thread decides for the workgroup: after an earlier give-up the scan's
     // offsets and owner table may be wrong, so touch nothing
     if (tid == 0) {
@@ -294,14 +306,16 @@ __global__ __launch_bounds__(kEmitThreads) void k_pair_emit(
     __syncthreads();
     const uint32_t vid = s_vid;
     if (vid == 0xFFFFFFFFu) return;
-    const int64_t m = m_dev ? min(m_cap, (int64_t)*m_dev) : m_cap;
-    const uint32_t p_pre = p_pre_dev ? min(p_pre_cap, *p_pre_dev) : p_pre_cap;
+    if constexpr (COMPACT) {
+        b_lo = bstart[vid];
+        b_hi = bstart[vid + 1];
+    }
     const uint32_t nparts = (uint32_t)(((uint64_t)p_pre + kEmitPart - 1) / kEmitPart);
     if (vid >= nparts) return;  // no later partition has work either
     const uint64_t c0 = (uint64_t)vid * kEmitPart;
     const uint64_t c1 = min((uint64_t)p_pre, c0 + kEmitPart);
-    const int64_t rlo = bstart[vid];
-    const int64_t rend = (c1 < (uint64_t)p_pre) ? (int64_t)bstart[vid + 1] + 1 : m;
+    const int64_t rlo = b_lo;
+    const int64_t rend = (c1 < (uint64_t)p_pre) ? (int64_t)b_hi + 1 : m;
     // every rank owns >= 1 candidate, so nr <= kEmitPart + 1; clamp defensively
     const int64_t nr = min(rend - rlo, (int64_t)kEmitPart + 1);
     const TsDiv tsd = ts_div(tp.tile_size);
