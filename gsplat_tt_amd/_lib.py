@@ -34,7 +34,8 @@ EXPORTED = (
     "gs_render_next",
     "gs_render_out_ring", "gs_out_release", "gs_out_ring_config", "gs_out_ring_info",
     "gs_set_chunk_cull",
-    "gs_frame_readback", "gs_set_cull_stats", "gs_set_spin_limit",
+    "gs_frame_readback", "gs_set_cull_stats", "gs_set_spin_limit", "gs_set_graphs",
+    "gs_graph_counts",
     "gs_sort_tile_depth_dev", "gs_last_ranges_ms",
     "gs_sort_tile_depth_noalloc",
 )
@@ -369,6 +370,18 @@ class Context:
         """Per-frame counts of the reference's microblock cull in the stats
         (pairs_dropped_mb, pairs_kept_mb)."""
         _check(self._L.gs_set_cull_stats(self._c, ctypes.c_int(1 if on else 0)))
+
+    def set_graphs(self, on: bool = True):
+        """render_batch frames replayed from captured HIP graphs (on by default)
+        or every kernel enqueued directly; the results are the same."""
+        _check(self._L.gs_set_graphs(self._c, ctypes.c_int(1 if on else 0)))
+
+    def graph_counts(self):
+        """(captures, replays) of frame graphs so far over the frame slots."""
+        c = ctypes.c_int64(0)
+        r = ctypes.c_int64(0)
+        _check(self._L.gs_graph_counts(self._c, ctypes.byref(c), ctypes.byref(r)))
+        return c.value, r.value
 
     def set_spin_limit(self, limit: int = 0):
         """Spin limit of the kernels' bounded look-back waits (0: default); a tiny

@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <climits>
 #include <cmath>
@@ -63,6 +64,10 @@ int guard(F&& f) {
     }
 }
 
+// Bumped by every device (re)allocation of a DevBuf: a captured frame graph
+// holds buffer addresses and is replayed only while this is unchanged.
+std::atomic<uint64_t> g_alloc_gen{0};
+
 struct DevBuf {
     void* p = nullptr;
     size_t cap = 0;
@@ -72,6 +77,7 @@ struct DevBuf {
         size_t want = std::max<size_t>(bytes, 256);
         if (cap > 0) want = std::max(want, cap + cap / 2);
         want = (want + 4095) & ~size_t(4095);
+        ++g_alloc_gen;
         if (p) HIPCHK(hipFree(p));
         p = nullptr;
         cap = 0;
@@ -79,7 +85,10 @@ struct DevBuf {
         cap = want;
     }
     void release() {
-        if (p) (void)hipFree(p);
+        if (p) {
+            ++g_alloc_gen;
+            (void)hipFree(p);
+        }
         p = nullptr;
         cap = 0;
     }
@@ -196,6 +205,9 @@ struct gs_ctx {
     // entry points.
     uint32_t spin_limit = 0;   // 0: the kernels' default (gs_set_spin_limit)
     bool cull_stats = false;   // microblock-cull statistics per frame (gs_set_cull_stats)
+    bool graphs = true;        // batch frames replayed from captured graphs (gs_set_graphs)
+    bool batch_frame = false;  // render_begin is enqueueing a gs_render_batch frame
+    int64_t graph_captures = 0, graph_replays = 0;  // gs_graph_counts
     // Enqueues the reset of a pair of control words (flags 0, spin limit).
     void ctl_reset(uint32_t* ctl) {
         HIPCHK(gs::launch_fill_u32(ctl, 0u, 1, st));
@@ -222,6 +234,7 @@ struct gs_ctx {
     ~gs_ctx() {
         for (gs_ctx* p : peers) delete p;
         if (st) (void)hipStreamSynchronize(st);
+        drop_graph();
         for (DevBuf* b : {&b_mean, &b_cov, &b_opac, &b_col, &b_terms, &b_upload, &b_rc,
                           &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_bstart, &b_pair_tile, &b_pair_id,
                           &b_ranges, &b_out, &b_kalt, &b_valt, &b_hist, &b_state, &b_lb, &b_cnt,
@@ -630,7 +643,7 @@ struct gs_ctx {
     }
 
     void enqueue_attempt() {
-        frame(&pend.v, pend.dout, pend.T, pend.tiles_x, pend.tiles_y);
+        if (!graph_frame()) frame(&pend.v, pend.dout, pend.T, pend.tiles_x, pend.tiles_y);
         if (!pend.out_dev)
             HIPCHK(hipMemcpyAsync(pend.out, pend.dout, pend.bytes, hipMemcpyDeviceToHost, st));
         HIPCHK(hipMemcpyAsync(h_pin, b_frame.p, 64 * 4, hipMemcpyDeviceToHost, st));
@@ -715,6 +728,7 @@ struct gs_ctx {
             p->timing = timing;
             p->spin_limit = spin_limit;
             p->cull_stats = cull_stats;
+            p->graphs = graphs;
             p->sd = sd;
             p->has_opac = has_opac;
             p->skey.valid = true;
@@ -838,7 +852,14 @@ struct gs_ctx {
         for (int i = 0; i < n; ++i) {
             gs_ctx* c = slot(i % S);
             if (i >= S) c->render_end();  // frame i-S used this slot
-            c->render_begin(&views[i], outs[i], out_dev, stats ? &stats[i] : nullptr, true);
+            c->batch_frame = true;
+            try {
+                c->render_begin(&views[i], outs[i], out_dev, stats ? &stats[i] : nullptr, true);
+            } catch (...) {
+                c->batch_frame = false;
+                throw;
+            }
+            c->batch_frame = false;
         }
         for (int i = std::max(0, n - S); i < n; ++i) slot(i % S)->render_end();
     }
@@ -955,6 +976,149 @@ struct gs_ctx {
         return ids_sorted;
     }
 
+    // The projection's parameters for a frame of view v in layout L.
+    gs::ProjParams frame_proj_params(const gs_view* v, const FrameLayout& L, int64_t N,
+                                     int tiles_x, int tiles_y) {
+        gs::ProjParams p = proj_params(v);
+        p.ctl = L.cnt + C_CTL;
+        // depth-sort values carry each Gaussian's tile count
+        p.tiles_x = tiles_x;
+        p.tiles_y = tiles_y;
+        p.tile_size = v->tile_size;
+        p.idx_bits = dval_idx_bits(N);
+        p.dvals = p.idx_bits ? b_tmp_a.as<uint32_t>() : nullptr;
+        return p;
+    }
+
+    // ------------------------------------------------------------ frame graphs
+    // A gs_render_batch frame's kernels (everything frame() enqueues) captured
+    // once per frame slot and shape and replayed for the slot's later frames of
+    // that shape, with the view set on the graph's k_project node: one launch
+    // instead of ~20 per frame (100K-Gaussian orbit 12.9K -> 13.4K frames/s; a
+    // single frame, whose host waits for it, gains nothing and stays direct). A
+    // shape is everything the captured launches depend on besides the view's
+    // camera: the view's other fields, the output, the scene size and SH
+    // degree, the pair capacity, the spin limit, the device buffers (their
+    // allocation generation) and the sort's look-back state — the state-
+    // clearing launches of the passes are baked into the graph, so a graph is
+    // kept only if the frame leaves that state as it found it (a frame's six
+    // passes do, from the second frame of a shape on). Frames with timing,
+    // microblock statistics or the chunk skip, a capacity re-run and sorts of
+    // 2^30 keys or more (epoch-tagged descriptors) are enqueued directly.
+    struct FrameGraph {
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        hipGraphNode_t proj = nullptr;  // null: not replayable (the sort state moved)
+        gs_view shape{};
+        gs::SceneDev sd{};  // the scene's device pointers, held by the projection node
+        void* dout = nullptr;
+        int64_t n = -1, T = -1;
+        int deg = -2;
+        uint64_t pcap = 0, gen = 0;
+        uint32_t spin = 0;
+        int half = 0;
+        uint32_t dirty0 = 0, dirty1 = 0;
+    } fg;
+
+    void drop_graph() {
+        if (fg.exec) (void)hipGraphExecDestroy(fg.exec);
+        if (fg.graph) (void)hipGraphDestroy(fg.graph);
+        fg = FrameGraph{};
+    }
+
+    static bool same_scene(const gs::SceneDev& a, const gs::SceneDev& b) {
+        return a.n == b.n && a.sh_degree == b.sh_degree && a.opac == b.opac && a.sh == b.sh &&
+               a.kfac == b.kfac && a.m2thr == b.m2thr && a.lthr == b.lthr &&
+               a.chunk_box == b.chunk_box && a.chunk_k == b.chunk_k &&
+               std::equal(a.mean, a.mean + 3, b.mean) && std::equal(a.cov, a.cov + 6, b.cov);
+    }
+
+    static gs_view graph_shape(const gs_view* v) {
+        gs_view k = *v;
+        std::memset(k.extrinsics, 0, sizeof(k.extrinsics));
+        std::memset(k.intrinsics, 0, sizeof(k.intrinsics));
+        return k;
+    }
+
+    // Enqueues pend's frame through a graph; false when it must be enqueued
+    // directly (frame()).
+    bool graph_frame() {
+        const int64_t N = sd.n;
+        if (!graphs || !batch_frame || timing || cull_stats || pend.attempt != 0) return false;
+        if (sd.chunk_box != nullptr && pend.v.k_cap <= 3.0f) return false;
+        if (N >= ((int64_t)1 << 30) || pair_cap >= (1ull << 30)) return false;
+        const FrameLayout L = frame_prepare(N, pend.T);  // every allocation before a capture
+        const gs_view shape = graph_shape(&pend.v);
+        const uint64_t gen = g_alloc_gen.load();
+        if (fg.exec != nullptr && fg.proj != nullptr && fg.dout == pend.dout && fg.n == N &&
+            fg.T == pend.T && fg.deg == sd.sh_degree && fg.pcap == pair_cap && fg.gen == gen &&
+            fg.spin == spin_limit && fg.half == sort.half && fg.dirty0 == sort.dirty[0] &&
+            fg.dirty1 == sort.dirty[1] && same_scene(fg.sd, sd) &&
+            std::memcmp(&fg.shape, &shape, sizeof(shape)) == 0) {
+            const gs::ProjParams p = frame_proj_params(&pend.v, L, N, pend.tiles_x, pend.tiles_y);
+            HIPCHK(gs::graph_set_project_params(fg.exec, fg.proj, p));
+            HIPCHK(hipGraphLaunch(fg.exec, st));
+            ++graph_replays;
+            return true;
+        }
+        drop_graph();  // the stream is idle: this slot's last frame was waited for
+        FrameGraph g;
+        g.shape = shape;
+        g.sd = sd;
+        g.dout = pend.dout;
+        g.n = N;
+        g.T = pend.T;
+        g.deg = sd.sh_degree;
+        g.pcap = pair_cap;
+        g.gen = gen;
+        g.spin = spin_limit;
+        g.half = sort.half;
+        g.dirty0 = sort.dirty[0];
+        g.dirty1 = sort.dirty[1];
+        HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        try {
+            frame(&pend.v, pend.dout, pend.T, pend.tiles_x, pend.tiles_y);
+        } catch (...) {
+            hipGraph_t dead = nullptr;
+            (void)hipStreamEndCapture(st, &dead);
+            if (dead) (void)hipGraphDestroy(dead);
+            throw;
+        }
+        HIPCHK(hipStreamEndCapture(st, &g.graph));
+        hipError_t e = hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(g.graph);
+            HIPCHK(e);
+        }
+        fg = g;
+        HIPCHK(hipGraphLaunch(fg.exec, st));  // this frame
+        ++graph_captures;
+        // replayable only from the sort state it was captured in, with the
+        // buffers it captured, and with a projection node to set the view on
+        if (sort.half == g.half && sort.dirty[0] == g.dirty0 && sort.dirty[1] == g.dirty1 &&
+            g_alloc_gen.load() == gen) {
+            size_t nn = 0;
+            HIPCHK(hipGraphGetNodes(fg.graph, nullptr, &nn));
+            std::vector<hipGraphNode_t> nodes(nn);
+            if (nn) HIPCHK(hipGraphGetNodes(fg.graph, nodes.data(), &nn));
+            const void* fn = gs::project_kernel(sd.sh_degree);
+            for (hipGraphNode_t node : nodes) {
+                hipGraphNodeType ty;
+                HIPCHK(hipGraphNodeGetType(node, &ty));
+                if (ty != hipGraphNodeTypeKernel) continue;
+                hipKernelNodeParams kp;
+                HIPCHK(hipGraphKernelNodeGetParams(node, &kp));
+                if (kp.func == fn && kp.kernelParams != nullptr) {
+                    const gs::ProjParams p =
+                        frame_proj_params(&pend.v, L, N, pend.tiles_x, pend.tiles_y);
+                    if (gs::graph_project_args_are(node, sd, p)) fg.proj = node;
+                    break;
+                }
+            }
+        }
+        return true;
+    }
+
     // Enqueues one frame (project -> depth sort -> tile assign -> tile sort ->
     // ranges -> blend) on the stream; no host synchronisation.
     void frame(const gs_view* v, void* dout, int64_t T, int tiles_x, int tiles_y) {
@@ -964,14 +1128,7 @@ struct gs_ctx {
         HIPCHK(gs::launch_fill_u32(L.fr, 0u, L.fwords, st));
         if (spin_limit) HIPCHK(gs::launch_fill_u32(L.cnt + C_CTL + 1, spin_limit, 1, st));
         if (timing) HIPCHK(gs::launch_fill_u32(b_evals.as<uint32_t>(), 0u, 64 * 8 * 2, st));
-        gs::ProjParams p = proj_params(v);
-        p.ctl = L.cnt + C_CTL;
-        // depth-sort values carry each Gaussian's tile count
-        p.tiles_x = tiles_x;
-        p.tiles_y = tiles_y;
-        p.tile_size = v->tile_size;
-        p.idx_bits = dval_idx_bits(N);
-        p.dvals = p.idx_bits ? b_tmp_a.as<uint32_t>() : nullptr;
+        gs::ProjParams p = frame_proj_params(v, L, N, tiles_x, tiles_y);
         // the boxes bound three standard deviations: no skipping for wider k
         if (sd.chunk_box != nullptr && v->k_cap <= 3.0f) {
             b_skip.ensure(gs::project_partitions(N));
@@ -1463,6 +1620,35 @@ int gs_set_cull_stats(gs_ctx* ctx, int on) {
         REQUIRE(ctx, "null ctx");
         ctx->drain_spec();
         ctx->cull_stats = on != 0;
+    });
+}
+
+int gs_set_graphs(gs_ctx* ctx, int on) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
+        ctx->graphs = on != 0;
+        for (gs_ctx* p : ctx->peers) {
+            if (p->pend.active) p->render_end();
+            p->graphs = ctx->graphs;
+            p->drop_graph();
+        }
+        if (ctx->pend.active) ctx->render_end();
+        ctx->drop_graph();
+    });
+}
+
+int gs_graph_counts(gs_ctx* ctx, int64_t* captures, int64_t* replays) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        int64_t c = ctx->graph_captures, r = ctx->graph_replays;
+        for (gs_ctx* p : ctx->peers) {
+            c += p->graph_captures;
+            r += p->graph_replays;
+        }
+        if (captures) *captures = c;
+        if (replays) *replays = r;
     });
 }
 

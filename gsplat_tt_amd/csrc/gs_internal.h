@@ -81,6 +81,14 @@ struct Compact {
 hipError_t launch_project(const SceneDev& s, const ProjParams& p, Compact out,
                           uint8_t* valid_mask, uint64_t* lb_state, uint32_t* ticket,
                           uint32_t* count_out, uint32_t* part_hist, hipStream_t st);
+// Captured frames (HIP graphs): the k_project instance launch_project uses for
+// an SH degree, and an update of a captured k_project node's view parameters
+// in an instantiated graph (the node's other arguments are kept).
+const void* project_kernel(int sh_degree);
+// The captured k_project node's scene and view arguments are s and p (its
+// argument layout is what graph_set_project_params assumes).
+bool graph_project_args_are(hipGraphNode_t node, const SceneDev& s, const ProjParams& p);
+hipError_t graph_set_project_params(hipGraphExec_t exec, hipGraphNode_t node, const ProjParams& p);
 // Chunk frustum skip (render/host/chunk_cull.h): per projection partition of the
 // scene, the box of mean +- k rho, rho = 3 sqrt(trace cov3d), the largest rho and
 // a non-finite flag (8 doubles per partition); per view, the partitions that lie

@@ -477,6 +477,52 @@ hipError_t launch_project(const SceneDev& s, const ProjParams& p, Compact out,
 
 size_t project_partitions(int64_t n) { return (size_t)((n + kProjPart - 1) / kProjPart); }
 
+const void* project_kernel(int sh_degree) {
+    switch (sh_degree) {
+        case -1: return reinterpret_cast<const void*>(&k_project<-1>);
+        case 0: return reinterpret_cast<const void*>(&k_project<0>);
+        case 1: return reinterpret_cast<const void*>(&k_project<1>);
+        case 2: return reinterpret_cast<const void*>(&k_project<2>);
+        case 3: return reinterpret_cast<const void*>(&k_project<3>);
+        default: return nullptr;
+    }
+}
+
+bool graph_project_args_are(hipGraphNode_t node, const SceneDev& s, const ProjParams& p) {
+    hipKernelNodeParams kp;
+    if (hipGraphKernelNodeGetParams(node, &kp) != hipSuccess || kp.kernelParams == nullptr)
+        return false;
+    const SceneDev& a = *static_cast<const SceneDev*>(kp.kernelParams[0]);
+    const ProjParams& b = *static_cast<const ProjParams*>(kp.kernelParams[1]);
+    bool same = a.n == s.n && a.sh_degree == s.sh_degree && a.sh == s.sh && a.opac == s.opac &&
+                a.mean[0] == s.mean[0] && a.cov[5] == s.cov[5] && a.lthr == s.lthr &&
+                b.ctl == p.ctl && b.dvals == p.dvals && b.skip == p.skip && b.fx == p.fx &&
+                b.fy == p.fy && b.width == p.width && b.height == p.height;
+    for (int j = 0; j < 9; ++j) same = same && b.r[j] == p.r[j];
+    for (int j = 0; j < 3; ++j) same = same && b.t[j] == p.t[j];
+    return same;
+}
+
+hipError_t graph_set_project_params(hipGraphExec_t exec, hipGraphNode_t node, const ProjParams& p) {
+    hipKernelNodeParams kp;
+    hipError_t e = hipGraphKernelNodeGetParams(node, &kp);
+    if (e != hipSuccess) return e;
+    if (kp.kernelParams == nullptr) return hipErrorInvalidValue;
+    // the node's arguments as launch_project passed them, the view's replaced
+    SceneDev a0 = *static_cast<const SceneDev*>(kp.kernelParams[0]);
+    ProjParams a1 = p;
+    Compact a2 = *static_cast<const Compact*>(kp.kernelParams[2]);
+    uint8_t* a3 = *static_cast<uint8_t* const*>(kp.kernelParams[3]);
+    uint64_t* a4 = *static_cast<uint64_t* const*>(kp.kernelParams[4]);
+    uint32_t* a5 = *static_cast<uint32_t* const*>(kp.kernelParams[5]);
+    uint32_t* a6 = *static_cast<uint32_t* const*>(kp.kernelParams[6]);
+    uint32_t* a7 = *static_cast<uint32_t* const*>(kp.kernelParams[7]);
+    void* args[8] = {&a0, &a1, &a2, &a3, &a4, &a5, &a6, &a7};
+    kp.kernelParams = args;
+    kp.extra = nullptr;
+    return hipGraphExecKernelNodeSetParams(exec, node, &kp);
+}
+
 size_t chunk_box_doubles(int64_t n) { return project_partitions(n) * 8; }
 
 hipError_t launch_chunk_boxes(const SceneDev& s, double k, double* box, hipStream_t st) {

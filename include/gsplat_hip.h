@@ -144,6 +144,16 @@ int gs_set_cull_stats(gs_ctx* ctx, int on);
  * results; every kernel still exits normally. A tiny limit is for tests of that
  * error path only. */
 int gs_set_spin_limit(gs_ctx* ctx, uint32_t limit);
+/* gs_render_batch frames replayed from HIP graphs (on by default): each frame
+ * slot captures its frame's kernels once per frame shape and replays them for
+ * its later frames of that shape with the new camera (no counterpart in the
+ * reference, whose device path is not HIP; for callers of many small frames,
+ * whose launches cost host time). Results are identical either way; off
+ * enqueues every kernel directly. Completes frames in flight. */
+int gs_set_graphs(gs_ctx* ctx, int on);
+/* Frame graphs captured and replayed so far by the context's frame slots (no
+ * counterpart in the reference; for tests and tuning of gs_set_graphs). */
+int gs_graph_counts(gs_ctx* ctx, int64_t* captures, int64_t* replays);
 
 /* Chunk frustum skip (render/host/chunk_cull.h; GSPLAT_TT_CHUNK_CULL and
  * GSPLAT_TT_CHUNK_K of render/host/pfwc_device.cpp:214-240): per scene, the box of
