@@ -1018,6 +1018,7 @@ struct gs_ctx {
         uint32_t spin = 0;
         int half = 0;
         uint32_t dirty0 = 0, dirty1 = 0;
+        int misses = 0;  // captures of this shape in a row that were not replayable
     } fg;
 
     void drop_graph() {
@@ -1050,19 +1051,26 @@ struct gs_ctx {
         const FrameLayout L = frame_prepare(N, pend.T);  // every allocation before a capture
         const gs_view shape = graph_shape(&pend.v);
         const uint64_t gen = g_alloc_gen.load();
-        if (fg.exec != nullptr && fg.proj != nullptr && fg.dout == pend.dout && fg.n == N &&
-            fg.T == pend.T && fg.deg == sd.sh_degree && fg.pcap == pair_cap && fg.gen == gen &&
-            fg.spin == spin_limit && fg.half == sort.half && fg.dirty0 == sort.dirty[0] &&
-            fg.dirty1 == sort.dirty[1] && same_scene(fg.sd, sd) &&
-            std::memcmp(&fg.shape, &shape, sizeof(shape)) == 0) {
+        const bool same_shape = fg.dout == pend.dout && fg.n == N && fg.T == pend.T &&
+                                fg.deg == sd.sh_degree && fg.pcap == pair_cap && fg.gen == gen &&
+                                fg.spin == spin_limit && same_scene(fg.sd, sd) &&
+                                std::memcmp(&fg.shape, &shape, sizeof(shape)) == 0;
+        // a shape whose frames never leave the sort state as they found it (an
+        // odd pass count flips its half every frame: above 2^16 tiles the tile
+        // sort has three passes) is enqueued directly after two such captures
+        if (same_shape && fg.proj == nullptr && fg.misses >= 2) return false;
+        if (fg.exec != nullptr && fg.proj != nullptr && same_shape && fg.half == sort.half &&
+            fg.dirty0 == sort.dirty[0] && fg.dirty1 == sort.dirty[1]) {
             const gs::ProjParams p = frame_proj_params(&pend.v, L, N, pend.tiles_x, pend.tiles_y);
             HIPCHK(gs::graph_set_project_params(fg.exec, fg.proj, p));
             HIPCHK(hipGraphLaunch(fg.exec, st));
             ++graph_replays;
             return true;
         }
+        const int misses = same_shape && fg.proj == nullptr ? fg.misses : 0;
         drop_graph();  // the stream is idle: this slot's last frame was waited for
         FrameGraph g;
+        g.misses = misses;
         g.shape = shape;
         g.sd = sd;
         g.dout = pend.dout;
@@ -1095,6 +1103,7 @@ struct gs_ctx {
         ++graph_captures;
         // replayable only from the sort state it was captured in, with the
         // buffers it captured, and with a projection node to set the view on
+        ++fg.misses;  // until a projection node is found below
         if (sort.half == g.half && sort.dirty[0] == g.dirty0 && sort.dirty[1] == g.dirty1 &&
             g_alloc_gen.load() == gen) {
             size_t nn = 0;
@@ -1111,7 +1120,10 @@ struct gs_ctx {
                 if (kp.func == fn && kp.kernelParams != nullptr) {
                     const gs::ProjParams p =
                         frame_proj_params(&pend.v, L, N, pend.tiles_x, pend.tiles_y);
-                    if (gs::graph_project_args_are(node, sd, p)) fg.proj = node;
+                    if (gs::graph_project_args_are(node, sd, p)) {
+                        fg.proj = node;
+                        fg.misses = 0;
+                    }
                     break;
                 }
             }

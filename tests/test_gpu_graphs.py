@@ -165,3 +165,30 @@ def test_graph_shape_changes(orbit):
         if out is not None:
             ctx.dev_free(out)
         ctx.close()
+
+
+def test_graph_odd_pass_count_goes_direct():
+    """A 4160x4200 frame of 68380 tiles sorts its tiles in three passes, so a
+    frame flips the sort's look-back half and never leaves its state as it
+    found it: after two captures that cannot be replayed its frames are
+    enqueued directly, and every frame equals the direct one."""
+    H, W = 4160, 4200
+    scene, cams = scenes.config1(seed=31, n=4_000)
+    K = scenes.intrinsics(500 * W / 640, 500 * W / 640, W / 2, H / 2)
+    view = L.make_view(cams[0].w2c, K, H, W, tile_size=16, output="bf16")
+    ctx = L.Context(0, timing=False)
+    out = None
+    try:
+        ctx.set_scene(scene.means, O.cov3d(scene.scales, scene.quats), scene.opacities,
+                      scene.colors)
+        ref = _direct(ctx, [view])[0]
+        out = ctx.dev_alloc(ref[0].nbytes)
+        for f in range(5):
+            _check(_batch1(ctx, view, ref[0], out), ref, f"frame {f}")
+        caps, reps = ctx.graph_counts()
+        print("graphs captured", caps, "replayed", reps, flush=True)
+        assert caps == 2 and reps == 0, (caps, reps)
+    finally:
+        if out is not None:
+            ctx.dev_free(out)
+        ctx.close()
