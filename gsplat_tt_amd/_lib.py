@@ -34,7 +34,8 @@ EXPORTED = (
     "gs_render_next",
     "gs_render_out_ring", "gs_out_release", "gs_out_ring_config", "gs_out_ring_info",
     "gs_set_chunk_cull",
-    "gs_frame_readback", "gs_set_cull_stats", "gs_set_spin_limit", "gs_set_graphs",
+    "gs_frame_readback", "gs_frame_readback_info", "gs_set_cull_stats", "gs_set_spin_limit",
+    "gs_set_graphs",
     "gs_graph_counts",
     "gs_sort_tile_depth_dev", "gs_last_ranges_ms",
     "gs_sort_tile_depth_noalloc",
@@ -101,7 +102,8 @@ class GsTrainStats(ctypes.Structure):
                 ("step", ctypes.c_int64), ("loss", ctypes.c_double),
                 ("ms_forward", ctypes.c_float), ("ms_backward", ctypes.c_float),
                 ("ms_adam", ctypes.c_float), ("ms_total", ctypes.c_float),
-                ("l1", ctypes.c_double), ("ssim", ctypes.c_double)]
+                ("l1", ctypes.c_double), ("ssim", ctypes.c_double),
+                ("pairs_pre", ctypes.c_int64), ("pair_capacity", ctypes.c_int64)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
@@ -225,7 +227,6 @@ class Context:
             _check(self._L.gs_set_timing(self._c, 1))
         self._keep = None
         self._version = 0
-        self._last_tiles = 0
 
     def close(self):
         if self._c:
@@ -275,8 +276,6 @@ class Context:
             out = np.empty((H, W, 3), _OUT_DTYPE[view.out_format])
         st = GsStats()
         _check(self._L.gs_render(self._c, ctypes.byref(view), _ptr(out), 0, ctypes.byref(st)))
-        ts = view.tile_size
-        self._last_tiles = ((W + ts - 1) // ts) * ((H + ts - 1) // ts)
         return out, st.as_dict()
 
     def train_loss(self, image, target, lambda_dssim=0.2, loss_scale=1.0):
@@ -347,15 +346,15 @@ class Context:
         return [st.as_dict() for st in sts]
 
     def frame_readback(self, ids=True, ranges=True):
-        """The last render()'s frame: dict(M, pairs_pre, P, sorted_ids int64 (P,),
-        tile_ranges int64 (T, 2)) - the tile-sorted compact ids and the tile
-        ranges of the frame path itself (gs_frame_readback)."""
-        cnt = np.zeros(3, np.int64)
-        _check(self._L.gs_frame_readback(self._c, _ptr(cnt), None, ctypes.c_int64(0), None,
-                                         ctypes.c_int64(0)))
-        M, ppre, P = (int(x) for x in cnt)
-        out = dict(M=M, pairs_pre=ppre, P=P)
-        T = self._last_tiles
+        """The frame held by the context's first slot (the last render(), or after
+        render_batch the last view i with i % 4 == 0): dict(M, pairs_pre, P, T,
+        batch_index, replayed, sorted_ids int64 (P,), tile_ranges int64 (T, 2)) -
+        the tile-sorted compact ids and the tile ranges of the frame path itself
+        (gs_frame_readback, sized by gs_frame_readback_info)."""
+        info = np.zeros(6, np.int64)
+        _check(self._L.gs_frame_readback_info(self._c, _ptr(info)))
+        M, ppre, P, T, bi, rep = (int(x) for x in info)
+        out = dict(M=M, pairs_pre=ppre, P=P, T=T, batch_index=bi, replayed=bool(rep))
         sid = np.empty(max(P, 1), np.int64) if ids else None
         rg = np.empty((T, 2), np.int64) if ranges else None
         _check(self._L.gs_frame_readback(self._c, None, _ptr(sid), ctypes.c_int64(P if ids else 0),
@@ -406,8 +405,6 @@ class Context:
         st = GsStats()
         _check(self._L.gs_render(self._c, ctypes.byref(view), ctypes.c_void_p(dev_out_ptr), 1,
                                  ctypes.byref(st)))
-        ts = view.tile_size
-        self._last_tiles = ((view.image_width + ts - 1) // ts) * ((view.image_height + ts - 1) // ts)
         return st.as_dict()
 
     # ---- stages (host arrays)

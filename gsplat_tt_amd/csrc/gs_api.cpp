@@ -64,9 +64,6 @@ int guard(F&& f) {
     }
 }
 
-// Bumped by every device (re)allocation of a DevBuf: a captured frame graph
-// holds buffer addresses and is replayed only while this is unchanged.
-std::atomic<uint64_t> g_alloc_gen{0};
 
 struct DevBuf {
     void* p = nullptr;
@@ -77,7 +74,6 @@ struct DevBuf {
         size_t want = std::max<size_t>(bytes, 256);
         if (cap > 0) want = std::max(want, cap + cap / 2);
         want = (want + 4095) & ~size_t(4095);
-        ++g_alloc_gen;
         if (p) HIPCHK(hipFree(p));
         p = nullptr;
         cap = 0;
@@ -85,10 +81,7 @@ struct DevBuf {
         cap = want;
     }
     void release() {
-        if (p) {
-            ++g_alloc_gen;
-            (void)hipFree(p);
-        }
+        if (p) (void)hipFree(p);
         p = nullptr;
         cap = 0;
     }
@@ -230,6 +223,8 @@ struct gs_ctx {
     bool rb_valid = false, rb_empty = false;
     uint32_t* rb_ids = nullptr;
     int64_t rb_T = 0, rb_M = 0, rb_ppre = 0, rb_P = 0;
+    int64_t rb_batch = -1;     // its index in the last gs_render_batch (-1: another call)
+    bool rb_replayed = false;  // it was replayed from a captured graph
 
     ~gs_ctx() {
         for (gs_ctx* p : peers) delete p;
@@ -577,6 +572,8 @@ struct gs_ctx {
         size_t bytes = 0;
         int64_t T = 0;
         int tiles_x = 0, tiles_y = 0, attempt = 0;
+        int64_t batch_index = -1;  // index in the gs_render_batch call (-1: another call)
+        bool replayed = false;     // the last attempt replayed a captured graph
         gs_stats* stats = nullptr;
         std::chrono::steady_clock::time_point t0;
     } pend;
@@ -643,6 +640,7 @@ struct gs_ctx {
     }
 
     void enqueue_attempt() {
+        pend.replayed = false;
         if (!graph_frame()) frame(&pend.v, pend.dout, pend.T, pend.tiles_x, pend.tiles_y);
         if (!pend.out_dev)
             HIPCHK(hipMemcpyAsync(pend.out, pend.dout, pend.bytes, hipMemcpyDeviceToHost, st));
@@ -700,6 +698,8 @@ struct gs_ctx {
         rb_valid = true;
         rb_empty = pend.empty;
         rb_T = pend.T;
+        rb_batch = pend.batch_index;
+        rb_replayed = pend.replayed;
         rb_M = pend.empty ? 0 : (int64_t)h_pin[C_M];
         rb_ppre = pend.empty ? 0 : (int64_t)h_pin[C_PPRE];
         rb_P = pend.empty ? 0 : (int64_t)h_pin[C_P];
@@ -860,6 +860,7 @@ struct gs_ctx {
                 throw;
             }
             c->batch_frame = false;
+            c->pend.batch_index = i;
         }
         for (int i = std::max(0, n - S); i < n; ++i) slot(i % S)->render_end();
     }
@@ -949,13 +950,14 @@ struct gs_ctx {
         const int dw = gs::sort_digit_width(tile_bits(T));
         HIPCHK(gs::launch_reduce_rows(b_phist_emit.as<uint32_t>(), hcols, (uint32_t)L.eparts,
                                       cnt + C_PPRE, L.pcap, gs::kEmitPartition, dw,
-                                      fr + kFrTileHist, st, b_pchunk.as<uint32_t>()));
+                                      fr + kFrTileHist, st, b_pchunk.as<uint32_t>(),
+                                      cnt + C_CTL));
         // the first tile pass's output positions per partition, from the emit
         // rows (four emit partitions per sort partition): no look-back
         HIPCHK(gs::launch_part_offsets(b_phist_emit.as<uint32_t>(), hcols, (uint32_t)L.eparts,
                                        cnt + C_PPRE, L.pcap, gs::kEmitPartition, kEmitPerSort,
                                        dw, b_pchunk.as<uint32_t>(), fr + kFrTileHist,
-                                       b_poffs.as<uint32_t>(), st));
+                                       b_poffs.as<uint32_t>(), st, cnt + C_CTL));
         record(3);
         // stable tile sort of the depth-ordered candidate slots; its first pass
         // drops the culled ones (kPairDrop), so the kept pairs come out compact
@@ -998,11 +1000,13 @@ struct gs_ctx {
     // single frame, whose host waits for it, gains nothing and stays direct). A
     // shape is everything the captured launches depend on besides the view's
     // camera: the view's other fields, the output, the scene size and SH
-    // degree, the pair capacity, the spin limit, the device buffers (their
-    // allocation generation) and the sort's look-back state — the state-
+    // degree, the pair capacity, the spin limit, the slot's device buffers
+    // (their addresses) and the sort's look-back state — the state-
     // clearing launches of the passes are baked into the graph, so a graph is
     // kept only if the frame leaves that state as it found it (a frame's six
-    // passes do, from the second frame of a shape on). Frames with timing,
+    // passes do from the second frame of a shape on; the first frame's capture
+    // is redone from the state it leaves, so a slot replays from its second
+    // frame). Frames with timing,
     // microblock statistics or the chunk skip, a capacity re-run and sorts of
     // 2^30 keys or more (epoch-tagged descriptors) are enqueued directly.
     struct FrameGraph {
@@ -1041,6 +1045,22 @@ struct gs_ctx {
         return k;
     }
 
+    // The addresses of this slot's frame buffers: a captured frame graph holds
+    // them and is replayed only while none moved (the scene planes and opacity
+    // terms, which a slot shares with the first one, are compared through the
+    // scene descriptor; another slot's allocations do not matter).
+    uint64_t buffers_key() const {
+        uint64_t h = 1469598103934665603ull;
+        for (const DevBuf* b : {&b_rc, &b_dkey, &b_brec, &b_src, &b_tmp_a, &b_offs, &b_bstart,
+                                &b_pair_tile, &b_pair_id, &b_ranges, &b_phist_proj, &b_phist_emit,
+                                &b_pchunk, &b_poffs, &b_frame, &b_kalt, &b_valt, &b_hist,
+                                &b_state, &b_out}) {
+            h ^= (uint64_t)(uintptr_t)b->p;
+            h *= 1099511628211ull;
+        }
+        return h;
+    }
+
     // Enqueues pend's frame through a graph; false when it must be enqueued
     // directly (frame()).
     bool graph_frame() {
@@ -1050,7 +1070,7 @@ struct gs_ctx {
         if (N >= ((int64_t)1 << 30) || pair_cap >= (1ull << 30)) return false;
         const FrameLayout L = frame_prepare(N, pend.T);  // every allocation before a capture
         const gs_view shape = graph_shape(&pend.v);
-        const uint64_t gen = g_alloc_gen.load();
+        const uint64_t gen = buffers_key();
         const bool same_shape = fg.dout == pend.dout && fg.n == N && fg.T == pend.T &&
                                 fg.deg == sd.sh_degree && fg.pcap == pair_cap && fg.gen == gen &&
                                 fg.spin == spin_limit && same_scene(fg.sd, sd) &&
@@ -1065,6 +1085,7 @@ struct gs_ctx {
             HIPCHK(gs::graph_set_project_params(fg.exec, fg.proj, p));
             HIPCHK(hipGraphLaunch(fg.exec, st));
             ++graph_replays;
+            pend.replayed = true;
             return true;
         }
         const int misses = same_shape && fg.proj == nullptr ? fg.misses : 0;
@@ -1083,16 +1104,36 @@ struct gs_ctx {
         g.half = sort.half;
         g.dirty0 = sort.dirty[0];
         g.dirty1 = sort.dirty[1];
-        HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-        try {
-            frame(&pend.v, pend.dout, pend.T, pend.tiles_x, pend.tiles_y);
-        } catch (...) {
-            hipGraph_t dead = nullptr;
-            (void)hipStreamEndCapture(st, &dead);
-            if (dead) (void)hipGraphDestroy(dead);
-            throw;
+        auto capture = [&](hipGraph_t* out) {
+            HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+            try {
+                frame(&pend.v, pend.dout, pend.T, pend.tiles_x, pend.tiles_y);
+            } catch (...) {
+                hipGraph_t dead = nullptr;
+                (void)hipStreamEndCapture(st, &dead);
+                if (dead) (void)hipGraphDestroy(dead);
+                throw;
+            }
+            HIPCHK(hipStreamEndCapture(st, out));
+        };
+        capture(&g.graph);
+        if ((sort.half != g.half || sort.dirty[0] != g.dirty0 || sort.dirty[1] != g.dirty1) &&
+            buffers_key() == gen) {
+            // The frame moved the sort's look-back bookkeeping (a slot's first
+            // frame of a shape leaves more rows marked than it found). The
+            // graph is dropped unlaunched, the whole descriptor buffer is
+            // cleared directly (a clean buffer is within any marking), and the
+            // frame is captured again from the moved bookkeeping, which a
+            // steady shape's frames leave as they find it: the slot replays
+            // from its next frame on instead of capturing twice.
+            (void)hipGraphDestroy(g.graph);
+            g.graph = nullptr;
+            HIPCHK(gs::launch_fill_u32(b_state.as<uint32_t>(), 0u, b_state.cap / 4, st));
+            g.half = sort.half;
+            g.dirty0 = sort.dirty[0];
+            g.dirty1 = sort.dirty[1];
+            capture(&g.graph);
         }
-        HIPCHK(hipStreamEndCapture(st, &g.graph));
         hipError_t e = hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0);
         if (e != hipSuccess) {
             (void)hipGraphDestroy(g.graph);
@@ -1105,7 +1146,7 @@ struct gs_ctx {
         // buffers it captured, and with a projection node to set the view on
         ++fg.misses;  // until a projection node is found below
         if (sort.half == g.half && sort.dirty[0] == g.dirty0 && sort.dirty[1] == g.dirty1 &&
-            g_alloc_gen.load() == gen) {
+            buffers_key() == gen) {
             size_t nn = 0;
             HIPCHK(hipGraphGetNodes(fg.graph, nullptr, &nn));
             std::vector<hipGraphNode_t> nodes(nn);
@@ -1153,7 +1194,8 @@ struct gs_ctx {
         HIPCHK(gs::launch_project(sd, p, c, nullptr, L.lb_proj, L.cnt + C_PROJ_TICKET,
                                   L.cnt + C_M, b_phist_proj.as<uint32_t>(), st));
         HIPCHK(gs::launch_reduce_rows(b_phist_proj.as<uint32_t>(), 1024, (uint32_t)L.pparts,
-                                      nullptr, 0, 0, 0, L.fr + kFrDepthHist, st));
+                                      nullptr, 0, 0, 0, L.fr + kFrDepthHist, st, nullptr,
+                                      L.cnt + C_CTL));
         record(1);
         gs::TileParams tp{tiles_x, tiles_y, v->tile_size, v->cull_disabled ? 0 : 1,
                           L.cnt + C_CTL, p.idx_bits};
@@ -1186,7 +1228,7 @@ struct gs_ctx {
         bool grads_valid = false;
         int H = 0, W = 0, tiles_x = 0, tiles_y = 0;
         gs::TrainCam cam{};
-        uint32_t M = 0, P = 0;
+        uint32_t M = 0, P = 0, p_pre = 0;
         uint32_t* ids = nullptr;  // tile-sorted compact ids of the last forward
         double loss = 0.0, l1 = 0.0, ssim = 0.0;
     } tr;
@@ -1367,7 +1409,8 @@ struct gs_ctx {
                                         L.cnt + C_PROJ_TICKET, L.cnt + C_M,
                                         b_phist_proj.as<uint32_t>(), dbg, st));
         HIPCHK(gs::launch_reduce_rows(b_phist_proj.as<uint32_t>(), 1024, (uint32_t)L.pparts,
-                                      nullptr, 0, 0, 0, L.fr + kFrDepthHist, st));
+                                      nullptr, 0, 0, 0, L.fr + kFrDepthHist, st, nullptr,
+                                      L.cnt + C_CTL));
         gs::TileParams tp{tr.tiles_x, tr.tiles_y, 16, 1, L.cnt + C_CTL};
         tr.ids = frame_tiles(L, std::max<int64_t>(N, 1), T, tp, nullptr);
         gs::TrainFwdParams fp{};
@@ -1419,15 +1462,21 @@ struct gs_ctx {
             HIPCHK(hipMemcpyAsync(h_pin, b_frame.p, 64 * 4, hipMemcpyDeviceToHost, st));
             HIPCHK(hipMemcpyAsync(h_pin + 64, t_loss.p, 16, hipMemcpyDeviceToHost, st));
             sync();
-            ctl_check(h_pin[C_CTL], "train forward");
+            // The capacity test comes first: an attempt past the capacity has
+            // kErrCapacity raised by the count scan, and is re-run (its fill
+            // clears the word) rather than reported.
             const uint32_t p_pre = h_pin[C_PPRE];
             if (p_pre == 0xFFFFFFFFu)
                 throw GsError(GS_E_CAPACITY, "train: more than 2^32-1 candidate pairs");
-            if (p_pre <= pair_cap) break;
+            if (p_pre <= pair_cap) {
+                ctl_check(h_pin[C_CTL], "train forward");
+                break;
+            }
             REQUIRE(attempt == 0, "train: pair capacity did not converge");
             pair_cap = std::min<uint64_t>(0xFFFFFFFFull, (uint64_t)p_pre + p_pre / 8 + 4096);
         }
         tr.M = h_pin[C_M];
+        tr.p_pre = h_pin[C_PPRE];
         tr.P = h_pin[C_P];
         double sums[2];
         std::memcpy(sums, h_pin + 64, 16);
@@ -1504,6 +1553,8 @@ struct gs_ctx {
         o.loss = tr.loss;
         o.l1 = tr.l1;
         o.ssim = tr.ssim;
+        o.pairs_pre = tr.p_pre;
+        o.pair_capacity = (int64_t)pair_cap;
         if (timing) {
             float ms = 0.0f;
             if (fwd && hipEventElapsedTime(&ms, tev[0], tev[1]) == hipSuccess) o.ms_forward = ms;
@@ -1624,6 +1675,20 @@ int gs_frame_readback(gs_ctx* ctx, int64_t* counts, int64_t* sorted_ids, int64_t
         for (size_t i = 0; i < ids.size(); ++i) sorted_ids[i] = ids[i];
         if (tile_ranges)
             for (int64_t i = 0; i < T * 2; ++i) tile_ranges[i] = rg.empty() ? 0 : rg[(size_t)i];
+    });
+}
+
+int gs_frame_readback_info(gs_ctx* ctx, int64_t* info) {
+    return guard([&] {
+        REQUIRE(ctx && info, "null argument");
+        REQUIRE(ctx->rb_valid, "frame_readback_info: no frame to read (or a later call reused "
+                               "its buffers)");
+        info[0] = ctx->rb_M;
+        info[1] = ctx->rb_ppre;
+        info[2] = ctx->rb_P;
+        info[3] = ctx->rb_T;
+        info[4] = ctx->rb_batch;
+        info[5] = ctx->rb_replayed ? 1 : 0;
     });
 }
 

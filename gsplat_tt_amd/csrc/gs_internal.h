@@ -249,11 +249,12 @@ hipError_t launch_tile_bounds64(const uint64_t* sorted_keys, uint32_t p, uint32_
 // with dig_w > 0 the columns are digit rows of 2^dig_w words and column c adds
 // into out[(c >> dig_w) * 256 + (c & (2^dig_w - 1))].
 // chunk_out (optional, reduce_chunks(rows_cap) x cols words): the column sums
-// of each workgroup's rows, for launch_part_offsets.
+// of each workgroup's rows, for launch_part_offsets. ctl (optional): the
+// kernel does nothing when an upstream kernel raised an error flag there.
 hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,
                               const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
                               int dig_w, uint32_t* out, hipStream_t st,
-                              uint32_t* chunk_out = nullptr);
+                              uint32_t* chunk_out = nullptr, const uint32_t* ctl = nullptr);
 size_t reduce_chunks(uint32_t rows_cap);
 // After launch_reduce_rows with chunk_out over the same rows: per partition of
 // rows_per_part rows and per digit d < 2^dig_w (columns 0 .. 2^dig_w - 1 of a
@@ -261,10 +262,12 @@ size_t reduce_chunks(uint32_t rows_cap);
 // part[e][d] over rows e < s * rows_per_part): the output position of the
 // partition's first key of digit d in a sort pass over those keys (hist: that
 // pass's digit histogram). ceil(rows in use / rows_per_part) << dig_w words.
+// Nothing is done when an upstream kernel raised an error flag in ctl.
 hipError_t launch_part_offsets(const uint32_t* part, int cols, uint32_t rows_cap,
                                const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
                                int rows_per_part, int dig_w, const uint32_t* chunks,
-                               const uint32_t* hist, uint32_t* offs, hipStream_t st);
+                               const uint32_t* hist, uint32_t* offs, hipStream_t st,
+                               const uint32_t* ctl = nullptr);
 constexpr uint32_t kEmitPartition = 2048;   // candidates per emit partition
 constexpr uint32_t kProjPartition = 2048;   // Gaussians per project partition
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t st);

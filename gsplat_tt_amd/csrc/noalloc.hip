@@ -1,6 +1,9 @@
 // noalloc.hip - the standalone tile/depth sort with its per-tile ranges, with no
-// device or host allocation: for callers that cannot allocate (code under HIP
-// graph capture, tight serving loops, harnesses that forbid hipMalloc).
+// device or host allocation: for callers that cannot allocate (tight serving
+// loops, harnesses that forbid hipMalloc). It is not capturable into a HIP
+// graph: it reads the error word back and waits for the stream, and its host
+// bookkeeping of the look-back halves advances per call. A call on a stream
+// that is capturing is refused (GS_E_INVALID) before anything is enqueued.
 //
 // Every scratch buffer of gs_sort_tile_depth_dev (the ping-pong key and value
 // arrays, the look-back descriptors, the digit histograms and tickets, the
@@ -104,6 +107,13 @@ extern "C" int gs_sort_tile_depth_noalloc(gs_ctx* ctx, uint64_t* keys, uint32_t*
         return fail(GS_E_INVALID, "sort_tile_depth_noalloc: device index out of range");
     hipError_t e = hipSetDevice(ci.device);
     if (e != hipSuccess) return fail(GS_E_DEVICE, std::string("hipSetDevice: ") + hipGetErrorString(e));
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(ci.stream, &cap);
+    if (e != hipSuccess)
+        return fail(GS_E_DEVICE, std::string("hipStreamIsCapturing: ") + hipGetErrorString(e));
+    if (cap != hipStreamCaptureStatusNone)
+        return fail(GS_E_INVALID, "sort_tile_depth_noalloc: the context's stream is capturing a "
+                                  "graph; this call waits for the stream and cannot be captured");
     std::call_once(g_once[ci.device], init_device, ci.device, ci.stream);
     if (g_init_err[ci.device] != hipSuccess)
         return fail(GS_E_DEVICE, std::string("sort_tile_depth_noalloc: scratch set-up: ") +
@@ -114,8 +124,7 @@ extern "C" int gs_sort_tile_depth_noalloc(gs_ctx* ctx, uint64_t* keys, uint32_t*
     const int end_bit = 32 + tile_bits_of(num_tiles);
     const int npass = (end_bit + 7) / 8;
     uint32_t* tickets = tmp.hist + (size_t)8 * 256;
-    // histograms, tickets and control words start at zero (a fill kernel, not a
-    // memset, so the call can sit in a captured graph)
+    // histograms, tickets and control words start at zero
     e = launch_fill_u32(tmp.hist, 0u, kHistWords, st);
     if (e == hipSuccess) e = launch_fill_u32(tmp.ctl, 0u, 2, st);
     void* kf = keys;

@@ -28,10 +28,7 @@ namespace {
 constexpr int kWaves = 4;  // waves of the 256-thread histogram / scan blocks
 constexpr int kHistThreads = 256;
 constexpr int kMaxPasses = 8;
-#ifndef GS_LB_BATCH
-#define GS_LB_BATCH 4
-#endif
-constexpr int kLbBatch = GS_LB_BATCH;  // predecessors read per look-back round trip
+constexpr int kLbBatch = 4;  // predecessors read per look-back round trip
 
 // descriptor: [63:34] epoch, [33:32] flag (1 aggregate, 2 inclusive), [31:0] value
 __device__ __forceinline__ uint64_t make_desc(uint32_t epoch, uint32_t flag, uint32_t v) {

@@ -576,14 +576,16 @@ __device__ __forceinline__ uint32_t rows_in_use(uint32_t rows_cap, const uint32_
 // sums with one atomic per column (few workgroups, so little contention on the
 // atomics). chunk_out (optional): workgroup b also stores its column sums at
 // chunk_out[b * cols + c], zeros included (workgroups past the rows in use
-// store nothing).
+// store nothing). After an upstream failure (ctl) nothing is read or written:
+// the rows may not have been written by this frame.
 constexpr int kRedThreads = 1024;
 constexpr uint32_t kRedBlocks = 96;  // workgroups for the largest row count
 __global__ __launch_bounds__(kRedThreads) void k_reduce_rows(
     const uint32_t* __restrict__ part, int cols, uint32_t rows_cap, uint32_t span,
     const uint32_t* __restrict__ count_dev, uint32_t count_cap, uint32_t per_row, int dig_w,
-    uint32_t* __restrict__ out, uint32_t* __restrict__ chunk_out) {
+    uint32_t* __restrict__ out, uint32_t* __restrict__ chunk_out, const uint32_t* ctl) {
     __shared__ uint4 s_acc[kRedThreads];
+    if (upstream_failed(ctl)) return;  // uniform over the workgroup
     const uint32_t rows = rows_in_use(rows_cap, count_dev, count_cap, per_row);
     const uint32_t r0 = blockIdx.x * span;
     if (r0 >= rows) return;  // uniform over the workgroup
@@ -635,15 +637,17 @@ __global__ __launch_bounds__(kRedThreads) void k_reduce_rows(
 // before it. Thread (d, g): digit d, g-th contiguous run of the chunk's
 // partitions; the runs' sums are scanned in LDS, then each thread writes its
 // partitions' offsets. No look-back: every workgroup reads only sums that the
-// reduce finished before this kernel started.
+// reduce finished before this kernel started. Nothing is done after an
+// upstream failure (ctl).
 constexpr int kOffsThreads = 1024;
 __global__ __launch_bounds__(kOffsThreads) void k_part_offsets(
     const uint32_t* __restrict__ part, int cols, uint32_t rows_cap, uint32_t span,
     const uint32_t* __restrict__ count_dev, uint32_t count_cap, uint32_t per_row,
     int rows_per_part, int dig_w, const uint32_t* __restrict__ chunks,
-    const uint32_t* __restrict__ hist, uint32_t* __restrict__ offs) {
+    const uint32_t* __restrict__ hist, uint32_t* __restrict__ offs, const uint32_t* ctl) {
     __shared__ uint32_t s_base[256];
     __shared__ uint32_t s_run[kOffsThreads];
+    if (upstream_failed(ctl)) return;  // uniform over the workgroup
     const uint32_t rows = rows_in_use(rows_cap, count_dev, count_cap, per_row);
     const uint32_t r0 = blockIdx.x * span;
     if (r0 >= rows) return;  // uniform over the workgroup
@@ -864,21 +868,23 @@ size_t reduce_chunks(uint32_t rows_cap) {
 
 hipError_t launch_reduce_rows(const uint32_t* part, int cols, uint32_t rows_cap,
                               const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
-                              int dig_w, uint32_t* out, hipStream_t st, uint32_t* chunk_out) {
+                              int dig_w, uint32_t* out, hipStream_t st, uint32_t* chunk_out,
+                              const uint32_t* ctl) {
     if (rows_cap == 0) return hipSuccess;
     if (cols <= 0 || cols % 4 != 0 || kRedThreads % (cols / 4) != 0) return hipErrorInvalidValue;
     const uint32_t span = reduce_span(rows_cap);
     const unsigned grid = (rows_cap + span - 1) / span;
     if (dig_w < 0 || dig_w > 8) return hipErrorInvalidValue;
     k_reduce_rows<<<grid, kRedThreads, 0, st>>>(part, cols, rows_cap, span, count_dev,
-                                                count_cap, per_row, dig_w, out, chunk_out);
+                                                count_cap, per_row, dig_w, out, chunk_out, ctl);
     return hipGetLastError();
 }
 
 hipError_t launch_part_offsets(const uint32_t* part, int cols, uint32_t rows_cap,
                                const uint32_t* count_dev, uint32_t count_cap, uint32_t per_row,
                                int rows_per_part, int dig_w, const uint32_t* chunks,
-                               const uint32_t* hist, uint32_t* offs, hipStream_t st) {
+                               const uint32_t* hist, uint32_t* offs, hipStream_t st,
+                               const uint32_t* ctl) {
     if (rows_cap == 0) return hipSuccess;
     const uint32_t span = reduce_span(rows_cap);
     if (dig_w < 0 || dig_w > 8 || (1 << dig_w) > cols || rows_per_part <= 0 ||
@@ -887,7 +893,7 @@ hipError_t launch_part_offsets(const uint32_t* part, int cols, uint32_t rows_cap
     const unsigned grid = (rows_cap + span - 1) / span;
     k_part_offsets<<<grid, kOffsThreads, 0, st>>>(part, cols, rows_cap, span, count_dev,
                                                   count_cap, per_row, rows_per_part, dig_w,
-                                                  chunks, hist, offs);
+                                                  chunks, hist, offs, ctl);
     return hipGetLastError();
 }
 

@@ -123,7 +123,7 @@ int gs_render_batch(gs_ctx* ctx, const gs_view* views, int n, void* const* outs,
 int gs_render_next(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device,
                    const gs_view* next_view, gs_stats* stats);
 
-/* The last gs_render frame of this context, read back for parity checks (the
+/* The last frame of this context's first slot, read back for parity checks (the
  * SortResult of src/gsplat_cpu/sort.cpp:146-165,217-257 after the frame's
  * tile_assign, backends/cpu_cpp/pybind_module.cpp:1149-1575). counts (3):
  * M, candidate pairs before the per-pair cull, P. sorted_ids (ids_cap >= P):
@@ -131,9 +131,16 @@ int gs_render_next(gs_ctx* ctx, const gs_view* view, void* out, int out_on_devic
  * in source order, the reference's m), stable by (tile, depth bits, id).
  * tile_ranges (num_tiles x 2, num_tiles = the frame's tile count): [start,
  * end), (0, 0) for empty tiles. Any NULL output is skipped. GS_E_INVALID when
- * no frame is held (a later call reused the frame buffers). */
+ * no frame is held (a later call reused the frame buffers). After
+ * gs_render_batch the held frame is the last one of the context's first slot
+ * (views i with i % 4 == 0); gs_frame_readback_info says which. */
 int gs_frame_readback(gs_ctx* ctx, int64_t* counts, int64_t* sorted_ids, int64_t ids_cap,
                       int64_t* tile_ranges, int64_t num_tiles);
+/* No counterpart in the reference: what gs_frame_readback would read. info (6):
+ * M, candidate pairs, P, the frame's tile count, its index in the last
+ * gs_render_batch (-1 when another call rendered it), 1 when it was replayed
+ * from a captured graph. GS_E_INVALID when no frame is held. */
+int gs_frame_readback_info(gs_ctx* ctx, int64_t* info);
 /* Per-frame counts of the reference's microblock cull (gs_stats.pairs_dropped_mb,
  * pairs_kept_mb; cull_and_blend.cpp:384-504,835-836): one more pass over the
  * frame's pairs after the blend, off by default. */
@@ -242,8 +249,10 @@ int gs_sort_tile_depth_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t 
  * call when timing is on (0 otherwise). */
 float gs_last_ranges_ms(gs_ctx* ctx);
 /* gs_sort_tile_depth_dev with no allocation of any kind. It has no counterpart
- * in the reference: it is for callers that cannot allocate (code under HIP
- * graph capture, tight serving loops, harnesses that forbid hipMalloc). Its
+ * in the reference: it is for callers that cannot allocate (tight serving
+ * loops, harnesses that forbid hipMalloc). It waits for the context's stream
+ * (the error word is read back), so it cannot sit under HIP graph capture: a
+ * call while the stream is capturing returns GS_E_INVALID, nothing done. Its
  * scratch (ping-pong keys and values, look-back descriptors, digit histograms,
  * control words) is one file-scope device array of 12.5 MiB per GPU, held
  * until the process ends, so n is at most 2^20 keys (larger n: GS_E_CAPACITY,
@@ -299,6 +308,8 @@ typedef struct gs_train_stats {
     float ms_total;         /* host wall clock of the call */
     double l1;              /* mean |image - target| */
     double ssim;            /* mean SSIM (computed when lambda_dssim > 0) */
+    int64_t pairs_pre;      /* candidate tile-Gaussian pairs before the cull */
+    int64_t pair_capacity;  /* candidate-pair capacity after the call (grown on overflow) */
 } gs_train_stats;
 
 /* Gaussian-indexed projection values of the last forward (parity tests). */

@@ -9,7 +9,10 @@ ranges bit-exact (src/gsplat_cpu/tile_assign.cpp:121-349, sort.cpp:146-165,
 
   * 100K Gaussians at 640x480 (RGB, fp32 out);
   * 1M Gaussians at 1280x720, SH degree 3, bf16 out;
-  * two views of the 64-view orbit of the 6M-Gaussian scene at 1237x822;
+  * two views of the 64-view orbit of the 6M-Gaussian scene at 1237x822 (bf16
+    and f32), and eight views through the benchmark's path (gs_render_batch,
+    four frame slots replaying captured graphs) against directly enqueued
+    frames and, for one replayed frame, the reference's ids and ranges;
   * the 50M-key tile/depth sort with its per-tile ranges, against numpy's
     stable argsort;
   * the 1M-Gaussian SH-1 training step at 1280x720 through size-independent
@@ -112,6 +115,9 @@ def c3_scene():
 
 @pytest.mark.parametrize("view_index", [0, 21])
 def test_c3_6m_orbit_view_frame(gpu_ctx, c3_scene, view_index):
+    """Two orbit views of the 6M scene: bf16 (the benchmark's output) within the
+    stated tolerance and f32 within 1e-5 of the reference's render_full, with the
+    frame's ids and ranges bit-exact."""
     print(f"C3 6M orbit view {view_index}", flush=True)
     scene, cams, cov = c3_scene
     cam = cams[view_index]
@@ -119,11 +125,67 @@ def test_c3_6m_orbit_view_frame(gpu_ctx, c3_scene, view_index):
     ref = F.frame(scene.means, cov, scene.opacities, rgb, cam, 16)
     assert 20_000_000 <= ref["P"] <= 40_000_000, ref["P"]  # the scene's stated pair load
     gpu_ctx.set_scene(scene.means, cov, scene.opacities, scene.sh, sh_degree=3)
-    view = L.make_view(cam.w2c, cam.K, cam.height, cam.width, tile_size=16, output="bf16")
-    img, st = gpu_ctx.render(view)
-    rb = F.check_frame(gpu_ctx, view, ref, img, st, bf16=True, label=f"C3 view {view_index}")
+    for out in ("bf16", "f32"):
+        view = L.make_view(cam.w2c, cam.K, cam.height, cam.width, tile_size=16, output=out)
+        img, st = gpu_ctx.render(view)
+        rb = F.check_frame(gpu_ctx, view, ref, img, st, bf16=out == "bf16",
+                           label=f"C3 view {view_index} {out}")
     heaviest = int((rb["tile_ranges"][:, 1] - rb["tile_ranges"][:, 0]).max())
     print(f"C3 view {view_index}: heaviest tile {heaviest} pairs", flush=True)
+
+
+def test_c3_6m_orbit_batch_graph_replay(c3_scene):
+    """The benchmark's timed path at its size: eight orbit views of the 6M scene
+    through gs_render_batch (four frame slots, graphs on, timing off: the
+    benchmark's settings), three passes: each slot captures its first frame
+    once and replays every later one. Every frame's bf16 image and counts equal
+    the same view rendered with every kernel enqueued directly; the frame held
+    by the first slot after the last pass (a replayed graph) has the
+    reference's tile-sorted ids and tile ranges (tile_assign.cpp:121-349,
+    sort.cpp:146-165)."""
+    scene, cams, cov = c3_scene
+    idx = list(range(0, 64, 8))
+    print(f"C3 6M batch graph replay: views {idx}", flush=True)
+    ctx = L.Context(0, timing=False)
+    outs = []
+    try:
+        ctx.set_scene(scene.means, cov, scene.opacities, scene.sh, sh_degree=3)
+        views = [L.make_view(cams[i].w2c, cams[i].K, cams[i].height, cams[i].width,
+                             tile_size=16, output="bf16") for i in idx]
+        ctx.set_graphs(False)
+        ref = [ctx.render(v) for v in views]
+        ctx.set_graphs(True)
+        # one output buffer per frame slot, as the benchmark has (slot k of a
+        # four-view call renders view k into outs[k])
+        outs = [ctx.dev_alloc(ref[0][0].nbytes) for _ in range(4)]
+        img = np.empty_like(ref[0][0])
+        for rep in range(3):
+            for j in (0, 4):
+                sts = ctx.render_batch(views[j:j + 4], outs)
+                for k, (st, o) in enumerate(zip(sts, outs)):
+                    ctx.d2h(img, o)
+                    assert np.array_equal(img, ref[j + k][0]), (rep, j + k)
+                    for key in ("num_visible", "pairs_pre", "num_entries"):
+                        assert st[key] == ref[j + k][1][key], (rep, j + k, key)
+            caps, reps = ctx.graph_counts()
+            print(f"pass {rep}: frames equal to direct; graphs captured {caps} replayed {reps}",
+                  flush=True)
+            # one capture per slot (its first frame), every later frame replayed
+            assert (caps, reps) == (4, 4 + 8 * rep), (rep, caps, reps)
+        rb = ctx.frame_readback()  # slot 0's last frame: views[4]
+        assert rb["batch_index"] == 0 and rb["replayed"]
+    finally:
+        for o in outs:
+            ctx.dev_free(o)
+        ctx.close()
+    cam = cams[idx[4]]
+    rgb = O.sh_rgb(scene.means, scene.sh, 3, cam.w2c)
+    oref = F.frame(scene.means, cov, scene.opacities, rgb, cam, 16, want_image=False)
+    print(f"replayed view {idx[4]}: M={rb['M']} pre={rb['pairs_pre']} P={rb['P']} "
+          f"(oracle {oref['M']} {oref['pairs_pre']} {oref['P']})", flush=True)
+    assert (rb["M"], rb["pairs_pre"], rb["P"]) == (oref["M"], oref["pairs_pre"], oref["P"])
+    assert np.array_equal(rb["tile_ranges"], oref["tile_ranges"])
+    assert np.array_equal(rb["sorted_ids"], oref["sorted_ids"])
 
 
 def test_c4_50m_key_sort_with_tile_ranges(gpu_ctx):

@@ -193,3 +193,62 @@ def test_train_step_ssim_loss_matches_oracle(gpu_ctx):
         moved = np.abs(out[k][0] - params[k]).max()
         print(k, "max diff", d, "moved", moved)
         assert d <= 1e-2 * max(moved, 1e-12) + 1e-6, k
+
+
+
+def test_train_pair_capacity_retry():
+    """A first training forward whose candidate pairs exceed the context's
+    starting capacity (max(2^20, 8N)): 4000 large, faint Gaussians at 320x240
+    (300 tiles) give about 1.19M candidates. The forward grows the capacity and
+    re-runs: its image and loss equal the oracle's, and its backward equals the
+    backward of the same forward run again at the grown capacity (no re-run).
+    (The oracle blends every pixel for every Gaussian, so its cost is at least
+    256 x 2^20 pixel evaluations: its backward is left to the smaller cases.)"""
+    print("train pair-capacity retry", flush=True)
+    rng = np.random.default_rng(61)
+    n, H, W = 4000, 240, 320
+    z = rng.uniform(4.0, 6.0, n)
+    params = {
+        "means": np.stack([rng.uniform(-1.2, 1.2, n) * z / 4.0,
+                           rng.uniform(-0.9, 0.9, n) * z / 4.0, z], -1).astype(np.float32),
+        "log_scales": rng.normal(np.log(2.2), 0.1, (n, 3)).astype(np.float32),
+        "quats": rng.normal(0, 1, (n, 4)).astype(np.float32),
+        "opacity_logits": rng.normal(-3.5, 0.3, n).astype(np.float32),
+        "sh": rng.uniform(-0.5, 0.5, (n, 1, 3)).astype(np.float32),
+    }
+    target = rng.uniform(0.0, 1.0, (H, W, 3)).astype(np.float32)
+    w2c = np.eye(4, dtype=np.float32)
+    K = scenes.intrinsics(250.0, 250.0, W / 2, H / 2)
+    cfg = L.make_train_cfg()
+    view = L.make_view(w2c, K, H, W, tile_size=16)
+    ctx = L.Context(0)  # a fresh context: the capacity starts at the default
+    try:
+        tr = L.Trainer(ctx, params, 0)
+        img, T, _, st = tr.forward(view, cfg, target)
+        print(f"pairs_pre {st['pairs_pre']} capacity {st['pair_capacity']} "
+              f"P {st['num_entries']}", flush=True)
+        assert st["pairs_pre"] > (1 << 20)
+        assert st["pair_capacity"] >= st["pairs_pre"]
+        tr.backward(cfg)
+        g_retry = tr.read(3)
+        cap = st["pair_capacity"]
+        img2, _, _, st2 = tr.forward(view, cfg, target)
+        assert st2["pair_capacity"] == cap and st2["pairs_pre"] == st["pairs_pre"]
+        assert np.array_equal(img2, img) and st2["loss"] == st["loss"]
+        tr.backward(cfg)
+        g_direct = tr.read(3)
+    finally:
+        ctx.close()
+    for k in TO.PARAM_NAMES:
+        # atomics add in another order: equal up to fp32 summation order
+        e = rel_err(g_retry[k], g_direct[k])
+        d = float(np.abs(g_retry[k] - g_direct[k]).max() / np.abs(g_direct[k]).max())
+        print("grad", k, "retry vs direct: rel", e, "max-normalised", d)
+        assert e < 1e-2 and d < 1e-4, k
+    cfg_o = TO.Cfg(sh_degree=0)
+    _, img_o, T_o, _, _ = TO.forward(params, w2c, K, H, W, cfg_o)
+    loss_o, _ = TO.l1_loss_grad(img_o, target)
+    d = float(np.abs(img - img_o).max())
+    print(f"image max_abs {d:.3g}; loss gpu {st['loss']:.7f} oracle {loss_o:.7f}", flush=True)
+    assert d < 1e-4 and float(np.abs(T - T_o).max()) < 1e-4
+    assert abs(st["loss"] - loss_o) <= 1e-4 * loss_o
