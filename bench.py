@@ -104,7 +104,7 @@ def bench_frames(args):
     dt = time.perf_counter() - t0
     log(f"timed {args.steps} frames in {dt:.3f}s")
     _check = L._check
-    _check(ctx._L.gs_set_timing(ctx.handle, 1))
+    _check(ctx._L.gs_set_timing(ctx.handle, 2))  # stage events + blend counters
     stats = [ctx.render_dev(views[i % len(views)], outs[0]) for i in range(16)]
     for o in outs:
         ctx.dev_free(o)
@@ -320,6 +320,46 @@ def bench_host_out(ctx, cams, frames):
     return res
 
 
+def bench_render_view(scene, cov, cams, frames):
+    """The drop-in call itself: render_clean.render_view over the orbit with the
+    module's defaults (u8 zero-copy images from its pinned output ring) and the
+    next view announced (next_extrinsics), the scene passed as host arrays on
+    every call as render/run.py does (a scene-cache hit after the first call).
+    PCIe-inclusive, through the module's own context; not the headline value.
+    Also the module's host spans per view (stage_timings: head, frame, tail)."""
+    import gsplat_tt_amd
+
+    rc = gsplat_tt_amd.render_clean_module()
+    H, W = cams[0].height, cams[0].width
+    args = (scene.means, cov, scene.opacities, scene.sh)
+    kw = dict(image_height=H, image_width=W, tile_size=16, min_opacity=1.0 / 255.0,
+              contrib_floor=1.0 / 16384.0, mb_contrib_floor=1.0 / 16384.0,
+              cull_disabled=False, transmittance_threshold=1.0 / 255.0, max_radius=0,
+              k_cap=3.0, use_isoellipse=False)
+
+    def run(first, count):
+        for i in range(first, first + count):
+            c, nx = cams[i % len(cams)], cams[(i + 1) % len(cams)]
+            img, _ = rc.render_view(*args, c.w2c, c.K, **kw, next_extrinsics=nx.w2c)
+            del img
+
+    try:
+        run(0, 8)  # scene upload, ring buffers, the first frames
+        rc.reset_stage_timings()
+        t0 = time.perf_counter()
+        run(8, frames)
+        dt = time.perf_counter() - t0
+        t = rc.stage_timings()
+    finally:
+        rc.device_shutdown()
+    n = max(int(t["views"]), 1)
+    return {"format": "u8", "zero_copy": True, "next_extrinsics": True, "frames": frames,
+            "frames_per_s": round(frames / dt, 1),
+            "host_ms_per_view": {k: round(t[k] / n, 4) for k in ("head", "frame", "tail",
+                                                                 "view_total")},
+            "xview_hits": int(t["xview_hits"])}
+
+
 def bench_view(ctx, name, tag, scene, cam, steps, warmup, cpu_frames, cpu_threads, out="bf16"):
     """One workload's single view, rendered `steps` times through gs_render_batch
     (four frames in flight), then 8 frames one at a time with per-stage events;
@@ -341,7 +381,7 @@ def bench_view(ctx, name, tag, scene, cam, steps, warmup, cpu_frames, cpu_thread
     ctx.render_batch([view] * steps, [outs[i % FRAMES_IN_FLIGHT] for i in range(steps)])
     ctx._L.gs_sync(ctx.handle)
     dt = time.perf_counter() - t0
-    L._check(ctx._L.gs_set_timing(ctx.handle, 1))
+    L._check(ctx._L.gs_set_timing(ctx.handle, 2))  # stage events + blend counters
     stats = [ctx.render_dev(view, outs[0]) for _ in range(8)]
     for o in outs:
         ctx.dev_free(o)
@@ -360,11 +400,12 @@ def bench_view(ctx, name, tag, scene, cam, steps, warmup, cpu_frames, cpu_thread
     return res
 
 
-def bench_sort(ctx, n, tiles=5000):
+def bench_sort(ctx, n, tiles=5000, cpu_threads=0, cpu=True):
     """The 50M-key tile/depth sort with its per-tile ranges (gs_sort_tile_depth_dev):
     wall time from the host around the call (inputs restored outside it), the
     bytes model keys*(24*passes + 8) over that wall time, the onesweep passes'
-    own event times, and the range extraction's."""
+    own event times, and the range extraction's; then the reference's CPU sort
+    of the same keys (cpu_baseline)."""
     from gsplat_tt_amd import scenes
 
     t = time.time()
@@ -404,6 +445,8 @@ def bench_sort(ctx, n, tiles=5000):
     ok = ok and int(rg[:, 1].max()) == n and int((rg[:, 1] - rg[:, 0]).astype(np.int64).sum()) == n
     for p in (dk, dv, dr):
         ctx.dev_free(p)
+    cpu_res = cpu_sort_baseline(keys, vo, cpu_threads) if cpu else None
+    del ko, vo
     best = min(times[1:])
     kernel_ms = float(np.mean([sum(p) for p in pass_ms]))
     per_pass_ms = float(np.mean([np.mean(p) for p in pass_ms if p]))
@@ -424,6 +467,7 @@ def bench_sort(ctx, n, tiles=5000):
                                   "achieved": round(n * 24 / (per_pass_ms * 1e-3) / 1e9, 1),
                                   "frac": round(n * 24 / (per_pass_ms * 1e-3) / 1e9
                                                 / HBM_PEAK_GBS, 4)}},
+        "cpu_baseline": cpu_res,
     }
 
 
@@ -467,12 +511,24 @@ def bench_train(ctx, n, steps):
     for _ in range(steps):
         stats_s.append(tr.step(view, cfg_s, dt, target_on_device=True))
     el_s = time.perf_counter() - t1
+    # the L1 steps again with the moments stored as bf16 (the reference's
+    # device step default): Adam moves 4 B less per moment
+    tr.set_moments(True)
+    tr.step(view, cfg, dt, target_on_device=True)
+    stats_b = []
+    t2 = time.perf_counter()
+    for _ in range(steps):
+        stats_b.append(tr.step(view, cfg, dt, target_on_device=True))
+    el_b = time.perf_counter() - t2
+    tr.set_moments(False)
     ctx.dev_free(dt)
     keys = ("ms_forward", "ms_backward", "ms_adam")
     avg = {k: float(np.mean([s[k] for s in stats])) for k in keys}
     avg_s = {k: float(np.mean([s[k] for s in stats_s])) for k in keys}
+    avg_b = {k: float(np.mean([s[k] for s in stats_b])) for k in keys}
     planes = 11 + 3 * 4
     adam_bytes = visible * planes * 28
+    adam_bytes_b = visible * planes * 20
     P = stats[-1]["num_entries"]
     bwd_bytes = P * 48 + stats[-1]["num_blendable"] * 9 * 4 * 2
     return {"workload": "training step, 1M Gaussians (64-component mixture), SH degree 1, "
@@ -500,7 +556,18 @@ def bench_train(ctx, n, steps):
                           "steps_per_s": round(steps / el_s, 2),
                           "ms": {k[3:]: round(v, 4) for k, v in avg_s.items()},
                           "ssim_last": round(stats_s[-1]["ssim"], 6),
-                          "loss_last": round(stats_s[-1]["loss"], 6)}}
+                          "loss_last": round(stats_s[-1]["loss"], 6)},
+            "bf16_moments": {"ms_per_step": round(el_b / steps * 1e3, 4),
+                             "steps_per_s": round(steps / el_b, 2),
+                             "ms": {k[3:]: round(v, 4) for k, v in avg_b.items()},
+                             "adam_roofline": {
+                                 "bound": "hbm", "bytes": adam_bytes_b,
+                                 "achieved": round(adam_bytes_b / (avg_b["ms_adam"] * 1e-3)
+                                                   / 1e9, 1),
+                                 "frac": round(adam_bytes_b / (avg_b["ms_adam"] * 1e-3) / 1e9
+                                               / HBM_PEAK_GBS, 4),
+                                 "model": "visible rows x 23 planes x (12 B read + 8 B write)"},
+                             "loss_last": round(stats_b[-1]["loss"], 6)}}
 
 
 def cpu_info():
@@ -547,7 +614,7 @@ def cpu_baseline(scene, cov, cams, frames, threads, sample):
 
     R = O.ref_module()
     kind = "reference" if R is not None else "port"
-    times = []
+    times, stages = [], []
     for i in range(frames + 1):
         cam = cams[(i * 7) % len(cams)]
         t0 = time.perf_counter()
@@ -555,24 +622,72 @@ def cpu_baseline(scene, cov, cams, frames, threads, sample):
             rgb = sh_rgb_parallel(O, scene.means, scene.sh, scene.sh_degree, cam.w2c, threads)
         else:
             rgb = scene.colors
+        t1 = time.perf_counter()
         if R is not None:
-            R.render_full(scene.means, cov, scene.opacities, rgb, cam.w2c, cam.K, cam.height,
-                          cam.width, tile_size=16)
+            _, st = R.render_full(scene.means, cov, scene.opacities, rgb, cam.w2c, cam.K,
+                                  cam.height, cam.width, tile_size=16)
         else:
-            O.render_full(scene.means, cov, scene.opacities, rgb, cam.w2c, cam.K, cam.height,
-                          cam.width, tile_size=16)
+            _, st, _ = O.render_full(scene.means, cov, scene.opacities, rgb, cam.w2c, cam.K,
+                                     cam.height, cam.width, tile_size=16)
         dt = time.perf_counter() - t0
         if i > 0:
             times.append(dt)
+            st = dict(st)
+            st["sh_ms"] = (t1 - t0) * 1e3
+            stages.append(st)
     med = float(np.median(times))
-    log(f"cpu baseline ({sample}): {med * 1e3:.0f} ms/frame on {threads} threads")
+    # the reference's own per-stage wall times (render_full's stats dict,
+    # pybind_module.cpp:1537-1566), medians over the sample
+    split = {k: round(float(np.median([float(s.get(k, 0.0)) for s in stages])), 3)
+             for k in ("sh_ms", "project_ms", "tile_assign_ms", "sort_ms", "cull_ms",
+                       "blend_ms", "total_ms")}
+    log(f"cpu baseline ({sample}): {med * 1e3:.0f} ms/frame on {threads} threads; {split}")
     return {"value": round(1.0 / med, 4), "unit": "frames/s",
             "cores": threads if kind == "reference" else 1, "kind": kind,
             "nproc": info["nproc"], "os_cpu_count": info["os_cpu_count"],
-            "cpu_model": info["model"],
+            "cpu_model": info["model"], "stages_ms": split,
             "sample": f"{sample}: median {med * 1e3:.1f} ms/frame (SH colour + render_full, "
                       f"16x16 tiles, {threads} threads; the box's share of one GPU is "
                       f"{BOX_CPU_SHARE} threads)"}
+
+
+def cpu_sort_baseline(keys, vals_gpu, threads, reps=3):
+    """The reference's own stable bin-and-radix sort (_gsplat_cpu.sort, i.e.
+    sort_and_bin of src/gsplat_cpu/sort.cpp:89-263, compiled from its sources into
+    oracle/_ref) on the same 50M keys: gaussian id = key index, tile id = the
+    key's high word, depth = the fp32 of its low word; its sorted ids are the
+    stable order of the keys. `reps` timed calls after one warm-up, median, on
+    `threads` threads; the result is checked against the GPU's sorted values."""
+    info = cpu_info()
+    if threads <= 0:
+        threads = max(1, min(info["nproc"], BOX_CPU_SHARE))
+    os.environ["GSPLAT_TT_NUM_THREADS"] = str(threads)
+    from oracle import oracle as O
+
+    R = O.ref_module()
+    if R is None:
+        return None
+    n = keys.shape[0]
+    tiles = int(keys.max() >> np.uint64(32)) + 1
+    gids = np.arange(n, dtype=np.int64)
+    tids = (keys >> np.uint64(32)).astype(np.int64)
+    depths = (keys & np.uint64(0xFFFFFFFF)).astype(np.uint32).view(np.float32)
+    times = []
+    sid = None
+    for i in range(reps + 1):
+        t0 = time.perf_counter()
+        sid, _ = R.sort(gids, tids, depths, tiles, 1)
+        if i > 0:
+            times.append(time.perf_counter() - t0)
+    same = bool(np.array_equal(np.asarray(sid), vals_gpu.astype(np.int64)))
+    med = float(np.median(times))
+    log(f"cpu sort baseline: {med * 1e3:.0f} ms for {n} keys on {threads} threads "
+        f"(equal to the GPU order: {same})")
+    return {"value": round(n / med / 1e9, 4), "unit": "Gkeys/s", "cores": threads,
+            "kind": "reference", "nproc": info["nproc"], "os_cpu_count": info["os_cpu_count"],
+            "cpu_model": info["model"], "equal_to_gpu": same,
+            "sample": f"the {n}-key sort, {reps} calls after 1 warm-up: median "
+                      f"{med * 1e3:.1f} ms (_gsplat_cpu.sort, {threads} threads)"}
 
 
 def main():
@@ -590,7 +705,7 @@ def main():
     if args.sort_only:
         from gsplat_tt_amd import _lib as L
         ctx = L.Context(0, timing=False)
-        print(json.dumps({"sort": bench_sort(ctx, args.sort_keys)}), flush=True)
+        print(json.dumps({"sort": bench_sort(ctx, args.sort_keys, cpu=False)}), flush=True)
         ctx.close()
         return
     ctx, scene, cov, cams, stats, dt = bench_frames(args)
@@ -618,6 +733,8 @@ def main():
     }
     res["host_out"] = bench_host_out(ctx, cams, min(args.steps, 64))
     log(f"host_out: {res['host_out']}")
+    res["render_view"] = bench_render_view(scene, cov, cams, min(args.steps, 64))
+    log(f"render_view: {res['render_view']}")
     if not args.no_morton:
         res["morton_chunk_cull"] = bench_morton(scene, cov, cams, args.steps, args.warmup)
         log(f"morton_chunk_cull: {res['morton_chunk_cull']}")
@@ -637,7 +754,8 @@ def main():
                                   0 if args.no_cpu else 3, args.cpu_threads, out="bf16")
         del s1, s2
     if not args.no_sort:
-        res["sort"] = bench_sort(ctx, args.sort_keys)
+        res["sort"] = bench_sort(ctx, args.sort_keys, cpu_threads=args.cpu_threads,
+                                 cpu=not args.no_cpu)
         log(f"sort: {res['sort']}")
     if not args.no_train:
         res["train"] = bench_train(ctx, args.train_n, args.train_steps)

@@ -28,6 +28,7 @@ EXPORTED = (
     "gs_dev_free", "gs_memcpy_h2d", "gs_memcpy_d2h", "gs_memcpy_d2d", "gs_sync",
     "gs_train_init", "gs_train_read", "gs_train_write", "gs_train_set_step",
     "gs_train_set_visible", "gs_train_forward", "gs_train_backward", "gs_train_adam",
+    "gs_train_set_moments",
     "gs_train_step",
     "gs_train_loss",
     "gs_render_batch",
@@ -219,12 +220,14 @@ class _LeasedImage:
 class Context:
     """One GPU context (device + stream + resident scene)."""
 
-    def __init__(self, device: int = 0, timing: bool = False):
+    def __init__(self, device: int = 0, timing: int = 0):
+        """timing: 0 off, 1 (or True) per-stage hipEvent times in the stats, 2 also
+        the blend's evaluation counters (gs_set_timing)."""
         self._L = load_library()
         self._c = ctypes.c_void_p()
         _check(self._L.gs_create(int(device), ctypes.byref(self._c)))
         if timing:
-            _check(self._L.gs_set_timing(self._c, 1))
+            _check(self._L.gs_set_timing(self._c, int(timing)))
         self._keep = None
         self._version = 0
 
@@ -579,6 +582,11 @@ class Trainer:
     def set_visible(self, visible):
         v = np.ascontiguousarray(np.asarray(visible, bool).astype(np.uint8))
         _check(self._L.gs_train_set_visible(self.ctx.handle, _ptr(v)))
+
+    def set_moments(self, bf16: bool):
+        """Adam moments stored as bf16 (round to nearest even) or fp32 (default);
+        the stored moments are carried over."""
+        _check(self._L.gs_train_set_moments(self.ctx.handle, ctypes.c_int(1 if bf16 else 0)))
 
     def forward(self, view: GsView, cfg: GsTrainCfg, target=None, want_proj=False):
         H, W = view.image_height, view.image_width

@@ -53,8 +53,11 @@ class HipBackend:
     """The reference's `Backend` (gsplat/backend.py:40) on one GPU.
 
     Constructor keywords are those of CpuCppBackend (backends/cpu_cpp/backend.py:
-    24-40) plus `device` (GPU index) and `tile_size` (16 or 32; the reference's
-    fused path uses 32)."""
+    24-40) plus `device` (GPU index), `tile_size` (16 or 32; the reference's
+    fused path uses 32) and `cull_stats`: render_fused's microblock-cull counts
+    (pairs_dropped, pairs_kept_per_mb) take one more pass over the frame's pairs
+    (k_mb_stats), so they are collected only when asked for; without them those
+    two keys are left out of the stats (the reference's pipeline then reads 0)."""
 
     name = NAME
 
@@ -63,7 +66,8 @@ class HipBackend:
                  cull_disabled: bool = False, transmittance_threshold: float = 1.0 / 255.0,
                  min_opacity: float = 1.0 / 255.0, max_radius: int = 0,
                  contrib_floor: float | None = None, k_cap: float = 3.0,
-                 use_isoellipse: bool = False, device: int = 0, tile_size: int = 32):
+                 use_isoellipse: bool = False, device: int = 0, tile_size: int = 32,
+                 cull_stats: bool = False):
         if tile_size not in (16, 32):
             raise ValueError("tile_size must be 16 or 32")
         self.verbose = verbose
@@ -79,9 +83,12 @@ class HipBackend:
         self.k_cap = float(k_cap)
         self.use_isoellipse = bool(use_isoellipse)
         self.tile_size = int(tile_size)
-        self.ctx = L.Context(device, timing=True)  # raises without library / GPU
-        # render_fused reports the microblock cull's pairs_dropped / pairs_kept_per_mb
-        self.ctx.set_cull_stats(True)
+        # per-stage device times (hipEvents) for render_fused's *_ms keys; raises
+        # without the library or a GPU
+        self.ctx = L.Context(device, timing=True)
+        self.cull_stats = bool(cull_stats)
+        if self.cull_stats:
+            self.ctx.set_cull_stats(True)
         self._cov_key = None
         self._cov = None
 
@@ -193,8 +200,8 @@ class HipBackend:
                      use_isoellipse: bool = False):
         """backends/cpu_cpp/backend.py:319-380: one call from the Gaussians to the
         (H,W,3) float32 image and a stats dict (project_ms, tile_assign_ms,
-        sort_ms, cull_ms, blend_ms, total_ms, num_visible, num_entries, pairs_in,
-        pairs_dropped, pairs_kept_per_mb). `gaussians` has means, scales,
+        sort_ms, cull_ms, blend_ms, total_ms, num_visible, num_entries, pairs_in, and
+        with cull_stats pairs_dropped, pairs_kept_per_mb). `gaussians` has means, scales,
         rotations, opacities and colors (N,3) RGB. As in the reference, the
         contrib_floor / k_cap / use_isoellipse arguments of this call are not
         read: the constructor's settings apply (the per-pair floor is the
@@ -214,9 +221,10 @@ class HipBackend:
                  "tile_assign_ms": st["ms_tile_assign"], "sort_ms": st["ms_tile_sort"],
                  "cull_ms": 0.0, "blend_ms": st["ms_blend"], "total_ms": st["ms_total"],
                  "num_visible": int(st["num_visible"]), "num_entries": int(st["num_entries"]),
-                 "pairs_in": int(st["num_entries"]),
-                 "pairs_dropped": int(st["pairs_dropped_mb"]),
-                 "pairs_kept_per_mb": int(st["pairs_kept_mb"])}
+                 "pairs_in": int(st["num_entries"])}
+        if self.cull_stats:
+            stats["pairs_dropped"] = int(st["pairs_dropped_mb"])
+            stats["pairs_kept_per_mb"] = int(st["pairs_kept_mb"])
         return img, stats
 
     def close(self) -> None:

@@ -52,11 +52,6 @@ __device__ __forceinline__ float exp4(float x) {
     return __builtin_amdgcn_ldexpf(p, n);
 }
 
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
-    uint32_t u = __float_as_uint(x);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-}
 
 // u8 of a bf16 colour, uint8(float32(clip(float32(b), 0, 1)) * 255) with
 // truncation, in integer form: a bf16 in [0, 1) is (128 + m) 2^(e - 134), so

@@ -157,7 +157,8 @@ int dval_idx_bits(int64_t n) {
 struct gs_ctx {
     int device = 0;
     hipStream_t st = nullptr;
-    bool timing = false;
+    bool timing = false;        // per-stage hipEvents (gs_set_timing >= 1)
+    bool blend_counts = false;  // the blend's evaluation counters (gs_set_timing 2)
     hipEvent_t ev[12] = {};
     hipEvent_t sort_ev[16] = {};
     int last_sort_passes = 0;
@@ -645,7 +646,7 @@ struct gs_ctx {
         if (!pend.out_dev)
             HIPCHK(hipMemcpyAsync(pend.out, pend.dout, pend.bytes, hipMemcpyDeviceToHost, st));
         HIPCHK(hipMemcpyAsync(h_pin, b_frame.p, 64 * 4, hipMemcpyDeviceToHost, st));
-        if (timing)
+        if (blend_counts)
             HIPCHK(hipMemcpyAsync(h_evals.data(), b_evals.p, 64 * 8 * 8, hipMemcpyDeviceToHost, st));
     }
 
@@ -690,8 +691,8 @@ struct gs_ctx {
                 s.ms_tile_assign = elapsed(2, 3);
                 s.ms_tile_sort = elapsed(3, 4);
                 s.ms_blend = elapsed(4, 5);
-                blend_diag(s);
             }
+            if (blend_counts) blend_diag(s);
         }
         s.ms_total = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() -
                                                                pend.t0).count();
@@ -726,6 +727,7 @@ struct gs_ctx {
         }
         for (gs_ctx* p : peers) {
             p->timing = timing;
+            p->blend_counts = blend_counts;
             p->spin_limit = spin_limit;
             p->cull_stats = cull_stats;
             p->graphs = graphs;
@@ -904,7 +906,7 @@ struct gs_ctx {
         L.fwords = kFrLb + lb_words + (size_t)T;
         b_frame.ensure(L.fwords * 4);
         ensure_sort(std::max<int64_t>(N, L.pcap), 4);
-        if (timing) b_evals.ensure(64 * 8 * 8);
+        if (blend_counts) b_evals.ensure(64 * 8 * 8);
         L.fr = b_frame.as<uint32_t>();
         L.lb_proj = reinterpret_cast<uint64_t*>(L.fr + kFrLb);
         L.lb_rect = L.lb_proj + L.pparts;
@@ -1065,7 +1067,8 @@ struct gs_ctx {
     // directly (frame()).
     bool graph_frame() {
         const int64_t N = sd.n;
-        if (!graphs || !batch_frame || timing || cull_stats || pend.attempt != 0) return false;
+        if (!graphs || !batch_frame || timing || blend_counts || cull_stats || pend.attempt != 0)
+            return false;
         if (sd.chunk_box != nullptr && pend.v.k_cap <= 3.0f) return false;
         if (N >= ((int64_t)1 << 30) || pair_cap >= (1ull << 30)) return false;
         const FrameLayout L = frame_prepare(N, pend.T);  // every allocation before a capture
@@ -1180,7 +1183,8 @@ struct gs_ctx {
         record(0);
         HIPCHK(gs::launch_fill_u32(L.fr, 0u, L.fwords, st));
         if (spin_limit) HIPCHK(gs::launch_fill_u32(L.cnt + C_CTL + 1, spin_limit, 1, st));
-        if (timing) HIPCHK(gs::launch_fill_u32(b_evals.as<uint32_t>(), 0u, 64 * 8 * 2, st));
+        if (blend_counts)
+            HIPCHK(gs::launch_fill_u32(b_evals.as<uint32_t>(), 0u, 64 * 8 * 2, st));
         gs::ProjParams p = frame_proj_params(v, L, N, tiles_x, tiles_y);
         // the boxes bound three standard deviations: no skipping for wider k
         if (sd.chunk_box != nullptr && v->k_cap <= 3.0f) {
@@ -1204,7 +1208,8 @@ struct gs_ctx {
         record(4);
         gs::BlendParams bp{tiles_x, tiles_y, v->tile_size, v->image_height, v->image_width,
                            v->cull_disabled ? 1 : 0, v->transmittance_threshold, v->out_format,
-                           timing ? b_evals.as<unsigned long long>() : nullptr, L.cnt + C_CTL};
+                           blend_counts ? b_evals.as<unsigned long long>() : nullptr,
+                           L.cnt + C_CTL};
         HIPCHK(gs::launch_blend(b_brec.as<float4>(), ids_sorted, b_ranges.as<uint32_t>(), bp,
                                 dout, st));
         record(5);
@@ -1232,6 +1237,9 @@ struct gs_ctx {
         uint32_t* ids = nullptr;  // tile-sorted compact ids of the last forward
         double loss = 0.0, l1 = 0.0, ssim = 0.0;
     } tr;
+    // Adam moments stored as bf16 bits (gs_train_set_moments), kept across
+    // gs_train_init; fp32 by default
+    bool t_bf16_mom = false;
     DevBuf t_p, t_m, t_v, t_g, t_cidx, t_vis, t_grad2d, t_img, t_T, t_stop, t_dimg, t_tgt,
         t_loss, t_dbg, t_ssim;
     std::vector<float> t_host;
@@ -1252,6 +1260,18 @@ struct gs_ctx {
     }
 
     // AoS host arrays <-> SoA planes (mean 3, log-scale 3, quat 4, logit 1, SH 3K).
+    // bf16 bits of x, round to nearest even (a NaN stays a quiet NaN), as
+    // torch's float -> bfloat16 conversion rounds
+    static uint16_t bf16_rne(float x) {
+        uint32_t u;
+        std::memcpy(&u, &x, 4);
+        if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+        u += 0x7FFFu + ((u >> 16) & 1u);
+        return (uint16_t)(u >> 16);
+    }
+    // Moments are bf16 planes when t_bf16_mom (gs_train_set_moments).
+    bool bf16_planes(const DevBuf& b) const { return t_bf16_mom && (&b == &t_m || &b == &t_v); }
+
     void train_upload(DevBuf& b, const gs_train_arrays* a) {
         REQUIRE(a && a->means && a->log_scales && a->quats && a->opacity_logits && a->sh,
                 "train: null parameter array");
@@ -1272,6 +1292,15 @@ struct gs_ctx {
                         h[(11 + 3 * k + c) * n + i] = a->sh[(i * K + k) * 3 + c];
             }
         });
+        if (bf16_planes(b)) {
+            std::vector<uint16_t> hb((size_t)tr.planes * (size_t)n);
+            parallel_for((int64_t)hb.size(), [&](int64_t lo, int64_t hi) {
+                for (int64_t i = lo; i < hi; ++i) hb[(size_t)i] = bf16_rne(h[i]);
+            });
+            HIPCHK(hipMemcpyAsync(b.p, hb.data(), hb.size() * 2, hipMemcpyHostToDevice, st));
+            sync();
+            return;
+        }
         HIPCHK(hipMemcpyAsync(b.p, h, (size_t)tr.planes * n * 4, hipMemcpyHostToDevice, st));
         sync();
     }
@@ -1282,8 +1311,20 @@ struct gs_ctx {
         const int K = (tr.deg + 1) * (tr.deg + 1);
         t_host.resize((size_t)tr.planes * (size_t)std::max<int64_t>(n, 1));
         float* h = t_host.data();
-        HIPCHK(hipMemcpyAsync(h, b.p, (size_t)tr.planes * n * 4, hipMemcpyDeviceToHost, st));
-        sync();
+        if (bf16_planes(b)) {
+            std::vector<uint16_t> hb((size_t)tr.planes * (size_t)n);
+            HIPCHK(hipMemcpyAsync(hb.data(), b.p, hb.size() * 2, hipMemcpyDeviceToHost, st));
+            sync();
+            parallel_for((int64_t)hb.size(), [&](int64_t lo, int64_t hi) {
+                for (int64_t i = lo; i < hi; ++i) {
+                    const uint32_t u = (uint32_t)hb[(size_t)i] << 16;
+                    std::memcpy(&h[i], &u, 4);
+                }
+            });
+        } else {
+            HIPCHK(hipMemcpyAsync(h, b.p, (size_t)tr.planes * n * 4, hipMemcpyDeviceToHost, st));
+            sync();
+        }
         parallel_for(n, [&](int64_t lo, int64_t hi) {
             for (int64_t i = lo; i < hi; ++i) {
                 for (int c = 0; c < 3; ++c) {
@@ -1536,9 +1577,8 @@ struct gs_ctx {
             for (int ch = 0; ch < 3; ++ch)
                 ap.step[j++] = (float)(k == 0 ? c->lr_sh_dc : c->lr_sh_rest) / (float)bc1;
         if (timing) HIPCHK(hipEventRecord(tev[4], st));
-        HIPCHK(gs::launch_sparse_adam(t_p.as<float>(), t_m.as<float>(), t_v.as<float>(),
-                                      t_g.as<float>(), t_vis.as<uint8_t>(), tr.n, tr.planes, ap,
-                                      st));
+        HIPCHK(gs::launch_sparse_adam(t_p.as<float>(), t_m.p, t_v.p, t_g.as<float>(),
+                                      t_vis.as<uint8_t>(), tr.n, tr.planes, ap, t_bf16_mom, st));
         if (timing) HIPCHK(hipEventRecord(tev[5], st));
         ++tr.step;
     }
@@ -1617,6 +1657,7 @@ int gs_set_timing(gs_ctx* ctx, int on) {
     return guard([&] {
         REQUIRE(ctx, "null ctx");
         ctx->timing = on != 0;
+        ctx->blend_counts = on >= 2;
     });
 }
 
@@ -2149,6 +2190,39 @@ int gs_train_write(gs_ctx* ctx, int which, const gs_train_arrays* in) {
         ctx->train_upload(*b[which], in);
         if (which == 0) ctx->tr.fwd_valid = false;
         if (which == 3) ctx->tr.grads_valid = true;
+    });
+}
+
+int gs_train_set_moments(gs_ctx* ctx, int bf16) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        REQUIRE(bf16 == 0 || bf16 == 1, "train: moment format must be 0 (fp32) or 1 (bf16)");
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
+        const bool want = bf16 != 0;
+        if (want == ctx->t_bf16_mom) return;
+        if (!ctx->tr.ready) {
+            ctx->t_bf16_mom = want;
+            return;
+        }
+        // the stored moments are carried over (rounded to nearest even into bf16)
+        const int64_t n = ctx->tr.n;
+        const int K = (ctx->tr.deg + 1) * (ctx->tr.deg + 1);
+        const size_t nn = (size_t)std::max<int64_t>(n, 1);
+        std::vector<float> buf[2][5];
+        gs_train_arrays a[2];
+        for (int w = 0; w < 2; ++w) {
+            const size_t sz[5] = {nn * 3, nn * 3, nn * 4, nn, nn * K * 3};
+            for (int q = 0; q < 5; ++q) buf[w][q].resize(sz[q]);
+            a[w] = gs_train_arrays{buf[w][0].data(), buf[w][1].data(), buf[w][2].data(),
+                                   buf[w][3].data(), buf[w][4].data()};
+        }
+        ctx->sync();
+        ctx->train_download(ctx->t_m, &a[0]);
+        ctx->train_download(ctx->t_v, &a[1]);
+        ctx->t_bf16_mom = want;
+        ctx->train_upload(ctx->t_m, &a[0]);
+        ctx->train_upload(ctx->t_v, &a[1]);
     });
 }
 

@@ -149,6 +149,18 @@ __device__ __forceinline__ void report_error(uint32_t* ctl, uint32_t bits) {
 // A plain load: a flag that matters here was raised by an earlier launch, and
 // launch boundaries make it visible (an agent-scope atomic load of the one
 // address by every workgroup would serialise on it).
+// fp32 -> bf16 bits, round to nearest even (a NaN stays a quiet NaN), as
+// torch's float -> bfloat16 conversion rounds.
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+    return __uint_as_float((uint32_t)b << 16);
+}
+
 __device__ __forceinline__ bool upstream_failed(const uint32_t* ctl) {
     return ctl != nullptr && *ctl != 0u;
 }

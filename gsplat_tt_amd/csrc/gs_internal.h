@@ -396,8 +396,9 @@ hipError_t launch_train_bwd(const float4* trec, const uint32_t* sid, const uint3
 hipError_t launch_train_param_grads(const TrainParamsDev& P, const TrainCam& cam,
                                     const uint32_t* cidx, const float* grad2d,
                                     const TrainParamsDev& G, hipStream_t st);
-hipError_t launch_sparse_adam(float* p, float* m, float* v, const float* g,
+// m, v: float planes, or bf16 bits (uint16_t planes) with bf16_moments.
+hipError_t launch_sparse_adam(float* p, void* m, void* v, const float* g,
                               const uint8_t* visible, int64_t n, int planes, const AdamParams& ap,
-                              hipStream_t st);
+                              bool bf16_moments, hipStream_t st);
 
 }  // namespace gs

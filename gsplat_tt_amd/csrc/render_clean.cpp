@@ -31,6 +31,16 @@
 // GSPLAT_TT_CHUNK_CULL=1 turns on the chunk frustum skip with box factor
 // GSPLAT_TT_CHUNK_K (default 1.5), as render/host/pfwc_device.cpp:214-240 reads
 // them; the images are the same either way.
+//
+// Stage timings (render/host/stage_timers.h:1-60): host wall-clock spans,
+// always on and cheap: head (entry to the device call: argument checks, scene
+// cache lookup), frame (the device call: enqueue, wait, image copy-out; the
+// frame has one host wait, so its stages are not split on the host), tail
+// (stats and return value) and view_total; head + frame + tail = view_total.
+// GSPLAT_TT_STAGE_EVENTS=1 (a diagnostic, like the reference's
+// GSPLAT_TT_SPLIT_BLEND) adds per-stage device times from hipEvents on the
+// render stream under project, depth_sort, tile_assign, sort and blend; they
+// are 0.0 otherwise.
 #include <pybind11/numpy.h>
 #include <pybind11/pybind11.h>
 
@@ -55,8 +65,14 @@ uint64_t g_scene_version = 0;
 
 struct Timings {
     int64_t views = 0, xview_hits = 0, xview_misses = 0;
-    double project = 0, depth_sort = 0, tile_assign = 0, tile_sort = 0, blend = 0, view_total = 0;
+    double head = 0, frame = 0, tail = 0, view_total = 0;  // host spans
+    double project = 0, depth_sort = 0, tile_assign = 0, tile_sort = 0, blend = 0;  // events
 } g_t;
+bool g_events = false;  // per-stage hipEvents on the context (GSPLAT_TT_STAGE_EVENTS)
+using clk = std::chrono::steady_clock;
+double ms_between(clk::time_point a, clk::time_point b) {
+    return std::chrono::duration<double, std::milli>(b - a).count();
+}
 // the view announced by the last call's next_extrinsics (xview hit accounting)
 bool g_have_next = false;
 gs_view g_next{};
@@ -71,7 +87,7 @@ void check(int rc) {
 gs_ctx* ctx_locked() {
     if (g_ctx == nullptr) {
         check(gs_create(0, &g_ctx));
-        check(gs_set_timing(g_ctx, 1));
+        g_events = false;
     }
     return g_ctx;
 }
@@ -108,6 +124,7 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
                       bool cull_disabled, float transmittance_threshold, int max_radius,
                       float k_cap, bool use_isoellipse, int blend_mode, py::object next_extrinsics,
                       const std::string& output, bool sh_clamp) {
+    const clk::time_point t_entry = clk::now();
     (void)blend_mode;
     const auto mi = means.request();
     if (mi.ndim != 2 || mi.shape[1] != 3) throw std::invalid_argument("means must have shape (N, 3)");
@@ -181,10 +198,16 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
     void* out = zerocopy ? nullptr : image.mutable_data();
     gs_out_image ring_img{};
     gs_stats st{};
+    clk::time_point t_call, t_done;
     {
         py::gil_scoped_release nogil;
         std::lock_guard<std::mutex> lock(g_mutex);
         gs_ctx* c = ctx_locked();
+        const bool events = env_uint("GSPLAT_TT_STAGE_EVENTS", 0u) != 0u;
+        if (events != g_events) {
+            check(gs_set_timing(c, events ? 1 : 0));
+            g_events = events;
+        }
         const bool chunk_on = env_uint("GSPLAT_TT_CHUNK_CULL", 0u) != 0u;
         const double chunk_k = env_double("GSPLAT_TT_CHUNK_K", 1.5);
         if (chunk_on != g_chunk_on || chunk_k != g_chunk_k) {
@@ -197,12 +220,14 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
         // the next view: this call's parameters at the announced pose
         gs_view nv = v;
         if (ne) std::memcpy(nv.extrinsics, ne.data(), sizeof(nv.extrinsics));
+        t_call = clk::now();
         if (zerocopy) {
             check(gs_out_ring_config(c, slots));
             check(gs_render_out_ring(c, &v, ne ? &nv : nullptr, &ring_img, &st));
         } else {
             check(gs_render_next(c, &v, out, 0, ne ? &nv : nullptr, &st));
         }
+        t_done = clk::now();
         g_t.views++;
         if (g_have_next) {
             if (std::memcmp(&g_next, &v, sizeof(gs_view)) == 0) g_t.xview_hits++;
@@ -215,7 +240,6 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
         g_t.tile_assign += st.ms_tile_assign;
         g_t.tile_sort += st.ms_tile_sort;
         g_t.blend += st.ms_blend;
-        g_t.view_total += st.ms_total;
     }
     if (zerocopy) {
         // the array's base holds the lease: released when the image is collected
@@ -236,7 +260,16 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
     py::dict stats;
     stats["num_visible"] = st.num_visible;
     stats["num_entries"] = st.num_entries;
-    return py::make_tuple(image, stats);
+    py::tuple result = py::make_tuple(image, stats);
+    const clk::time_point t_end = clk::now();
+    {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        g_t.head += ms_between(t_entry, t_call);
+        g_t.frame += ms_between(t_call, t_done);
+        g_t.tail += ms_between(t_done, t_end);
+        g_t.view_total += ms_between(t_entry, t_end);
+    }
+    return result;
 }
 
 }  // namespace
@@ -275,19 +308,22 @@ PYBIND11_MODULE(render_clean, m) {
         g_have_next = false;
     });
     // Totals in ms over every render_view since reset_stage_timings, under the
-    // reference's keys (render/host/render.cpp:662-720): project (projection +
-    // depth sort), tile_assign, sort (tile sort), blend (microblock cull + blend,
-    // one kernel), view_total (wall clock), xview_hits / xview_misses (calls whose
-    // view was / was not the one the previous call announced). The device
-    // stages are hipEvent times. Keys of Tenstorrent sub-steps that this path
-    // does not have (head, blend_setup, mat, cull, d2h, assemble, tail, xview,
-    // sort_*, project_cov3d, project_pfwc_*, project_gather_*, tile_assign_*)
-    // are present and stay 0.0; depth_sort is this path's own extra key.
+    // reference's keys (render/host/render.cpp:662-720): head, tail and
+    // view_total are host spans, as in the reference; frame (this path's own
+    // key) is the device call, whose stages the host does not see apart (one
+    // wait per frame). With GSPLAT_TT_STAGE_EVENTS=1, project (projection +
+    // depth sort), tile_assign, sort (tile sort) and blend (microblock cull +
+    // blend, one kernel) hold hipEvent device times, and depth_sort (this
+    // path's own key) the depth sort alone; 0.0 otherwise. xview_hits /
+    // xview_misses: calls whose view was / was not the one the previous call
+    // announced. Keys of Tenstorrent sub-steps that this path does not have
+    // (blend_setup, mat, cull, d2h, assemble, xview, sort_*, project_cov3d,
+    // project_pfwc_*, project_gather_*, tile_assign_*) are present and stay 0.0.
     m.def("stage_timings", []() {
+        std::lock_guard<std::mutex> lock(g_mutex);
         py::dict d;
         d["views"] = g_t.views;
-        for (const char* k : {"head", "blend_setup", "mat", "cull", "d2h", "assemble", "tail",
-                              "xview", "sort_pread", "sort_bin_count", "sort_bin_hist_d2h",
+        for (const char* k : {"blend_setup", "mat", "cull", "d2h", "assemble", "xview", "sort_pread", "sort_bin_count", "sort_bin_hist_d2h",
                               "sort_bin_layout", "sort_upload", "sort_bin_emit", "sort_kernel",
                               "sort_d2h", "sort_compact", "sort_publish_host",
                               "sort_publish_wait", "sort_mat", "sort_pre", "sort_log",
@@ -301,6 +337,9 @@ PYBIND11_MODULE(render_clean, m) {
                               "tile_assign_scan_finish", "tile_assign_p_d2h",
                               "tile_assign_k2_finish", "tile_assign_publish"})
             d[k] = 0.0;
+        d["head"] = g_t.head;
+        d["frame"] = g_t.frame;
+        d["tail"] = g_t.tail;
         d["project"] = g_t.project + g_t.depth_sort;
         d["depth_sort"] = g_t.depth_sort;
         d["tile_assign"] = g_t.tile_assign;
@@ -311,5 +350,8 @@ PYBIND11_MODULE(render_clean, m) {
         d["xview_misses"] = g_t.xview_misses;
         return d;
     });
-    m.def("reset_stage_timings", []() { g_t = Timings{}; });
+    m.def("reset_stage_timings", []() {
+        std::lock_guard<std::mutex> lock(g_mutex);
+        g_t = Timings{};
+    });
 }

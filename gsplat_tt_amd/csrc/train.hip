@@ -861,10 +861,28 @@ __global__ __launch_bounds__(256) void k_train_param_grads(TrainParamsDev P, Tra
 }
 
 // Sparse Adam (train_oracle.py:434-470): rows with visible[i] set; every plane
-// of the parameter block, fp32, bias correction folded into the per-plane step
-// sizes and sqrt(1 - beta2^t) computed by the host.
-__global__ __launch_bounds__(256) void k_sparse_adam(float* __restrict__ p, float* __restrict__ m,
-                                                     float* __restrict__ v,
+// of the parameter block, fp32 arithmetic, bias correction folded into the
+// per-plane step sizes and sqrt(1 - beta2^t) computed by the host. Moments
+// stored as MOM: float, or bf16 bits (uint16_t) read exactly into fp32, updated
+// in fp32, the update taken from the fp32 values, stored rounded to nearest
+// even (train_oracle.py:445-470 with moment_dtype bfloat16,
+// t2_param_backward.py:195-224): half the moments' bytes.
+template <typename MOM>
+__device__ __forceinline__ float mom_load(const MOM* a, size_t k);
+template <>
+__device__ __forceinline__ float mom_load<float>(const float* a, size_t k) { return a[k]; }
+template <>
+__device__ __forceinline__ float mom_load<uint16_t>(const uint16_t* a, size_t k) {
+    return bf16_to_f32(a[k]);
+}
+__device__ __forceinline__ void mom_store(float* a, size_t k, float x) { a[k] = x; }
+__device__ __forceinline__ void mom_store(uint16_t* a, size_t k, float x) {
+    a[k] = f32_to_bf16_rne(x);
+}
+
+template <typename MOM>
+__global__ __launch_bounds__(256) void k_sparse_adam(float* __restrict__ p, MOM* __restrict__ m,
+                                                     MOM* __restrict__ v,
                                                      const float* __restrict__ g,
                                                      const uint8_t* __restrict__ visible,
                                                      int64_t n, int planes, AdamParams ap) {
@@ -873,12 +891,12 @@ __global__ __launch_bounds__(256) void k_sparse_adam(float* __restrict__ p, floa
     for (int j = 0; j < planes; ++j) {
         const size_t k = (size_t)j * n + i;
         const float gj = g[k];
-        const float m1 = ap.beta1 * m[k] + ap.one_minus_beta1 * gj;
-        const float v1 = ap.beta2 * v[k] + ap.one_minus_beta2 * gj * gj;
+        const float m1 = ap.beta1 * mom_load(m, k) + ap.one_minus_beta1 * gj;
+        const float v1 = ap.beta2 * mom_load(v, k) + ap.one_minus_beta2 * gj * gj;
         const float den = sqrtf(v1) / ap.sqrt_bc2 + ap.eps;
         p[k] = p[k] - ap.step[j] * (m1 / den);
-        m[k] = m1;
-        v[k] = v1;
+        mom_store(m, k, m1);
+        mom_store(v, k, v1);
     }
 }
 
@@ -954,13 +972,20 @@ hipError_t launch_train_param_grads(const TrainParamsDev& P, const TrainCam& cam
     return hipGetLastError();
 }
 
-hipError_t launch_sparse_adam(float* p, float* m, float* v, const float* g,
+hipError_t launch_sparse_adam(float* p, void* m, void* v, const float* g,
                               const uint8_t* visible, int64_t n, int planes, const AdamParams& ap,
-                              hipStream_t st) {
+                              bool bf16_moments, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     if (planes > kMaxTrainPlanes) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)((n + 255) / 256);
-    k_sparse_adam<<<grid, 256, 0, st>>>(p, m, v, g, visible, n, planes, ap);
+    if (bf16_moments)
+        k_sparse_adam<uint16_t><<<grid, 256, 0, st>>>(p, static_cast<uint16_t*>(m),
+                                                      static_cast<uint16_t*>(v), g, visible, n,
+                                                      planes, ap);
+    else
+        k_sparse_adam<float><<<grid, 256, 0, st>>>(p, static_cast<float*>(m),
+                                                   static_cast<float*>(v), g, visible, n, planes,
+                                                   ap);
     return hipGetLastError();
 }
 

@@ -76,11 +76,11 @@ typedef struct gs_stats {
     float ms_tile_sort;
     float ms_blend;
     float ms_total;         /* host wall clock of the whole call */
-    int64_t blend_evals;    /* pixel x Gaussian evaluations blended (timing on) */
-    int64_t blend_batches;  /* wave x 32-entry batches culled (timing on) */
-    int64_t blend_iters;    /* wave apply iterations (timing on) */
-    int64_t blend_kept;     /* kept (entry, microblock) pairs seen (timing on) */
-    int64_t blend_max_iters; /* longest wave's apply iterations (timing on) */
+    int64_t blend_evals;    /* pixel x Gaussian evaluations blended (gs_set_timing 2) */
+    int64_t blend_batches;  /* wave x 32-entry batches culled (gs_set_timing 2) */
+    int64_t blend_iters;    /* wave apply iterations (gs_set_timing 2) */
+    int64_t blend_kept;     /* kept (entry, microblock) pairs seen (gs_set_timing 2) */
+    int64_t blend_max_iters; /* longest wave's apply iterations (gs_set_timing 2) */
     int64_t chunks_skipped;  /* projection partitions the chunk frustum skip ruled out */
     /* The reference's microblock-cull counts (cull_and_blend.cpp:835-836, the
      * pairs_dropped / pairs_kept_per_mb of render_full's stats), when
@@ -93,7 +93,10 @@ typedef struct gs_stats {
 int gs_create(int device, gs_ctx** out);
 void gs_destroy(gs_ctx* ctx);
 const char* gs_last_error(void);
-int gs_set_timing(gs_ctx* ctx, int on);      /* per-stage hipEvent timing */
+/* on: 0 off, 1 per-stage hipEvent times in gs_stats (ms_project ..), 2 also
+ * the blend's evaluation counters (blend_evals ..; device atomics per wave).
+ * Frames with either are enqueued directly, never replayed from a graph. */
+int gs_set_timing(gs_ctx* ctx, int on);
 int gs_device_info(gs_ctx* ctx, int* num_cus, int* arch_minor);
 
 /* ---- frame ----------------------------------------------------------
@@ -331,6 +334,13 @@ int gs_train_init(gs_ctx* ctx, const gs_train_arrays* params, int64_t n, int sh_
 int gs_train_read(gs_ctx* ctx, int which, gs_train_arrays* out);
 int gs_train_write(gs_ctx* ctx, int which, const gs_train_arrays* in);
 int gs_train_set_step(gs_ctx* ctx, int64_t step);
+/* Storage of the Adam moments: 0 fp32 (default), 1 bf16 - the moments are read
+ * exactly into fp32, updated in fp32 and stored rounded to nearest even
+ * (gsplat/train_oracle.py:434-470 with moment_dtype bfloat16, the default of
+ * the reference's device step, gsplat/t2_param_backward.py:195-224). Stored
+ * moments are carried over (rounded when going to bf16); gs_train_read/write of
+ * moments take and return fp32 arrays either way. Kept across gs_train_init. */
+int gs_train_set_moments(gs_ctx* ctx, int bf16);
 /* Replaces the sparse-Adam row mask (n bytes) of the last forward. */
 int gs_train_set_visible(gs_ctx* ctx, const uint8_t* visible);
 

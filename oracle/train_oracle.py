@@ -386,9 +386,23 @@ def projection_backward(pr, g2, cfg: Cfg):
 
 
 # ------------------------------------------------------------------ Adam
-def sparse_adam(params, grads, m, v, step, visible, lr=None, betas=(0.9, 0.999), eps=1e-15):
-    """train_oracle.py:434-470 with fp32 moments: rows where `visible` is set are
-    updated, with bias correction t = step + 1; fp32 arithmetic."""
+def bf16_round(x):
+    """fp32 -> bf16 -> fp32, round to nearest even (torch's float -> bfloat16
+    conversion; a NaN stays NaN)."""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32) << 16
+    nan = np.isnan(np.asarray(x, np.float32))
+    r = np.where(nan, (u.astype(np.uint32) | 0x00400000) & 0xFFFF0000, r).astype(np.uint32)
+    return r.view(np.float32)
+
+
+def sparse_adam(params, grads, m, v, step, visible, lr=None, betas=(0.9, 0.999), eps=1e-15,
+                bf16_moments=False):
+    """train_oracle.py:434-470: rows where `visible` is set are updated, with
+    bias correction t = step + 1; fp32 arithmetic. bf16_moments: the moments
+    given are bf16 values (exact in fp32) and the new ones are stored rounded to
+    nearest even (moment_dtype bfloat16, :445-470); the parameter update uses
+    the fp32 values before rounding."""
     lr = DEFAULT_LR if lr is None else lr
     f32 = np.float32
     b1, b2 = betas
@@ -411,7 +425,7 @@ def sparse_adam(params, grads, m, v, step, visible, lr=None, betas=(0.9, 0.999),
         else:
             ss = f32(lr[name] / bc1)
         p[vis] = p[vis] - ss * (m1 / den)
-        mm[vis] = m1
-        vv[vis] = v1
+        mm[vis] = bf16_round(m1) if bf16_moments else m1
+        vv[vis] = bf16_round(v1) if bf16_moments else v1
         out[name] = (p, mm, vv)
     return out

@@ -69,8 +69,15 @@ def test_backend_render_fused_matches_oracle(hip_backend):
     scene, cams = scenes.config1(seed=62, n=30_000)
     cam = cams[0]
     assert hip_backend.has_render_fused()
-    img, st = hip_backend.render_fused(_Gaussians(scene), torch.from_numpy(cam.w2c),
-                                       torch.from_numpy(cam.K), cam.height, cam.width)
+    g, e, k = _Gaussians(scene), torch.from_numpy(cam.w2c), torch.from_numpy(cam.K)
+    img0, st0 = hip_backend.render_fused(g, e, k, cam.height, cam.width)
+    assert "pairs_dropped" not in st0 and "pairs_kept_per_mb" not in st0  # not asked for
+    counted = B.get_backend("hip", cull_stats=True)
+    try:
+        img, st = counted.render_fused(g, e, k, cam.height, cam.width)
+    finally:
+        counted.close()
+    assert np.array_equal(img, img0)
     cov = O.cov3d(scene.scales, scene.quats)
     ref, st_o, _ = O.render_full(scene.means, cov, scene.opacities, scene.colors, cam.w2c,
                                  cam.K, cam.height, cam.width, tile_size=32)

@@ -55,7 +55,7 @@ def test_ply_scene_through_backend_and_render_view(tmp_path):
     ref, st_o, _ = O.render_full(g.means, cov, g.opacities, g.colors, cam.w2c, cam.K,
                                  cam.height, cam.width, tile_size=32)
     assert st_o["num_visible"] > 1000
-    b = B.get_backend("hip")
+    b = B.get_backend("hip", cull_stats=True)
     try:
         img, st = b.render_fused(g, torch.from_numpy(cam.w2c), torch.from_numpy(cam.K),
                                  cam.height, cam.width)

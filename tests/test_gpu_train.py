@@ -81,6 +81,39 @@ def test_train_adam_matches_dump(gpu_ctx, name):
         assert np.allclose(p[k], g["adam_fp32_param_" + k], rtol=0, atol=1e-7), k
 
 
+
+@pytest.mark.parametrize("name", golden_io.TRAIN_CASES)
+def test_train_adam_bf16_moments_matches_dump(gpu_ctx, name):
+    """k_sparse_adam with bf16-stored moments against the reference's
+    moment_dtype=bfloat16 step (train_oracle.py:434-470): moments bit-exact,
+    parameters within 1e-7; switching the format carries the moments over."""
+    print("train adam bf16 moments", name, flush=True)
+    g, cfg, view, params = _fixture(name)
+    tr = L.Trainer(gpu_ctx, params, g["sh_degree"])
+    try:
+        tr.write(1, {k: g["adam_m_in_" + k] for k in TO.PARAM_NAMES})
+        tr.set_moments(True)  # fp32 moments carried over, rounded to nearest even
+        m_b = tr.read(1)
+        for k in TO.PARAM_NAMES:
+            assert np.array_equal(m_b[k], TO.bf16_round(g["adam_m_in_" + k])), k
+        tr.write(1, {k: g["adam_bf16_m_in_" + k] for k in TO.PARAM_NAMES})
+        tr.write(2, {k: g["adam_bf16_v_in_" + k] for k in TO.PARAM_NAMES})
+        tr.write(3, {k: g["grad_" + k].astype(np.float32) for k in TO.PARAM_NAMES})
+        tr.set_visible(g["visible"])
+        tr.set_step(int(g["adam_step_in"]))
+        tr.adam(cfg)
+        p, m, v = tr.read(0), tr.read(1), tr.read(2)
+        for k in TO.PARAM_NAMES:
+            assert np.array_equal(m[k], g["adam_bf16_m_" + k]), k
+            assert np.array_equal(v[k], g["adam_bf16_v_" + k]), k
+            assert np.allclose(p[k], g["adam_bf16_param_" + k], rtol=0, atol=1e-7), k
+        tr.set_moments(False)  # back to fp32: the bf16 values exactly
+        m32 = tr.read(1)
+        for k in TO.PARAM_NAMES:
+            assert np.array_equal(m32[k], g["adam_bf16_m_" + k]), k
+    finally:
+        tr.set_moments(False)
+
 def _c5_small(n=1500, H=90, W=160, seed=55):
     scene, tgt_scene, cams = scenes.config5(seed=seed, n=n)
     K = scenes.intrinsics(0.5 * W / np.tan(np.deg2rad(25.0)), 0.5 * W / np.tan(np.deg2rad(25.0)),

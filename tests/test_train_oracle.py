@@ -81,6 +81,44 @@ def test_sparse_adam_matches_dump(name):
         assert np.array_equal(p[inv], np.asarray(params[k], np.float32)[inv])
 
 
+def test_bf16_round_is_torch_rne():
+    """bf16_round against torch's float -> bfloat16 conversion (round to nearest
+    even) on edge patterns and random floats, and the tie cases by hand."""
+    import torch
+    one = np.float32(1.0)
+    ulp = np.float32(2.0 ** -7)  # bf16 spacing at 1
+    ties = np.array([one + ulp / 2, one + 3 * ulp / 2, -(one + ulp / 2)], np.float32)
+    assert np.array_equal(TO.bf16_round(ties), np.array([one, one + 2 * ulp, -one], np.float32))
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.standard_normal(100_000).astype(np.float32) * 10.0 ** rng.integers(
+        -30, 30, 100_000), np.array([0.0, -0.0, np.inf, -np.inf, 3.4e38, 1e-45, -1e-40],
+                                    np.float32)]).astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(TO.bf16_round(x).view(np.uint32), ref.view(np.uint32))
+    assert np.isnan(TO.bf16_round(np.array([np.nan], np.float32))).all()
+
+
+@pytest.mark.parametrize("name", golden_io.TRAIN_CASES)
+def test_sparse_adam_bf16_moments_matches_dump(name):
+    """The reference's bf16-moment Adam (moment_dtype bfloat16): moments in
+    from the dump's adam_bf16_*_in, moments out bit-exact, parameters 1e-7."""
+    g, cfg, params = _case(name)
+    grads = {k: g["grad_" + k] for k in TO.PARAM_NAMES}
+    m = {k: g["adam_bf16_m_in_" + k] for k in TO.PARAM_NAMES}
+    v = {k: g["adam_bf16_v_in_" + k] for k in TO.PARAM_NAMES}
+    out = TO.sparse_adam(params, grads, m, v, g["adam_step_in"], g["visible"],
+                         g["adam_lr_json"], tuple(g["adam_betas"]), float(g["adam_eps"]),
+                         bf16_moments=True)
+    for k in TO.PARAM_NAMES:
+        p, mm, vv = out[k]
+        assert np.array_equal(mm, g["adam_bf16_m_" + k]), k
+        assert np.array_equal(vv, g["adam_bf16_v_" + k]), k
+        assert not (mm.view(np.uint32) & 0xFFFF).any() and not (vv.view(np.uint32) & 0xFFFF).any()
+        assert np.allclose(p, g["adam_bf16_param_" + k], rtol=0, atol=1e-7), k
+        # the bf16 step differs from the fp32 one (the fixture pins a real change)
+    assert any(not np.array_equal(out[k][1], g["adam_fp32_m_" + k]) for k in TO.PARAM_NAMES)
+
+
 def test_l1_gradient():
     rng = np.random.default_rng(0)
     a = rng.uniform(size=(4, 5, 3))
