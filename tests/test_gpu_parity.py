@@ -305,6 +305,42 @@ def test_sort_u64_config4_20m(gpu_ctx):
     assert np.array_equal(ko, keys[order]) and np.array_equal(vo, vals[order])
 
 
+def test_sort_tile_depth_partition_counts(gpu_ctx):
+    """gs_sort_tile_depth_dev (8192-key partitions, a histogram of the first
+    digit, each pass counting the next one's) at key counts on both sides of
+    partition boundaries and with one to many partitions: exact against
+    numpy's stable sort, with the per-tile ranges."""
+    rng = np.random.default_rng(19)
+    tiles = 300
+    for n in (1, 8191, 8193, 3 * 8192 + 5, 8 * 8192, 9 * 8192 + 1, 100_003, 1_000_003):
+        t = np.minimum(rng.zipf(1.3, n), tiles).astype(np.uint64) - np.uint64(1)
+        d = np.exp(rng.uniform(np.log(0.2), np.log(100.0), n)).astype(np.float32)
+        d[: n // 4] = 2.0  # ties
+        keys = (t << np.uint64(32)) | d.view(np.uint32).astype(np.uint64)
+        vals = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+        dk, dv = gpu_ctx.dev_alloc(n * 8), gpu_ctx.dev_alloc(n * 4)
+        dr = gpu_ctx.dev_alloc(tiles * 8)
+        try:
+            gpu_ctx.h2d(dk, keys)
+            gpu_ctx.h2d(dv, vals)
+            gpu_ctx.sort_tile_depth_dev(dk, dv, n, tiles, dr)
+            ko, vo = np.empty_like(keys), np.empty_like(vals)
+            rg = np.empty((tiles, 2), np.uint32)
+            gpu_ctx.d2h(ko, dk)
+            gpu_ctx.d2h(vo, dv)
+            gpu_ctx.d2h(rg, dr)
+        finally:
+            for q in (dk, dv, dr):
+                gpu_ctx.dev_free(q)
+        order = np.argsort(keys, kind="stable")
+        assert np.array_equal(ko, keys[order]) and np.array_equal(vo, vals[order]), n
+        tk = (ko >> np.uint64(32)).astype(np.int64)
+        lo = np.searchsorted(tk, np.arange(tiles), "left")
+        hi = np.searchsorted(tk, np.arange(tiles), "right")
+        exp = np.stack([np.where(lo == hi, 0, lo), np.where(lo == hi, 0, hi)], 1)
+        assert np.array_equal(rg.astype(np.int64), exp), n
+
+
 def test_render_opacity_prune_is_exact(gpu_ctx):
     """Dropping the Gaussians below min_opacity at load leaves the frame bit for
     bit unchanged (the projection drops them and compacts in source order)."""
