@@ -26,6 +26,16 @@ FP32_PEAK_TFLOPS = 157.3     # MI355X FP32 peak (packed FP32 VALU issue)
 # per pixel x Gaussian evaluation: dx, dy (2 sub), quadratic form (3 mul + 2 FMA),
 # clamp, exp, alpha (mul + min), alpha*T, 3 colour FMA, T update; FMA = 2 flops
 BLEND_FLOPS_PER_EVAL = 20
+# the training backward per (pixel, entry) pair it evaluates (k_train_bwd): the
+# forward's recomputation for every pair up to the pixel's stop (dx, dy 2;
+# quadratic form 3 mul + 2 FMA; clamp 1; exp 1; opacity product 1; alpha clamp
+# 1) and, for the blended pairs, the gradient terms (1 - alpha, reciprocal, T
+# update 3; dL/dalpha 3 sub + dot 5 + scale 1 + background FMA 2; alpha T 1;
+# colour terms 3; opacity term 1; dp 1; mean terms 2 x (mul + FMA + mul) = 8;
+# conic terms 9; colour-behind recursion 3 x (mul + FMA) = 9; the nine sums 9);
+# FMA = 2 flops
+TRAIN_BWD_FLOPS_CONSIDERED = 13
+TRAIN_BWD_FLOPS_BLENDED = 55
 # frame slots of gs_render_batch; one output buffer per slot
 FRAMES_IN_FLIGHT = 4
 # host threads of one GPU's share of the box (its worker pools are sized to it)
@@ -47,6 +57,8 @@ def parse():
     ap.add_argument("--no-sort", action="store_true")
     ap.add_argument("--sort-only", action="store_true",
                     help="only the 50M-key tile/depth sort leg (for profiling)")
+    ap.add_argument("--train-only", action="store_true",
+                    help="only the training leg (for profiling)")
     ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--train-steps", type=int, default=20)
     ap.add_argument("--train-n", type=int, default=1_000_000)
@@ -531,6 +543,10 @@ def bench_train(ctx, n, steps):
     adam_bytes_b = visible * planes * 20
     P = stats[-1]["num_entries"]
     bwd_bytes = P * 48 + stats[-1]["num_blendable"] * 9 * 4 * 2
+    considered = float(np.mean([s["pixel_pairs"] for s in stats]))
+    blended = float(np.mean([s["pixel_blended"] for s in stats]))
+    bwd_flops = TRAIN_BWD_FLOPS_CONSIDERED * considered + TRAIN_BWD_FLOPS_BLENDED * blended
+    bwd_tf = bwd_flops / (avg["ms_backward"] * 1e-3) / 1e12
     return {"workload": "training step, 1M Gaussians (64-component mixture), SH degree 1, "
                         "1280x720, L1 vs render of a perturbed copy, sparse Adam, fp32",
             "steps": steps, "ms_per_step": round(el / steps * 1e3, 4),
@@ -544,13 +560,21 @@ def bench_train(ctx, n, steps):
                          "frac": round(adam_bytes / (avg["ms_adam"] * 1e-3) / 1e9
                                        / HBM_PEAK_GBS, 4),
                          "model": "visible rows x 23 planes x (16 B read + 12 B write)"},
-                "backward": {"bound": "valu (per-pixel recomputation and wave sums)",
-                             "bytes": bwd_bytes,
-                             "achieved": round(bwd_bytes / (avg["ms_backward"] * 1e-3) / 1e9, 1),
-                             "frac": round(bwd_bytes / (avg["ms_backward"] * 1e-3) / 1e9
-                                           / HBM_PEAK_GBS, 4),
-                             "model": "pairs x 48 B records + M x 9 gradient terms "
-                                      "(read + write)"}},
+                "backward": {"bound": "valu", "pipe": "fp32 VALU (no MFMA issued)",
+                             "achieved": round(bwd_tf, 3), "peak": FP32_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(bwd_tf / FP32_PEAK_TFLOPS, 4),
+                             "flops": bwd_flops, "pixel_pairs": considered,
+                             "pixel_blended": blended,
+                             "model": f"{TRAIN_BWD_FLOPS_CONSIDERED} flops per (pixel, entry) "
+                                      f"pair up to the pixel's stop + "
+                                      f"{TRAIN_BWD_FLOPS_BLENDED} per blended pair",
+                             "hbm": {"bytes": bwd_bytes,
+                                     "achieved": round(bwd_bytes / (avg["ms_backward"] * 1e-3)
+                                                       / 1e9, 1),
+                                     "frac": round(bwd_bytes / (avg["ms_backward"] * 1e-3) / 1e9
+                                                   / HBM_PEAK_GBS, 4),
+                                     "model": "pairs x 48 B records + M x 9 gradient terms "
+                                              "(read + write)"}}},
             "full_loss": {"loss": "0.8 L1 + 0.2 (1 - SSIM)",
                           "ms_per_step": round(el_s / steps * 1e3, 4),
                           "steps_per_s": round(steps / el_s, 2),
@@ -701,6 +725,12 @@ def main():
         return
     if args.sequential_frames:
         sequential_frames(args)
+        return
+    if args.train_only:
+        from gsplat_tt_amd import _lib as L
+        ctx = L.Context(0, timing=False)
+        print(json.dumps({"train": bench_train(ctx, args.train_n, args.train_steps)}), flush=True)
+        ctx.close()
         return
     if args.sort_only:
         from gsplat_tt_amd import _lib as L

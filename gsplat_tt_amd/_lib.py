@@ -104,7 +104,8 @@ class GsTrainStats(ctypes.Structure):
                 ("ms_forward", ctypes.c_float), ("ms_backward", ctypes.c_float),
                 ("ms_adam", ctypes.c_float), ("ms_total", ctypes.c_float),
                 ("l1", ctypes.c_double), ("ssim", ctypes.c_double),
-                ("pairs_pre", ctypes.c_int64), ("pair_capacity", ctypes.c_int64)]
+                ("pairs_pre", ctypes.c_int64), ("pair_capacity", ctypes.c_int64),
+                ("pixel_pairs", ctypes.c_int64), ("pixel_blended", ctypes.c_int64)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}

@@ -1234,6 +1234,7 @@ struct gs_ctx {
         int H = 0, W = 0, tiles_x = 0, tiles_y = 0;
         gs::TrainCam cam{};
         uint32_t M = 0, P = 0, p_pre = 0;
+        int64_t pixel_pairs = 0, pixel_blended = 0;
         uint32_t* ids = nullptr;  // tile-sorted compact ids of the last forward
         double loss = 0.0, l1 = 0.0, ssim = 0.0;
     } tr;
@@ -1434,7 +1435,7 @@ struct gs_ctx {
         t_T.ensure(px * 4);
         t_stop.ensure(px * 4);
         t_dimg.ensure(px * 12);
-        t_loss.ensure(16);
+        t_loss.ensure(32);  // L1 sum, SSIM sum (f64), considered and blended pairs (u64)
         if (timing)
             for (auto& e : tev)
                 if (!e) HIPCHK(hipEventCreate(&e));
@@ -1442,7 +1443,7 @@ struct gs_ctx {
         HIPCHK(gs::launch_fill_u32(L.fr, 0u, L.fwords, st));
         if (spin_limit) HIPCHK(gs::launch_fill_u32(L.cnt + C_CTL + 1, spin_limit, 1, st));
         tr.cam.ctl = L.cnt + C_CTL;
-        HIPCHK(gs::launch_fill_u32(t_loss.as<uint32_t>(), 0u, 4, st));
+        HIPCHK(gs::launch_fill_u32(t_loss.as<uint32_t>(), 0u, 8, st));
         gs::Compact cpt{b_rc.as<float4>(), b_dkey.as<uint32_t>(),
                         nullptr, b_src.as<uint32_t>()};
         HIPCHK(gs::launch_train_project(tplanes(t_p), tr.cam, cpt, b_brec.as<float4>(),
@@ -1471,6 +1472,7 @@ struct gs_ctx {
         fp.grad_scale = (float)((double)c->loss_scale * (1.0 - (double)c->lambda_dssim) /
                                 (3.0 * (double)px));
         fp.loss = reinterpret_cast<double*>(t_loss.p);
+        fp.pairs = reinterpret_cast<unsigned long long*>(t_loss.p) + 2;
         fp.ctl = L.cnt + C_CTL;
         HIPCHK(gs::launch_train_fwd(b_brec.as<float4>(), tr.ids, b_ranges.as<uint32_t>(), fp, st));
         if (tgt_dev != nullptr && c->lambda_dssim > 0.0f)
@@ -1501,7 +1503,7 @@ struct gs_ctx {
         for (int attempt = 0;; ++attempt) {
             train_forward_enqueue(v, c, tgt, dbg);
             HIPCHK(hipMemcpyAsync(h_pin, b_frame.p, 64 * 4, hipMemcpyDeviceToHost, st));
-            HIPCHK(hipMemcpyAsync(h_pin + 64, t_loss.p, 16, hipMemcpyDeviceToHost, st));
+            HIPCHK(hipMemcpyAsync(h_pin + 64, t_loss.p, 32, hipMemcpyDeviceToHost, st));
             sync();
             // The capacity test comes first: an attempt past the capacity has
             // kErrCapacity raised by the count scan, and is re-run (its fill
@@ -1518,6 +1520,10 @@ struct gs_ctx {
         }
         tr.M = h_pin[C_M];
         tr.p_pre = h_pin[C_PPRE];
+        uint64_t pp[2];
+        std::memcpy(pp, h_pin + 68, 16);
+        tr.pixel_pairs = (int64_t)pp[0];
+        tr.pixel_blended = (int64_t)pp[1];
         tr.P = h_pin[C_P];
         double sums[2];
         std::memcpy(sums, h_pin + 64, 16);
@@ -1595,6 +1601,8 @@ struct gs_ctx {
         o.ssim = tr.ssim;
         o.pairs_pre = tr.p_pre;
         o.pair_capacity = (int64_t)pair_cap;
+        o.pixel_pairs = tr.pixel_pairs;
+        o.pixel_blended = tr.pixel_blended;
         if (timing) {
             float ms = 0.0f;
             if (fwd && hipEventElapsedTime(&ms, tev[0], tev[1]) == hipSuccess) o.ms_forward = ms;

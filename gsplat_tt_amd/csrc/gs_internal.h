@@ -347,6 +347,9 @@ struct TrainFwdParams {
     float* dimage;         // dL/dimage (H,W,3), written with a target
     float grad_scale;      // loss_scale / (3HW)
     double* loss;          // accumulates sum |image - target|
+    // (pixel, entry) pairs: [0] considered (each pixel's entries up to its
+    // stop), [1] blended; accumulated (the backward evaluates the same pairs)
+    unsigned long long* pairs;
     const uint32_t* ctl;   // control words of the forward (nothing is read after an error)
 };
 

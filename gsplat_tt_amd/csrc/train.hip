@@ -317,6 +317,7 @@ __global__ __launch_bounds__(256) void k_train_fwd(const float4* __restrict__ tr
                                                    TrainFwdParams fp) {
     __shared__ float4 s0[256], s1[256], s2[256];
     __shared__ double s_loss[4];
+    __shared__ unsigned long long s_pairs[2][4];
     // after an earlier give-up the sorted ids may be wrong: read nothing (the
     // flag was raised by an earlier launch, so every thread sees the same value)
     if (upstream_failed(fp.ctl)) return;
@@ -330,6 +331,7 @@ __global__ __launch_bounds__(256) void k_train_fwd(const float4* __restrict__ tr
     float T = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
     bool done = !inside;
     uint32_t stop = end - start;
+    uint32_t blended = 0;
     for (uint32_t base = start; base < end; base += 256) {
         const uint32_t nb = min(256u, end - base);
         if ((uint32_t)tid < nb) {
@@ -359,6 +361,7 @@ __global__ __launch_bounds__(256) void k_train_fwd(const float4* __restrict__ tr
                 cg += at * c.y;
                 cb += at * c.z;
                 T = tn;
+                ++blended;
             }
         }
         if (__syncthreads_count(!done) == 0) break;
@@ -386,8 +389,27 @@ __global__ __launch_bounds__(256) void k_train_fwd(const float4* __restrict__ tr
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, GS_WAVE);
         if (lane_id() == 0) s_loss[tid / GS_WAVE] = lsum;
-        __syncthreads();
-        if (tid == 0) atomicAdd(fp.loss, s_loss[0] + s_loss[1] + s_loss[2] + s_loss[3]);
+    }
+    if (fp.pairs != nullptr) {
+        unsigned long long pc = inside ? stop : 0u, pb = inside ? blended : 0u;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            pc += __shfl_xor(pc, o, GS_WAVE);
+            pb += __shfl_xor(pb, o, GS_WAVE);
+        }
+        if (lane_id() == 0) {
+            s_pairs[0][tid / GS_WAVE] = pc;
+            s_pairs[1][tid / GS_WAVE] = pb;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        if (fp.target != nullptr)
+            atomicAdd(fp.loss, s_loss[0] + s_loss[1] + s_loss[2] + s_loss[3]);
+        if (fp.pairs != nullptr) {
+            atomicAdd(&fp.pairs[0], s_pairs[0][0] + s_pairs[0][1] + s_pairs[0][2] + s_pairs[0][3]);
+            atomicAdd(&fp.pairs[1], s_pairs[1][0] + s_pairs[1][1] + s_pairs[1][2] + s_pairs[1][3]);
+        }
     }
 }
 

@@ -313,6 +313,9 @@ typedef struct gs_train_stats {
     double ssim;            /* mean SSIM (computed when lambda_dssim > 0) */
     int64_t pairs_pre;      /* candidate tile-Gaussian pairs before the cull */
     int64_t pair_capacity;  /* candidate-pair capacity after the call (grown on overflow) */
+    int64_t pixel_pairs;    /* (pixel, entry) pairs the forward considered (up to each
+                               pixel's stop); the backward evaluates the same pairs */
+    int64_t pixel_blended;  /* of those, the pairs blended (alpha >= alpha_min) */
 } gs_train_stats;
 
 /* Gaussian-indexed projection values of the last forward (parity tests). */

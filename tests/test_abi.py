@@ -54,6 +54,7 @@ int main(void) {
   P(gs_train_cfg, loss_scale) P(gs_train_cfg, lambda_dssim) P(gs_train_cfg, lr_means)
   P(gs_train_cfg, eps) P(gs_train_stats, loss) P(gs_train_stats, ms_total)
   P(gs_train_stats, l1) P(gs_train_stats, ssim) P(gs_train_stats, pair_capacity)
+  P(gs_train_stats, pixel_blended)
   P(gs_train_proj, visible)
   P(gs_scene, n) P(gs_scene, version) P(gs_view, image_height) P(gs_view, tile_size)
   P(gs_view, k_cap) P(gs_view, out_format) P(gs_view, sh_clamp_hi)
