@@ -71,6 +71,7 @@ struct Band {
     int tile, tile_x, tile_y, mbx, mby;
     int px_start, py0;
     float tx_tile, ty_tile, pxs, offx, pxc, pyc, mb_ox, mb_oy;
+    float ext_x0, ext_x1, ext_y0, ext_y1;  // the microblock's extent-test bounds
     float pxsA, pyr0;  // band: microblock A's first column, first row centre (+0.5)
     bool emptyA, emptyB, fullA, fullB, full, pix_valid;
 };
@@ -115,6 +116,10 @@ __device__ __forceinline__ Band make_band(const BlendParams& bp, int lane) {
     // microblock cull rectangle (cull_and_blend.cpp:447-498)
     g.mb_oy = g.ty_tile + (float)(g.mby * 4);
     g.mb_ox = g.tx_tile + (float)(g.mbx * 8);
+    g.ext_x0 = (float)(8 * g.mbx);
+    g.ext_x1 = (float)(8 * g.mbx + 8);
+    g.ext_y0 = (float)(4 * g.mby);
+    g.ext_y1 = (float)(4 * g.mby + 4);
     return g;
 }
 
@@ -122,13 +127,19 @@ __device__ __forceinline__ Band make_band(const BlendParams& bp, int lane) {
 // (cull_and_blend.cpp:447-498).
 __device__ __forceinline__ bool mb_keep(const Band& g, float4 r0, float4 r1, int cull_disabled) {
     const float lt = r1.w;
-    if (!(lt < 0.0f)) return false;
     const float mx = r0.x, my = r0.y;
-    const int mx_lo = max(0, (int)floorf(((mx - r0.z) - g.tx_tile) / 8.0f));
-    const int mx_hi = min(3, (int)floorf(((mx + r0.z) - g.tx_tile) / 8.0f));
-    const int my_lo = max(0, (int)floorf(((my - r0.w) - g.ty_tile) / 4.0f));
-    const int my_hi = min(7, (int)floorf(((my + r0.w) - g.ty_tile) / 4.0f));
-    if (!(mx_lo <= g.mbx && g.mbx <= mx_hi && my_lo <= g.mby && g.mby <= my_hi)) return false;
+    // The reference's microblock range of the extent, mx_lo = max(0, floor(ax / 8)),
+    // mx_hi = min(3, floor(bx / 8)) (and 4-row ones in y), tested against this
+    // microblock's column mbx without the integer round trip: mbx >= 0 and
+    // mbx <= 3, the divisions by 8 and 4 are exact, and floor(t) <= k <=> t < k + 1,
+    // k <= floor(t) <=> k <= t for an integer k, so
+    // mx_lo <= mbx <=> ax < 8 mbx + 8 and mbx <= mx_hi <=> 8 mbx <= bx.
+    // (The extents of a projected record are finite and far inside the int range.)
+    const float ax = (mx - r0.z) - g.tx_tile, bx = (mx + r0.z) - g.tx_tile;
+    const float ay = (my - r0.w) - g.ty_tile, by = (my + r0.w) - g.ty_tile;
+    // (one test with the floor check, lt < 0, so the record is read whole first)
+    if (!((lt < 0.0f) & (ax < g.ext_x1) & (g.ext_x0 <= bx) & (ay < g.ext_y1) & (g.ext_y0 <= by)))
+        return false;
     const float ci_a = r1.x, ci_b = r1.y, ci_c = r1.z;
     const float v_lo = g.mb_oy - my;
     const float v_hi = v_lo + 4.0f;
@@ -145,12 +156,13 @@ __device__ __forceinline__ bool mb_keep(const Band& g, float4 r0, float4 r1, int
         if (!x_in) {
             const float uf = (u_lo > 0.0f) ? u_lo : u_hi;
             float vs = -ci_b * uf / fmax_std(ci_c, 1e-12f);
-            vs = fclamp_std(vs, v_lo, v_hi);
+            // clamp to [v_lo, v_hi] (v_lo < v_hi; vs is not NaN for a projected record)
+            vs = __builtin_amdgcn_fmed3f(vs, v_lo, v_hi);
             m2_v = ci_a * uf * uf + 2.0f * ci_b * uf * vs + ci_c * vs * vs;
         }
         if (!y_in) {
             float us = -ci_b * v_fix / fmax_std(ci_a, 1e-12f);
-            us = fclamp_std(us, u_lo, u_hi);
+            us = __builtin_amdgcn_fmed3f(us, u_lo, u_hi);
             m2_h = ci_a * us * us + 2.0f * ci_b * us * v_fix + ci_c * v_fix * v_fix;
         }
         m2_min = fmin_std(m2_v, m2_h);
@@ -176,7 +188,7 @@ struct BandStage {
     float4 rows[32][2];   // rows 2k, 2k+1: (y_term, xy_coef, y_term, xy_coef)
     float4 dx[32][4];     // columns 4k .. 4k+3
     float2 aop[32][2];    // (-ci_a/2, op or 0) per half
-    float4 rgb[32];
+    float4 rgb[32];       // the record's (r, g, b, opacity)
 };
 union BlendLds {
     BatchRec rec[32];     // image-edge bands
@@ -218,13 +230,11 @@ __device__ __forceinline__ void blend_band_interior(const Band& g, const float4*
     for (uint32_t base = start; base < end; base += 32) {
         const uint32_t idx = base + q;
         const bool has = idx < end;
-        float4 r0 = make_float4(0, 0, 0, 0), r1 = r0, r2 = r0;
-        if (has) {
-            const uint32_t gi = sid[idx];
-            r0 = brec[3 * (size_t)gi + 0];
-            r1 = brec[3 * (size_t)gi + 1];
-            r2 = brec[3 * (size_t)gi + 2];
-        }
+        // lanes past the tile's end load its last entry (never walked: not kept)
+        const uint32_t gi = sid[has ? idx : end - 1];
+        const float4 r0 = brec[3 * (size_t)gi + 0];
+        const float4 r1 = brec[3 * (size_t)gi + 1];
+        const float4 r2 = brec[3 * (size_t)gi + 2];
         const bool keep = has && alive && mb_keep(g, r0, r1, bp.cull_disabled);
         const uint64_t mask = __ballot(keep);
         ++n_batch;
@@ -241,7 +251,7 @@ __device__ __forceinline__ void blend_band_interior(const Band& g, const float4*
         uint32_t pany = plo | phi;  // uniform: entries after which a half tests
         cnt += (uint32_t)__builtin_popcount(mine);
         // stage entry q (both halves hold its record): half h its rows 2h, 2h+1,
-        // its columns 8h .. 8h+7 and its own opacity, half 1 the colour (the
+        // its columns 8h .. 8h+7 and its own opacity, both the colour (the
         // AVX2 rule's operations, cull_and_blend.cpp:194-279: px_base = px0 - mx,
         // dx = px_base + (c + 0.5), dy = py + 0.5 - my, y_term = C dy dy,
         // xy_coef = B dy)
@@ -253,8 +263,8 @@ __device__ __forceinline__ void blend_band_interior(const Band& g, const float4*
             const float pb = g.pxs - r0.x;
             st->dx[q][2 * h] = make_float4(pb + 0.5f, pb + 1.5f, pb + 2.5f, pb + 3.5f);
             st->dx[q][2 * h + 1] = make_float4(pb + 4.5f, pb + 5.5f, pb + 6.5f, pb + 7.5f);
-            st->aop[q][h] = make_float2(-0.5f * r1.x, keep ? r2.x : 0.0f);
-            if (h) st->rgb[q] = make_float4(r2.y, r2.z, r2.w, 0.0f);
+            st->aop[q][h] = make_float2(-0.5f * r1.x, keep ? r2.w : 0.0f);
+            st->rgb[q] = r2;  // both halves hold entry q's record: the same words
         }
         __syncthreads();  // one wave per workgroup: orders the LDS writes and reads
         const float* rowp = &st->rows[0][pi >> 1].x + 2 * (pi & 1);
@@ -352,9 +362,9 @@ __device__ __forceinline__ void blend_band_edge(const Band& g, const float4* __r
         // power coefficients of the AVX2 path (cull_and_blend.cpp:198-200): exact
         // scalings of the conic, so the image-edge rule recovers it exactly
         if (h == 0) {
-            s_rec[q].p0 = make_float4(r0.x, r0.y, r2.x, 0.0f);
+            s_rec[q].p0 = make_float4(r0.x, r0.y, r2.w, 0.0f);
             s_rec[q].p1 = make_float4(-0.5f * r1.x, -r1.y, -0.5f * r1.z, 0.0f);
-            s_rec[q].p2 = make_float4(r2.y, r2.z, r2.w, 0.0f);
+            s_rec[q].p2 = r2;
         }
         __syncthreads();  // one wave per workgroup: orders the LDS writes and reads
         uint32_t uni = mA | mB;

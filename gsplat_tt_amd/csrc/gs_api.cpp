@@ -1888,11 +1888,11 @@ int gs_project(gs_ctx* ctx, const gs_scene* scene, const gs_view* view, uint8_t*
                 covs2d[m * 4 + 3] = rc[m * 8 + 6];
             }
             if (depths) std::memcpy(&depths[m], &dk[m], 4);
-            if (opac_out) opac_out[m] = brec[m * 12 + 8];
+            if (opac_out) opac_out[m] = brec[m * 12 + 11];
             if (colors_out) {
-                colors_out[m * 3 + 0] = brec[m * 12 + 9];
-                colors_out[m * 3 + 1] = brec[m * 12 + 10];
-                colors_out[m * 3 + 2] = brec[m * 12 + 11];
+                colors_out[m * 3 + 0] = brec[m * 12 + 8];
+                colors_out[m * 3 + 1] = brec[m * 12 + 9];
+                colors_out[m * 3 + 2] = brec[m * 12 + 10];
             }
         }
     });

@@ -312,7 +312,7 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
         const float op = p.has_opac ? s.opac[i] : 1.0f;
         out.brec[m * 3 + 0] = make_float4(vmx[it], vmy[it], xh, yh);
         out.brec[m * 3 + 1] = make_float4(ci_a, ci_b, ci_c, lt);
-        out.brec[m * 3 + 2] = make_float4(op, rgb[0], rgb[1], rgb[2]);
+        out.brec[m * 3 + 2] = make_float4(rgb[0], rgb[1], rgb[2], op);
         if (out.src != nullptr) out.src[m] = (uint32_t)i;
     }
 }
@@ -453,8 +453,8 @@ __global__ void k_brec_from_arrays(const float* __restrict__ means2d,
     }
     brec[i * 3 + 0] = make_float4(means2d[i * 2 + 0], means2d[i * 2 + 1], xh, yh);
     brec[i * 3 + 1] = make_float4(c / det, -b / det, a / det, lt);
-    brec[i * 3 + 2] = make_float4(opac[i], colors[i * 3 + 0], colors[i * 3 + 1],
-                                  colors[i * 3 + 2]);
+    brec[i * 3 + 2] = make_float4(colors[i * 3 + 0], colors[i * 3 + 1], colors[i * 3 + 2],
+                                  opac[i]);
 }
 
 }  // namespace

@@ -593,34 +593,53 @@ __device__ __forceinline__ float dpp_add(float v) {
     return v + __int_as_float(x);
 }
 
-// Sum over each row of 16 lanes, left in every lane of the row (quad swaps,
-// half-row and row mirrors).
-__device__ __forceinline__ float row_fsum(float v) {
+// Lanes whose per-pair terms are summed together before one of them adds the
+// sums into LDS: fewer LDS atomics against more DPP steps. Measured on the 1M
+// training step (backward ms): 8 lanes 0.99, 16 lanes 0.63, 32 lanes 0.57,
+// 64 lanes 0.58 (LDS float atomics cost more per lane than the DPP adds).
+constexpr int kBwdGroup = 32;
+constexpr int kBwdCopies = GS_WAVE / kBwdGroup;  // LDS accumulator copies, one per group
+constexpr int kBwdBatch = 128;
+
+// Sum over each group of kBwdGroup lanes, complete in the group's last lane
+// (quad swaps, half-row and row mirrors, then row broadcasts across rows).
+__device__ __forceinline__ float group_fsum(float v) {
     v = dpp_add<0xB1, 0xF>(v);   // quad_perm 1,0,3,2
     v = dpp_add<0x4E, 0xF>(v);   // quad_perm 2,3,0,1
     v = dpp_add<0x141, 0xF>(v);  // row_half_mirror
-    v = dpp_add<0x140, 0xF>(v);  // row_mirror
+    if constexpr (kBwdGroup >= 16) v = dpp_add<0x140, 0xF>(v);  // row_mirror
+    // Across rows: v += lane 15 of the row before (rows 1, 3), then v += lane 31
+    // (rows 2, 3). One DPP add each, the rows outside the row mask keeping v; the
+    // s_nop gives the two wait states a DPP read needs after a VALU write.
+    if constexpr (kBwdGroup >= 32)
+        asm volatile("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf"
+                     : "+v"(v));
+    if constexpr (kBwdGroup >= 64)
+        asm volatile("s_nop 1\n\tv_add_f32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf"
+                     : "+v"(v));
     return v;
 }
-
-constexpr int kBwdBatch = 128;
 
 // Backward of one 16x16 tile: entries from the last one any pixel considered
 // down to the first; per pixel the reverse recursion T_i = T_{i+1}/(1 - alpha_i),
 // behind_i = alpha_{i+1} c_{i+1} + (1 - alpha_{i+1}) behind_{i+1},
 // dL/dalpha_i = T_i (c_i - behind_i) . g - T_final bg . g / (1 - alpha_i).
-// The nine per-pair sums (dmx dmy dA dB dC dop dr dg db) are reduced over each
-// 16-lane row of a wave and added into four LDS accumulators (one per row
-// position, shared by the tile's four waves); their sum goes to the Gaussian's
-// accumulator with one global atomic per term. 1/(1 - alpha) is one reciprocal
-// estimate, exp the hardware exponential (the forward uses the same one, so both
-// see the same alpha).
+// Per (wave, entry): the entry's alpha for every lane, a ballot of the lanes
+// that blend it, and only when one does, the nine per-pair terms (dmx dmy dA
+// dB dC dop dr dg db) for every lane with the lanes that do not blend it
+// contributing exact zeros (selects, no divergent branches). The terms are
+// summed over each group of kBwdGroup lanes with DPP moves and the group's last
+// lane adds them into its own LDS accumulator copy (copies interleaved, so the
+// lanes hit distinct banks); the copies' sum goes to the Gaussian's accumulator
+// with one global atomic per term. 1/(1 - alpha) is one reciprocal estimate,
+// exp the hardware exponential (the forward uses the same one, so both see the
+// same alpha).
 __global__ __launch_bounds__(256) void k_train_bwd(const float4* __restrict__ trec,
                                                    const uint32_t* __restrict__ sid,
                                                    const uint32_t* __restrict__ ranges,
                                                    TrainBwdParams bp) {
     __shared__ float4 s0[kBwdBatch], s1[kBwdBatch], s2[kBwdBatch];
-    __shared__ float s_acc[4][kBwdBatch][9];
+    __shared__ __align__(16) float s_acc[kBwdBatch][9][kBwdCopies];
     __shared__ uint32_t s_has[4][kBwdBatch];
     __shared__ uint32_t s_nmax;
     const int tid = threadIdx.x, w = tid / GS_WAVE, lane = lane_id();
@@ -646,6 +665,12 @@ __global__ __launch_bounds__(256) void k_train_bwd(const float4* __restrict__ tr
     if (stop > 0) atomicMax(&s_nmax, stop);
     __syncthreads();
     const uint32_t nmax = min(s_nmax, end - start);
+    // the wave's own last considered entry: entries past it are skipped
+    uint32_t wstop = stop;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) wstop = max(wstop, (uint32_t)__shfl_xor((int)wstop, o, GS_WAVE));
+    float* const acc_lane = &s_acc[0][0][lane / kBwdGroup];  // this lane's copy (group leaders)
+    const bool leader = (lane % kBwdGroup) == kBwdGroup - 1;
     float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f;  // colour behind (normalised)
     for (int32_t hi = (int32_t)nmax; hi > 0; hi -= kBwdBatch) {
         const int32_t lo = max(0, hi - kBwdBatch);
@@ -656,56 +681,60 @@ __global__ __launch_bounds__(256) void k_train_bwd(const float4* __restrict__ tr
             s1[tid] = trec[3 * (size_t)gi + 1];
             s2[tid] = trec[3 * (size_t)gi + 2];
         }
-        for (int i = tid; i < 4 * kBwdBatch * 9; i += 256) (&s_acc[0][0][0])[i] = 0.0f;
+        for (int i = tid; i < kBwdBatch * 9 * kBwdCopies / 4; i += 256)
+            reinterpret_cast<float4*>(&s_acc[0][0][0])[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int i = lane; i < nb; i += GS_WAVE) s_has[w][i] = 0u;
         __syncthreads();
-        for (int32_t j = nb - 1; j >= 0; --j) {
+        const int32_t jtop = min(nb, (int32_t)wstop - lo) - 1;
+        for (int32_t j = jtop; j >= 0; --j) {
             const uint32_t e = (uint32_t)(lo + j);
-            float v[9];
-#pragma unroll
-            for (int k = 0; k < 9; ++k) v[k] = 0.0f;
-            bool live = false;
-            if (e < stop) {
-                const float4 r0 = s0[j], r1 = s1[j];
-                const float dx = pxc - r0.x, dy = pyc - r0.y;
-                const float power =
-                    -0.5f * (r1.x * dx * dx + 2.0f * r1.y * dx * dy + r1.z * dy * dy);
-                const float wgt = __expf(power < 0.0f ? power : 0.0f);
-                const float raw = r0.z * wgt;
-                const bool clamp = raw > bp.alpha_max;
-                const float alpha = clamp ? bp.alpha_max : raw;
-                if (alpha >= bp.alpha_min) {
-                    live = true;
-                    const float4 c = s2[j];
-                    const float om = 1.0f - alpha;
-                    const float rom = __builtin_amdgcn_rcpf(om);
-                    T = T * rom;
-                    const float dalpha =
-                        T * ((c.x - b0) * g0 + (c.y - b1) * g1 + (c.z - b2) * g2) - tbg * rom;
-                    const float at = alpha * T;
-                    v[6] = at * g0;
-                    v[7] = at * g1;
-                    v[8] = at * g2;
-                    if (!clamp) {
-                        v[5] = dalpha * wgt;
-                        const float dp = power <= 0.0f ? dalpha * raw : 0.0f;
-                        v[0] = dp * (r1.x * dx + r1.y * dy);
-                        v[1] = dp * (r1.y * dx + r1.z * dy);
-                        v[2] = -0.5f * dp * dx * dx;
-                        v[3] = -dp * dx * dy;
-                        v[4] = -0.5f * dp * dy * dy;
-                    }
-                    b0 = alpha * c.x + om * b0;
-                    b1 = alpha * c.y + om * b1;
-                    b2 = alpha * c.z + om * b2;
-                }
-            }
+            const float4 r0 = s0[j], r1 = s1[j];
+            const float dx = pxc - r0.x, dy = pyc - r0.y;
+            const float power = -0.5f * (r1.x * dx * dx + 2.0f * r1.y * dx * dy + r1.z * dy * dy);
+            const float wgt = __expf(power < 0.0f ? power : 0.0f);
+            const float raw = r0.z * wgt;
+            const bool clamp = raw > bp.alpha_max;
+            const float alpha = fminf(raw, bp.alpha_max);  // raw is finite: = clamp ? max : raw
+            const bool live = e < stop && alpha >= bp.alpha_min;
             const uint64_t any = __ballot(live);
             if (any) {
+                const float4 c = s2[j];
+                const float om = 1.0f - alpha;
+                const float rom = __builtin_amdgcn_rcpf(om);
+                const float Tn = T * rom;
+                const float dalpha =
+                    Tn * ((c.x - b0) * g0 + (c.y - b1) * g1 + (c.z - b2) * g2) - tbg * rom;
+                // a lane that does not blend the entry contributes exact zeros
+                const float at = live ? alpha * Tn : 0.0f;
+                const float d5 = (live && !clamp) ? dalpha : 0.0f;  // no gradient through the clamp
+                const float dp = (power <= 0.0f ? d5 : 0.0f) * raw;
+                float v[9];
+                v[0] = dp * (r1.x * dx + r1.y * dy);
+                v[1] = dp * (r1.y * dx + r1.z * dy);
+                v[2] = -0.5f * dp * dx * dx;
+                v[3] = -dp * dx * dy;
+                v[4] = -0.5f * dp * dy * dy;
+                v[5] = d5 * wgt;
+                v[6] = at * g0;
+                v[7] = at * g1;
+                v[8] = at * g2;
+                const float nb0 = alpha * c.x + om * b0;
+                const float nb1 = alpha * c.y + om * b1;
+                const float nb2 = alpha * c.z + om * b2;
+                T = live ? Tn : T;
+                b0 = live ? nb0 : b0;
+                b1 = live ? nb1 : b1;
+                b2 = live ? nb2 : b2;
 #pragma unroll
-                for (int k = 0; k < 9; ++k) v[k] = row_fsum(v[k]);
-                if ((lane & 15) == 0) {
+                for (int k = 0; k < 9; ++k) {
+                    v[k] = group_fsum(v[k]);
+                    // keep the last step in every lane (one DPP add) rather than
+                    // a DPP move for every lane plus an add in the leaders' branch
+                    asm volatile("" : : "v"(v[k]));
+                }
+                if (leader) {
 #pragma unroll
-                    for (int k = 0; k < 9; ++k) atomicAdd(&s_acc[lane >> 4][j][k], v[k]);
+                    for (int k = 0; k < 9; ++k) atomicAdd(acc_lane + (j * 9 + k) * kBwdCopies, v[k]);
                 }
             }
             if (lane == 0) s_has[w][j] = any ? 1u : 0u;
@@ -716,8 +745,12 @@ __global__ __launch_bounds__(256) void k_train_bwd(const float4* __restrict__ tr
             if (has) {
                 float acc[9];
 #pragma unroll
-                for (int k = 0; k < 9; ++k)
-                    acc[k] = (s_acc[0][tid][k] + s_acc[1][tid][k]) + (s_acc[2][tid][k] + s_acc[3][tid][k]);
+                for (int k = 0; k < 9; ++k) {
+                    float a = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < kBwdCopies; ++c) a += s_acc[tid][k][c];
+                    acc[k] = a;
+                }
                 const uint32_t gi = sid[start + lo + tid];
                 float* dst = bp.grad2d + 9 * (size_t)gi;
 #pragma unroll
