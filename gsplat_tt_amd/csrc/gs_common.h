@@ -179,14 +179,19 @@ constexpr uint64_t kLbAgg = 1ull << 62;
 constexpr uint64_t kLbInc = 2ull << 62;
 constexpr uint64_t kLbVal = (1ull << 62) - 1;
 
-__device__ __forceinline__ uint64_t lookback_exclusive(uint64_t* state, uint32_t vid,
-                                                      uint64_t aggregate, uint32_t* ctl) {
+// The first half of lookback_exclusive: publishes the partition's aggregate
+// (partition 0: its inclusive prefix), so that successors can walk past it
+// while this partition does other work before its own walk.
+__device__ __forceinline__ void lookback_publish(uint64_t* state, uint32_t vid,
+                                                 uint64_t aggregate) {
+    if (lane_id() == 0) st_agent(&state[vid], (vid == 0 ? kLbInc : kLbAgg) | aggregate);
+}
+
+// The second half: the walk over the predecessors, then the inclusive prefix.
+__device__ __forceinline__ uint64_t lookback_walk(uint64_t* state, uint32_t vid,
+                                                  uint64_t aggregate, uint32_t* ctl) {
     const int l = lane_id();
-    if (vid == 0) {
-        if (l == 0) st_agent(&state[0], kLbInc | aggregate);
-        return 0;
-    }
-    if (l == 0) st_agent(&state[vid], kLbAgg | aggregate);
+    if (vid == 0) return 0;
     uint32_t limit = 0;  // read at the first wait
     uint64_t excl = 0;
     int64_t base = (int64_t)vid - 1;
@@ -228,6 +233,12 @@ __device__ __forceinline__ uint64_t lookback_exclusive(uint64_t* state, uint32_t
         st_agent(&state[vid], kLbInc | (excl + aggregate));
     }
     return excl;
+}
+
+__device__ __forceinline__ uint64_t lookback_exclusive(uint64_t* state, uint32_t vid,
+                                                      uint64_t aggregate, uint32_t* ctl) {
+    lookback_publish(state, vid, aggregate);
+    return lookback_walk(state, vid, aggregate, ctl);
 }
 
 }  // namespace gs

@@ -97,6 +97,9 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
     __shared__ uint32_t s_cnt[kProjItems][kProjThreads / GS_WAVE];
     __shared__ uint32_t s_hist[4][256];
     __shared__ uint64_t s_excl;
+    // each item's projected values, held here over the colour evaluation (in
+    // registers they would leave one workgroup per CU instead of two)
+    __shared__ float4 s_iv[2][kProjItems][kProjThreads];
     const int tid = threadIdx.x;
     const int w = tid / GS_WAVE;
     const int lane = lane_id();
@@ -230,6 +233,8 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
             }
         }
         if (i < n && valid_mask != nullptr) valid_mask[i] = valid[it] ? 1 : 0;
+        s_iv[0][it][tid] = make_float4(vmx[it], vmy[it], vrx[it], vry[it]);
+        s_iv[1][it][tid] = make_float4(va[it], vb[it], vc[it], vtz[it]);
         bal[it] = __ballot(valid[it]);
         if (lane == 0) s_cnt[it][w] = (uint32_t)__popcll(bal[it]);
         if (part_hist != nullptr) {
@@ -256,8 +261,38 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
             total += s_cnt[it][ww];
         }
     }
+    // The partition's count goes out first; the colours of the valid items
+    // (the SH records, the kernel's largest reads) are evaluated before the
+    // walk over the predecessors, so that the walk finds them mostly done.
+    if (w == 0) lookback_publish(lb_state, vid, total);
+    float vr[kProjItems], vg[kProjItems], vbl[kProjItems];
+#pragma unroll
+    for (int it = 0; it < kProjItems; ++it) {
+        vr[it] = vg[it] = vbl[it] = 0.0f;
+        if (!valid[it]) continue;
+        const int64_t i = base + it * kProjThreads + tid;
+        float rgb[3];
+        if (DEG < 0) {
+            rgb[0] = s.sh[i * 3 + 0];
+            rgb[1] = s.sh[i * 3 + 1];
+            rgb[2] = s.sh[i * 3 + 2];
+        } else {
+            const float dx = s.mean[0][i] - p.ccx;
+            const float dy = s.mean[1][i] - p.ccy;
+            const float dz = s.mean[2][i] - p.ccz;
+            const float nrm = sqrtf(dx * dx + dy * dy + dz * dz);
+            constexpr int D = DEG < 0 ? 0 : DEG;
+            sh_eval<D>(s.sh + i * (3 * (D + 1) * (D + 1)), dx / nrm, dy / nrm, dz / nrm,
+                       p.sh_clamp_hi, rgb);
+        }
+        vr[it] = rgb[0];
+        vg[it] = rgb[1];
+        vbl[it] = rgb[2];
+        // one item's SH record in flight at a time (registers)
+        __builtin_amdgcn_sched_barrier(0);
+    }
     if (w == 0) {
-        const uint64_t excl = lookback_exclusive(lb_state, vid, total, p.ctl);
+        const uint64_t excl = lookback_walk(lb_state, vid, total, p.ctl);
         if (lane == 0) {
             s_excl = excl;
             if (vid == gridDim.x - 1) *count_out = (uint32_t)(excl + total);
@@ -272,6 +307,15 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
         if (!valid[it]) continue;
         const int64_t i = base + it * kProjThreads + tid;
         const uint64_t m = excl + my_off[it] + (uint64_t)__popcll(bal[it] & lt_mask);
+        const float4 q0 = s_iv[0][it][tid], q1 = s_iv[1][it][tid];
+        vmx[it] = q0.x;
+        vmy[it] = q0.y;
+        vrx[it] = q0.z;
+        vry[it] = q0.w;
+        va[it] = q1.x;
+        vb[it] = q1.y;
+        vc[it] = q1.z;
+        vtz[it] = q1.w;
         const float a = va[it], b = vb[it], c = vc[it];
         out.rc[2 * m + 0] = make_float4(vmx[it], vmy[it], vrx[it], vry[it]);
         out.rc[2 * m + 1] = make_float4(a, b, c, s.m2thr[i]);
@@ -295,24 +339,10 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
             xh = rd * sqrtf(fmax_std(a, 0.0f));
             yh = rd * sqrtf(fmax_std(c, 0.0f));
         }
-        float rgb[3];
-        if (DEG < 0) {
-            rgb[0] = s.sh[i * 3 + 0];
-            rgb[1] = s.sh[i * 3 + 1];
-            rgb[2] = s.sh[i * 3 + 2];
-        } else {
-            const float dx = s.mean[0][i] - p.ccx;
-            const float dy = s.mean[1][i] - p.ccy;
-            const float dz = s.mean[2][i] - p.ccz;
-            const float nrm = sqrtf(dx * dx + dy * dy + dz * dz);
-            constexpr int D = DEG < 0 ? 0 : DEG;
-            sh_eval<D>(s.sh + i * (3 * (D + 1) * (D + 1)), dx / nrm, dy / nrm, dz / nrm,
-                       p.sh_clamp_hi, rgb);
-        }
         const float op = p.has_opac ? s.opac[i] : 1.0f;
         out.brec[m * 3 + 0] = make_float4(vmx[it], vmy[it], xh, yh);
         out.brec[m * 3 + 1] = make_float4(ci_a, ci_b, ci_c, lt);
-        out.brec[m * 3 + 2] = make_float4(rgb[0], rgb[1], rgb[2], op);
+        out.brec[m * 3 + 2] = make_float4(vr[it], vg[it], vbl[it], op);
         if (out.src != nullptr) out.src[m] = (uint32_t)i;
     }
 }
