@@ -36,7 +36,7 @@ EXPORTED = (
     "gs_render_out_ring", "gs_out_release", "gs_out_ring_config", "gs_out_ring_info",
     "gs_set_chunk_cull",
     "gs_frame_readback", "gs_frame_readback_info", "gs_set_cull_stats", "gs_set_spin_limit",
-    "gs_set_graphs",
+    "gs_set_graphs", "gs_set_pair_limit", "gs_overflow_next_floor",
     "gs_graph_counts",
     "gs_sort_tile_depth_dev", "gs_last_ranges_ms",
     "gs_sort_tile_depth_noalloc",
@@ -71,7 +71,8 @@ class GsStats(ctypes.Structure):
                 ("blend_batches", ctypes.c_int64), ("blend_iters", ctypes.c_int64),
                 ("blend_kept", ctypes.c_int64), ("blend_max_iters", ctypes.c_int64),
                 ("chunks_skipped", ctypes.c_int64), ("pairs_dropped_mb", ctypes.c_int64),
-                ("pairs_kept_mb", ctypes.c_int64)]
+                ("pairs_kept_mb", ctypes.c_int64), ("contrib_floor", ctypes.c_float),
+                ("floor_retries", ctypes.c_int32)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
@@ -140,6 +141,11 @@ def make_train_cfg(near=0.2, lowpass=0.3, alpha_max=0.99, alpha_min=1.0 / 255.0,
 _LIB = None
 
 
+def overflow_next_floor(floor: float, max_n: int, cap: int) -> float:
+    """The floor ladder's next contribution floor (gs_overflow_next_floor)."""
+    return float(load_library().gs_overflow_next_floor(float(floor), int(max_n), int(cap)))
+
+
 def load_library():
     """Load libgsplat_hip.so (raises OSError when it was not built)."""
     global _LIB
@@ -151,6 +157,9 @@ def load_library():
         L.gs_destroy.restype = None
         L.gs_out_release.argtypes = [ctypes.c_uint64]
         L.gs_set_spin_limit.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
+        L.gs_set_pair_limit.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
+        L.gs_overflow_next_floor.restype = ctypes.c_float
+        L.gs_overflow_next_floor.argtypes = [ctypes.c_float, ctypes.c_uint32, ctypes.c_uint32]
         L.gs_last_ranges_ms.restype = ctypes.c_float
         L.gs_last_ranges_ms.argtypes = [ctypes.c_void_p]
         for name in EXPORTED:
@@ -385,6 +394,12 @@ class Context:
         r = ctypes.c_int64(0)
         _check(self._L.gs_graph_counts(self._c, ctypes.byref(c), ctypes.byref(r)))
         return c.value, r.value
+
+    def set_pair_limit(self, limit: int = 0):
+        """Most candidate pairs a rendered frame may hold (0: 2^32-1). A frame with
+        more is rendered again at a coarser contribution floor (gs_stats
+        contrib_floor / floor_retries)."""
+        _check(self._L.gs_set_pair_limit(self._c, ctypes.c_uint32(limit)))
 
     def set_spin_limit(self, limit: int = 0):
         """Spin limit of the kernels' bounded look-back waits (0: default); a tiny

@@ -152,6 +152,19 @@ int dval_idx_bits(int64_t n) {
     return b <= 28 ? b : 0;
 }
 
+// The coarser-floor ladder of a frame whose candidate pairs exceed the pair
+// limit (render/host/overflow_retry.h:26-61): a Gaussian reaches a tile while
+// 2 ln(o / floor) >= d^2, so the pair count grows roughly with L = ln(1 / floor);
+// the next floor scales L by 0.9 cap / max_n and at least doubles the floor.
+constexpr int kFloorRetries = 8;
+constexpr float kFloorMax = 0.5f;
+float next_contrib_floor(float floor, uint32_t max_n, uint32_t cap) {
+    const double f = std::min(std::max((double)floor, 1.0 / 1048576.0), (double)kFloorMax);
+    const double scale = 0.9 * (double)cap / (double)std::max(max_n, cap);
+    const double by_model = std::exp(std::log(f) * scale);  // exp(-L scale)
+    return (float)std::min(std::max(by_model, 2.0 * f), (double)kFloorMax);
+}
+
 }  // namespace
 
 struct gs_ctx {
@@ -198,6 +211,8 @@ struct gs_ctx {
     // limit): words C_CTL.. of the frame counters, or of b_cnt for the stage
     // entry points.
     uint32_t spin_limit = 0;   // 0: the kernels' default (gs_set_spin_limit)
+    uint32_t pair_limit = 0xFFFFFFFFu;  // most candidate pairs a frame holds (gs_set_pair_limit)
+    gs_ctx* owner = nullptr;   // a frame slot's first slot, whose opacity terms it shares
     bool cull_stats = false;   // microblock-cull statistics per frame (gs_set_cull_stats)
     bool graphs = true;        // batch frames replayed from captured graphs (gs_set_graphs)
     bool batch_frame = false;  // render_begin is enqueueing a gs_render_batch frame
@@ -573,6 +588,8 @@ struct gs_ctx {
         size_t bytes = 0;
         int64_t T = 0;
         int tiles_x = 0, tiles_y = 0, attempt = 0;
+        int floor_retries = 0;     // re-renders at a coarser contribution floor
+        gs_view asked{};           // the view as the caller gave it
         int64_t batch_index = -1;  // index in the gs_render_batch call (-1: another call)
         bool replayed = false;     // the last attempt replayed a captured graph
         gs_stats* stats = nullptr;
@@ -604,6 +621,7 @@ struct gs_ctx {
         tr.fwd_valid = false;  // the frame buffers are about to be reused
         rb_valid = false;
         check_view(v);
+        pend.asked = *v;
         REQUIRE(out != nullptr, "render: null output");
         if (!shared_terms) ensure_terms(v);
         if (timing)
@@ -636,7 +654,7 @@ struct gs_ctx {
             if (!out_dev) HIPCHK(hipMemcpyAsync(out, pend.dout, pend.bytes, hipMemcpyDeviceToHost, st));
             return;
         }
-        if (pair_cap == 0) pair_cap = default_pair_cap(sd.n);
+        if (pair_cap == 0) pair_cap = std::min<uint64_t>(default_pair_cap(sd.n), pair_limit);
         enqueue_attempt();
     }
 
@@ -656,20 +674,42 @@ struct gs_ctx {
         for (;;) {
             sync();
             if (pend.empty) break;
+            // candidates of the last attempt (0xFFFFFFFF: more than 2^32-2)
             const uint32_t p_pre = h_pin[C_PPRE];
-            if (p_pre == 0xFFFFFFFFu) {
-                pend.active = false;
-                throw GsError(GS_E_CAPACITY, "render: more than 2^32-1 candidate pairs");
-            }
-            if (p_pre <= pair_cap) break;
-            if (pend.attempt != 0) {
+            if (p_pre != 0xFFFFFFFFu && p_pre <= pair_cap) break;
+            if (pend.attempt > 2 * kFloorRetries + 2) {
                 pend.active = false;
                 throw GsError(GS_E_INVALID, "render: pair capacity did not converge");
             }
             ++pend.attempt;
-            pair_cap = std::min<uint64_t>(0xFFFFFFFFull, (uint64_t)p_pre + p_pre / 8 + 4096);
+            if (p_pre != 0xFFFFFFFFu && p_pre <= pair_limit) {
+                // the same frame again with room for its pairs
+                pair_cap = std::min<uint64_t>(pair_limit, (uint64_t)p_pre + p_pre / 8 + 4096);
+                enqueue_attempt();
+                continue;
+            }
+            // more candidates than the limit: the whole frame again at a
+            // coarser floor (render/host/render.cpp:537-565)
+            const float f = std::max(pend.v.contrib_floor, pend.v.mb_contrib_floor);
+            if (pend.v.cull_disabled || pend.floor_retries >= kFloorRetries || !(f < kFloorMax)) {
+                restore_terms();
+                pend.active = false;
+                throw GsError(GS_E_CAPACITY,
+                              p_pre == 0xFFFFFFFFu
+                                  ? "render: more than 2^32-1 candidate pairs"
+                                  : "render: more candidate pairs than the pair limit");
+            }
+            const float next = next_contrib_floor(f, p_pre, pair_limit);
+            pend.v.contrib_floor = next;
+            pend.v.mb_contrib_floor = next;
+            ++pend.floor_retries;
+            // every slot reads the one set of opacity terms: none may be running
+            gs_ctx* o = owner ? owner : this;
+            o->sync_slots();
+            o->ensure_terms(&pend.v);
             enqueue_attempt();
         }
+        restore_terms();
         pend.active = false;
         s.pairs_dropped_mb = -1;
         s.pairs_kept_mb = -1;
@@ -708,7 +748,22 @@ struct gs_ctx {
             s.pairs_dropped_mb = cull_stats ? 0 : -1;
             s.pairs_kept_mb = cull_stats ? 0 : -1;
         }
+        s.contrib_floor = pend.v.contrib_floor;
+        s.floor_retries = pend.floor_retries;
         if (pend.stats) *pend.stats = s;
+    }
+
+    // After a frame rendered at a coarser floor: the opacity terms of the floor
+    // the caller asked for (later frames, and the other slots, expect them).
+    void restore_terms() {
+        if (pend.floor_retries == 0) return;
+        gs_ctx* o = owner ? owner : this;
+        o->sync_slots();
+        o->ensure_terms(&pend.asked);
+    }
+    void sync_slots() {
+        sync();
+        for (gs_ctx* p : peers) p->sync();
     }
 
     // Frame slots 1..count-1: each its own stream and frame buffers, with this
@@ -729,6 +784,8 @@ struct gs_ctx {
             p->timing = timing;
             p->blend_counts = blend_counts;
             p->spin_limit = spin_limit;
+            p->pair_limit = pair_limit;
+            p->owner = this;
             p->cull_stats = cull_stats;
             p->graphs = graphs;
             p->sd = sd;
@@ -1784,6 +1841,20 @@ int gs_set_spin_limit(gs_ctx* ctx, uint32_t limit) {
         ctx->drain_spec();
         ctx->spin_limit = limit;
     });
+}
+
+int gs_set_pair_limit(gs_ctx* ctx, uint32_t limit) {
+    return guard([&] {
+        REQUIRE(ctx, "null ctx");
+        ctx->drain_spec();
+        ctx->pair_limit = limit == 0 ? 0xFFFFFFFFu : limit;
+        ctx->pair_cap = std::min<uint64_t>(ctx->pair_cap, ctx->pair_limit);
+        for (gs_ctx* p : ctx->peers) p->pair_cap = std::min<uint64_t>(p->pair_cap, ctx->pair_limit);
+    });
+}
+
+float gs_overflow_next_floor(float floor, uint32_t max_n, uint32_t cap) {
+    return next_contrib_floor(floor, max_n, cap);
 }
 
 int gs_render_next(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device,

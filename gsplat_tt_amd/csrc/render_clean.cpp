@@ -46,6 +46,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -113,6 +114,9 @@ double env_double(const char* name, double dflt) {
 }
 bool g_chunk_on = false;
 double g_chunk_k = 1.5;
+// GSPLAT_TT_PAIR_LIMIT: the pair limit of gs_set_pair_limit (0: none), for
+// tests of the overflow floor ladder (the reference's GSPLAT_TT_TEST_TILE_CAP)
+unsigned g_pair_limit = 0u;
 int out_zerocopy_slots() {
     const unsigned n = env_uint("GSPLAT_TT_OUT_ZEROCOPY_SLOTS", 4u);
     return n < 1u ? 1 : (int)std::min(n, 1024u);
@@ -215,6 +219,11 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
             g_chunk_on = chunk_on;
             g_chunk_k = chunk_k;
         }
+        const unsigned pair_limit = env_uint("GSPLAT_TT_PAIR_LIMIT", 0u);
+        if (pair_limit != g_pair_limit) {
+            check(gs_set_pair_limit(c, pair_limit));
+            g_pair_limit = pair_limit;
+        }
         sc.version = g_scene_version;
         check(gs_scene_set(c, &sc));
         // the next view: this call's parameters at the announced pose
@@ -257,6 +266,11 @@ py::tuple render_view(farr means, farr cov3d, farr opacities, farr colors, farr 
                                                   : py::dtype::of<float>();
         image = py::array(dt, shape, strides, ring_img.data, keep);
     }
+    if (st.floor_retries > 0)
+        std::fprintf(stderr,
+                     "[render_clean] pair overflow: the view was rendered at contrib floor "
+                     "1/%.0f after %d retries\n",
+                     1.0 / st.contrib_floor, st.floor_retries);
     py::dict stats;
     stats["num_visible"] = st.num_visible;
     stats["num_entries"] = st.num_entries;

@@ -87,6 +87,11 @@ typedef struct gs_stats {
      * gs_set_cull_stats is on; -1 otherwise. */
     int64_t pairs_dropped_mb;  /* pairs that no microblock keeps */
     int64_t pairs_kept_mb;     /* kept (pair, microblock) pairs */
+    /* The contribution floor the frame was rendered at: the view's, or a
+     * coarser one after floor_retries re-renders because its candidate pairs
+     * exceeded the pair limit (gs_set_pair_limit; render/host/render.cpp:537-565). */
+    float contrib_floor;
+    int32_t floor_retries;
 } gs_stats;
 
 /* ---- context -------------------------------------------------------- */
@@ -154,6 +159,22 @@ int gs_set_cull_stats(gs_ctx* ctx, int on);
  * results; every kernel still exits normally. A tiny limit is for tests of that
  * error path only. */
 int gs_set_spin_limit(gs_ctx* ctx, uint32_t limit);
+/* The most candidate pairs a rendered frame's pair buffer may hold (0: the
+ * default, 2^32-1; training steps are not limited). The buffer grows to a
+ * frame's count up to this limit; a frame with
+ * more candidates is rendered again, the whole frame at a coarser contribution
+ * floor (both floors set to gs_overflow_next_floor of the coarser one), up to
+ * 8 times and while the floor is below 1/2, the floor used reported in
+ * gs_stats (render/host/overflow_retry.h:26-61, render.cpp:537-565, where the
+ * limit is a sort bucket's record capacity). With the cull disabled, or past
+ * the ladder, the call fails with GS_E_CAPACITY. The opacity terms of the
+ * coarser floor are computed for that frame only (every frame slot is waited
+ * for first, since the slots share them). */
+int gs_set_pair_limit(gs_ctx* ctx, uint32_t limit);
+/* The next contribution floor after a frame of max_n candidates against a
+ * capacity of cap (max_n > cap): L = ln(1 / floor) scaled by 0.9 cap / max_n,
+ * and at least twice the floor, at most 1/2 (render/host/overflow_retry.h:35-42). */
+float gs_overflow_next_floor(float floor, uint32_t max_n, uint32_t cap);
 /* gs_render_batch frames replayed from HIP graphs (on by default): each frame
  * slot captures its frame's kernels once per frame shape and replays them for
  * its later frames of that shape with the new camera (no counterpart in the

@@ -58,7 +58,8 @@ int main(void) {
   P(gs_train_proj, visible)
   P(gs_scene, n) P(gs_scene, version) P(gs_view, image_height) P(gs_view, tile_size)
   P(gs_view, k_cap) P(gs_view, out_format) P(gs_view, sh_clamp_hi)
-  P(gs_stats, ms_project) P(gs_stats, blend_max_iters)
+  P(gs_stats, ms_project) P(gs_stats, blend_max_iters) P(gs_stats, contrib_floor)
+  P(gs_stats, floor_retries)
   return 0;
 }
 """
