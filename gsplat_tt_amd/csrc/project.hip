@@ -288,8 +288,6 @@ __global__ __launch_bounds__(kProjThreads) void k_project(SceneDev s, ProjParams
         vr[it] = rgb[0];
         vg[it] = rgb[1];
         vbl[it] = rgb[2];
-        // one item's SH record in flight at a time (registers)
-        __builtin_amdgcn_sched_barrier(0);
     }
     if (w == 0) {
         const uint64_t excl = lookback_walk(lb_state, vid, total, p.ctl);
