@@ -670,17 +670,28 @@ struct gs_ctx {
 
     void render_end() {
         REQUIRE(pend.active, "render: no frame in flight");
-        gs_stats s{};
+        try {
+            settle_attempts();
+        } catch (...) {
+            // no frame stays pending, and the caller's floor's terms are back
+            pend.active = false;
+            restore_terms();
+            throw;
+        }
+        finish_frame();
+    }
+
+    // Waits for the frame, re-running it while its candidate pairs do not fit:
+    // with a grown pair buffer up to the pair limit, past it at a coarser floor.
+    void settle_attempts() {
         for (;;) {
             sync();
             if (pend.empty) break;
             // candidates of the last attempt (0xFFFFFFFF: more than 2^32-2)
             const uint32_t p_pre = h_pin[C_PPRE];
             if (p_pre != 0xFFFFFFFFu && p_pre <= pair_cap) break;
-            if (pend.attempt > 2 * kFloorRetries + 2) {
-                pend.active = false;
+            if (pend.attempt > 2 * kFloorRetries + 2)
                 throw GsError(GS_E_INVALID, "render: pair capacity did not converge");
-            }
             ++pend.attempt;
             if (p_pre != 0xFFFFFFFFu && p_pre <= pair_limit) {
                 // the same frame again with room for its pairs
@@ -691,14 +702,11 @@ struct gs_ctx {
             // more candidates than the limit: the whole frame again at a
             // coarser floor (render/host/render.cpp:537-565)
             const float f = std::max(pend.v.contrib_floor, pend.v.mb_contrib_floor);
-            if (pend.v.cull_disabled || pend.floor_retries >= kFloorRetries || !(f < kFloorMax)) {
-                restore_terms();
-                pend.active = false;
+            if (pend.v.cull_disabled || pend.floor_retries >= kFloorRetries || !(f < kFloorMax))
                 throw GsError(GS_E_CAPACITY,
                               p_pre == 0xFFFFFFFFu
                                   ? "render: more than 2^32-1 candidate pairs"
                                   : "render: more candidate pairs than the pair limit");
-            }
             const float next = next_contrib_floor(f, p_pre, pair_limit);
             pend.v.contrib_floor = next;
             pend.v.mb_contrib_floor = next;
@@ -709,6 +717,11 @@ struct gs_ctx {
             o->ensure_terms(&pend.v);
             enqueue_attempt();
         }
+    }
+
+    // The frame's statistics and readback state, once its last attempt fit.
+    void finish_frame() {
+        gs_stats s{};
         restore_terms();
         pend.active = false;
         s.pairs_dropped_mb = -1;
