@@ -38,7 +38,7 @@ EXPORTED = (
     "gs_frame_readback", "gs_frame_readback_info", "gs_set_cull_stats", "gs_set_spin_limit",
     "gs_set_graphs", "gs_set_pair_limit", "gs_overflow_next_floor",
     "gs_graph_counts",
-    "gs_sort_tile_depth_dev", "gs_last_ranges_ms",
+    "gs_sort_tile_depth_dev", "gs_sort_tile_depth_ids_dev", "gs_last_ranges_ms",
     "gs_sort_tile_depth_noalloc",
 )
 TRAIN_PARAMS = ("means", "log_scales", "quats", "opacity_logits", "sh")
@@ -415,6 +415,21 @@ class Context:
                                               ctypes.c_void_p(vals_ptr), ctypes.c_int64(n),
                                               ctypes.c_int64(num_tiles),
                                               ctypes.c_void_p(ranges_ptr), ctypes.byref(passes)))
+        return passes.value
+
+    def sort_tile_depth_ids_dev(self, keys_ptr: int, ids_ptr: int, n: int, num_tiles: int,
+                                ranges_ptr: int, num_gaussians: int = 0):
+        """The same sort with sort_and_bin's outputs only: the ids at ids_ptr
+        (each below num_gaussians, sort_and_bin's M; 0: any 32-bit id) come back
+        in sorted key order, the keys at keys_ptr are overwritten, and ranges_ptr
+        receives the per-tile [start, end)."""
+        passes = ctypes.c_int()
+        _check(self._L.gs_sort_tile_depth_ids_dev(self._c, ctypes.c_void_p(keys_ptr),
+                                                  ctypes.c_void_p(ids_ptr), ctypes.c_int64(n),
+                                                  ctypes.c_int64(num_gaussians),
+                                                  ctypes.c_int64(num_tiles),
+                                                  ctypes.c_void_p(ranges_ptr),
+                                                  ctypes.byref(passes)))
         return passes.value
 
     def last_ranges_ms(self) -> float:

@@ -203,6 +203,7 @@ struct gs_ctx {
     DevBuf b_offs, b_bstart, b_pair_tile, b_pair_id, b_ranges, b_out;
     DevBuf b_kalt, b_valt, b_hist, b_state, b_lb, b_cnt;
     DevBuf b_tmp_a, b_tmp_b, b_tmp_c, b_evals;
+    DevBuf b_tcnt;  // per-tile key counts of gs_sort_tile_depth_ids_dev
     std::vector<uint64_t> h_evals = std::vector<uint64_t>(64 * 8);
     uint32_t* h_pin = nullptr;  // pinned: counters + histograms
     gs::SortTemp sort;
@@ -226,6 +227,8 @@ struct gs_ctx {
     static void ctl_check(uint32_t flags, const char* what) {
         if (flags & gs::kErrKeyRange)
             throw GsError(GS_E_INVALID, std::string(what) + ": a key's tile id is >= num_tiles");
+        if (flags & gs::kErrValRange)
+            throw GsError(GS_E_INVALID, std::string(what) + ": an id is >= num_gaussians");
         if (flags & gs::kErrCapacity)
             throw GsError(GS_E_CAPACITY, std::string(what) + ": candidate pairs past the capacity");
         if (flags != 0u)
@@ -251,7 +254,7 @@ struct gs_ctx {
                           &b_ranges, &b_out, &b_kalt, &b_valt, &b_hist, &b_state, &b_lb, &b_cnt,
                           &b_tmp_a, &b_tmp_b, &b_tmp_c, &b_evals, &b_frame, &b_phist_proj,
                           &b_phist_emit, &b_pchunk, &b_poffs, &b_spec, &b_chunk_box,
-                          &b_skip})
+                          &b_skip, &b_tcnt})
             b->release();
         if (h_pin) (void)hipHostFree(h_pin);
         ring.reset();  // held images stay valid until their leases are released
@@ -1039,7 +1042,7 @@ struct gs_ctx {
                                         cnt + C_PPRE, 4, 0, tile_bits(T), fr + kFrTileHist,
                                         cnt + C_TSORT_TICKETS, sort, st, false, &tiles_sorted,
                                         &ids_sorted, cnt + C_P, want_keys ? nullptr : L.tcnt,
-                                        b_poffs.as<uint32_t>()));
+                                        b_poffs.as<uint32_t>(), (uint32_t)T));
         if (want_keys) {
             HIPCHK(gs::launch_tile_bounds(static_cast<uint32_t*>(tiles_sorted), L.pcap, cnt + C_P,
                                           b_ranges.as<uint32_t>(), T, st));
@@ -2234,6 +2237,62 @@ int gs_sort_tile_depth_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t 
                 if (!ctx->ev[i]) HIPCHK(hipEventCreate(&ctx->ev[i]));
         sort_u64_dev(ctx, keys, vals, n, 0, 32 + tile_bits(num_tiles), num_tiles, tile_ranges,
                      passes_out);
+    });
+}
+
+int gs_sort_tile_depth_ids_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* ids, int64_t n,
+                               int64_t num_gaussians, int64_t num_tiles, uint32_t* tile_ranges,
+                               int* passes_out) {
+    return guard([&] {
+        REQUIRE(ctx && keys && ids && tile_ranges, "null argument");
+        REQUIRE(n >= 0 && n < ((int64_t)1 << 32) - 1, "n out of range");
+        REQUIRE(num_gaussians >= 0 && num_gaussians <= ((int64_t)1 << 32),
+                "num_gaussians out of range");
+        REQUIRE(num_tiles >= 1 && num_tiles <= ((int64_t)1 << 31), "num_tiles out of range");
+        if (ctx->timing)
+            for (int i : {6, 7})
+                if (!ctx->ev[i]) HIPCHK(hipEventCreate(&ctx->ev[i]));
+        const int tb = tile_bits(num_tiles);
+        // the tile counts of the last pass give the ranges (one workgroup scan)
+        if (num_tiles > ((int64_t)1 << 24)) {
+            sort_u64_dev(ctx, keys, ids, n, 0, 32 + tb, num_tiles, tile_ranges, passes_out);
+            return;
+        }
+        HIPCHK(hipSetDevice(ctx->device));
+        ctx->drain_spec();
+        ctx->rb_valid = false;
+        ctx->ensure_counters();
+        ctx->ensure_sort(n, 8);
+        ctx->b_tcnt.ensure((size_t)num_tiles * 4);
+        uint32_t* ctl = ctx->b_cnt.as<uint32_t>() + gs_ctx::C_CTL;
+        ctx->ctl_reset(ctl);
+        ctx->sort.ctl = ctl;
+        uint32_t* tcnt = ctx->b_tcnt.as<uint32_t>();
+        uint32_t* key_err = ctl + 2;  // a key-range flag that does not stop the passes
+        HIPCHK(gs::launch_fill_u32(key_err, 0u, 1, ctx->st));
+        HIPCHK(gs::launch_fill_u32(ctx->sort.hist, 0u, gs::sort_hist_words(), ctx->st));
+        HIPCHK(gs::launch_fill_u32(tcnt, 0u, (size_t)num_tiles, ctx->st));
+        int passes = 0;
+        const hipError_t e = gs::radix_sort_ids_dev_chain(
+            keys, ids, n, tb, (uint64_t)num_gaussians, (uint32_t)num_tiles, tcnt, key_err,
+            ctx->sort.hist, ctx->sort.hist + 8 * 256, ctx->sort, ctx->st, &passes);
+        if (e == hipErrorNotSupported) {
+            sort_u64_dev(ctx, keys, ids, n, 0, 32 + tb, num_tiles, tile_ranges, passes_out);
+            return;
+        }
+        HIPCHK(e);
+        const bool timed = ctx->timing;
+        if (timed) HIPCHK(hipEventRecord(ctx->ev[6], ctx->st));
+        HIPCHK(gs::launch_ranges_from_counts(tcnt, num_tiles, tile_ranges, ctx->st));
+        if (timed) HIPCHK(hipEventRecord(ctx->ev[7], ctx->st));
+        HIPCHK(hipMemcpyAsync(ctx->h_pin + 64 + 8 * 256, ctl, 12, hipMemcpyDeviceToHost, ctx->st));
+        ctx->sync();
+        ctx->last_sort_passes = passes;
+        ctx->last_ranges_ms = 0.0f;
+        if (timed) (void)hipEventElapsedTime(&ctx->last_ranges_ms, ctx->ev[6], ctx->ev[7]);
+        if (passes_out) *passes_out = passes;
+        const uint32_t* hw = ctx->h_pin + 64 + 8 * 256;
+        gs_ctx::ctl_check(hw[0] | hw[2], "sort");
     });
 }
 

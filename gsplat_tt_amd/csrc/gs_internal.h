@@ -19,6 +19,7 @@ constexpr uint32_t kErrKeyRange = 2u;  // a sorted key's tile id is past the til
 // the frame's candidate pairs exceed its pair capacity: the later kernels skip
 // their work and the host runs the frame again with a larger capacity
 constexpr uint32_t kErrCapacity = 4u;
+constexpr uint32_t kErrValRange = 8u;  // a sorted value is past its stated bound
 
 // Scene resident in HBM, structure-of-arrays (one coalesced dword stream per
 // attribute). `sh` holds (d+1)^2*3 planes of n floats, plane index k*3+c.
@@ -159,7 +160,8 @@ hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const
                                 void** keys_final, uint32_t** vals_final,
                                 const uint32_t* n_kept_dev = nullptr,
                                 uint32_t* run_cnt = nullptr,
-                                const uint32_t* first_offs = nullptr);
+                                const uint32_t* first_offs = nullptr,
+                                uint32_t run_limit = 0xFFFFFFFFu);
 
 // The 64-bit-key sort of radix_sort_pairs_dev over exactly n keys, with no
 // producer histogram: a histogram kernel counts the first pass's digits and
@@ -169,6 +171,26 @@ hipError_t radix_sort_pairs_dev_chain(uint64_t* keys, uint32_t* vals, int64_t n,
                                       int end_bit, uint32_t* hist, uint32_t* tickets,
                                       SortTemp& tmp, hipStream_t st, void** keys_final,
                                       uint32_t** vals_final);
+
+// The same stable sort of (tile << 32 | depth bits) keys below 2^(32 +
+// tile_bits) with values below val_limit (0: any 32-bit value; the values take
+// val_bits = the bits of val_limit - 1 in the words below), when only the values and the runs
+// of each tile are wanted: once the key bits left to sort and the value fit
+// 64 bits (after q passes of w-bit digits, the q-th writing each key's bits
+// [q * w, ...) above its value as one 64-bit word), the later passes move
+// those words, one store stream instead of two, and the last pass writes the
+// sorted values into vals and counts each tile's keys into run_cnt[tile]
+// (num_tiles words, cleared by the caller) instead of writing keys. The keys
+// buffer is overwritten (scratch). A key with a tile id >= num_tiles or a bit
+// set above the tile field flags kErrKeyRange, a value >= val_limit
+// kErrValRange, in *key_err (a word other than tmp.ctl[0], cleared by the
+// caller: the passes go on).
+// hipErrorNotSupported: the key bits and the value never fit one word before
+// the last pass; the caller sorts the keys whole instead.
+hipError_t radix_sort_ids_dev_chain(uint64_t* keys, uint32_t* vals, int64_t n, int tile_bits,
+                                    uint64_t val_limit, uint32_t num_tiles, uint32_t* run_cnt,
+                                    uint32_t* key_err, uint32_t* hist, uint32_t* tickets,
+                                    SortTemp& tmp, hipStream_t st, int* passes_out);
 
 // Device and stream of a context (gs_api.cpp), for entry points in other units.
 struct CtxInfo {

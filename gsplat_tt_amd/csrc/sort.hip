@@ -74,19 +74,21 @@ __device__ __forceinline__ uint32_t block_excl_scan256(uint32_t v, uint32_t* s_t
     return pre + incl - v;
 }
 
-// Digit histograms of every pass in one read of the keys. Four keys per thread
-// per step keep several loads in flight; per wave and pass, the lanes whose digit
-// equals lane 0's add as one (skewed digits, e.g. the high bits of Zipf tile ids,
-// would otherwise serialise up to 64 lanes on one LDS bin).
+// Digit histograms of up to NP passes in one read of the keys. Four keys per
+// thread per step keep several loads in flight; per wave and pass, the lanes
+// whose digit equals lane 0's add as one (skewed digits, e.g. the high bits of
+// Zipf tile ids, would otherwise serialise up to 64 lanes on one LDS bin).
+// The bins take NP x 4 KB of LDS: one pass's fit eight workgroups per CU, so
+// the whole grid is resident at once.
 constexpr int kHistItems = 4;
-template <typename K>
+template <typename K, int NP = kMaxPasses>
 __global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ keys, int64_t n,
                                                        int begin_bit, int end_bit, int npass,
                                                        int dw, uint32_t* __restrict__ g_hist) {
-    __shared__ uint32_t h[kWaves][kMaxPasses][256];
+    __shared__ uint32_t h[kWaves][NP][256];
     const int w = threadIdx.x / GS_WAVE;
     const int lane = lane_id();
-    for (int i = threadIdx.x; i < kWaves * kMaxPasses * 256; i += kHistThreads)
+    for (int i = threadIdx.x; i < kWaves * NP * 256; i += kHistThreads)
         (&h[0][0][0])[i] = 0;
     __syncthreads();
     constexpr int64_t kStep = (int64_t)kHistThreads * kHistItems;
@@ -104,7 +106,7 @@ __global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ key
         }
         // passes outside, items inside: the items' digit tests of one pass are
         // independent and interleave
-        for (int p = 0; p < npass; ++p) {
+        for (int p = 0; p < min(npass, NP); ++p) {
             const int shift = begin_bit + dw * p;
             const uint32_t mask = (1u << min(dw, end_bit - shift)) - 1u;
             uint32_t d[kHistItems], d0[kHistItems];
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(kHistThreads) void k_hist(const K* __restrict__ key
         }
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < npass * 256; i += kHistThreads) {
+    for (int i = threadIdx.x; i < min(npass, NP) * 256; i += kHistThreads) {
         const int p = i / 256, d = i % 256;
         uint32_t s = 0;
 #pragma unroll
@@ -193,23 +195,45 @@ __device__ __forceinline__ uint32_t digit_walk(DT* state, uint32_t vid, int digi
 // SPLIT: the keys are re-ordered in LDS and written out first, then the values
 // in the same LDS space, so a partition holds only its keys in LDS (larger
 // partitions, fewer look-back links).
-// RUNS (the last pass of a sort of 32-bit keys that index run_cnt): the sorted
-// keys are not written; instead every run of equal keys in the partition (the
-// last pass leaves a partition sorted by all the key bits in LDS) adds its
-// length to run_cnt[key], with at most two atomics per run.
+// RUNS (the last pass of a sort whose keys' high bits index run_cnt): the
+// sorted keys are not written; instead every run of equal key >> run_shift in
+// the partition (the last pass leaves a partition sorted by all the key bits
+// in LDS) adds its length to run_cnt[key >> run_shift], with at most two
+// atomics per run.
 // part_offs (optional, 2^bits words per partition): partition vid's keys of
 // digit d start at part_offs[vid << bits | d] of the output (the digit's base
 // plus the kept keys of that digit in all earlier partitions, counted by the
 // keys' producer): the partition neither publishes nor walks back.
+// NARROW (64-bit keys, split partitions): each key and its value leave as one
+// 64-bit word, (key >> out_shift) << val_bits | value (the key bits the later
+// passes still read, above the value; vout is not written). The words are
+// staged in LDS instead of the keys, so an element's digit, gone from its
+// word, is found from the partition's digit offsets (a start digit per 32
+// elements, then a short forward scan). A key bit lost off the word's top
+// flags kErrKeyRange, a value >= val_limit (when not 0) kErrValRange, in
+// *key_err (val_limit <= 2^val_bits).
+// KONLY (64-bit keys, split partitions): the keys carry their values (the
+// words NARROW writes); vin is not read and, unless RUNS, vout not written.
+// A RUNS run at or past run_limit flags kErrKeyRange in *key_err instead of
+// counting; with KONLY the low val_bits bits of each sorted key go to vout.
+// key_err (nullable) is not the control word:
+// partitions of the same pass that start after the flag still sort and
+// publish (every access stays in bounds whatever the keys), so no look-back
+// wait is left to run into its limit.
 template <typename K, bool IOTA, int THREADS, int ITEMS, bool D32, bool DROP, bool SPLIT,
-          bool RUNS>
+          bool RUNS, bool NARROW = false, bool KONLY = false>
 __global__ __launch_bounds__(THREADS) void k_onesweep(
     const K* __restrict__ kin, const uint32_t* __restrict__ vin, K* __restrict__ kout,
     uint32_t* __restrict__ vout, int64_t n_cap, const uint32_t* __restrict__ n_dev, int shift,
     int bits, const uint32_t* __restrict__ g_hist_pass, void* __restrict__ state_raw,
     uint32_t* __restrict__ ticket, uint32_t epoch, uint32_t* __restrict__ clear_next,
     uint32_t* ctl, uint32_t* __restrict__ next_hist, int next_shift, int next_bits,
-    uint32_t* __restrict__ run_cnt, const uint32_t* __restrict__ part_offs) {
+    uint32_t* __restrict__ run_cnt, const uint32_t* __restrict__ part_offs, int out_shift,
+    int run_shift, uint32_t run_limit, uint32_t* key_err, int val_bits, uint32_t val_limit) {
+    static_assert(!NARROW || (sizeof(K) == 8 && SPLIT && !RUNS && !KONLY),
+                  "narrowing: 64-bit split passes");
+    static_assert(!KONLY || (sizeof(K) == 8 && SPLIT && !IOTA && !DROP),
+                  "keys with their values: 64-bit split passes");
     using D = Desc<D32>;
     using DT = typename D::T;
     DT* state = static_cast<DT*>(state_raw);
@@ -227,6 +251,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     __shared__ uint32_t s_gpos[256];
     __shared__ uint32_t s_tmp[2][4];
     __shared__ uint32_t s_nh[256];  // next pass's digit counts (next_hist given)
+    __shared__ uint8_t s_blk[NARROW ? PART / 32 : 1];  // NARROW: digit of element 32 b
     __shared__ K s_keys[PART];
     __shared__ uint32_t s_vals_own[SPLIT ? 1 : PART];
     uint32_t* const s_vals = SPLIT ? reinterpret_cast<uint32_t*>(s_keys) : s_vals_own;
@@ -261,7 +286,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
         const int64_t idx = wave_base + it * GS_WAVE + lane;
         if (idx < n) {
             key[it] = kin[idx];
-            val[it] = IOTA ? (uint32_t)idx : vin[idx];
+            val[it] = KONLY ? 0u : IOTA ? (uint32_t)idx : vin[idx];
         } else {
             key[it] = 0;
             val[it] = 0;
@@ -349,10 +374,23 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
             const uint32_t d = digit_of(key[it], shift, mask);
             const uint32_t lp = s_loff[d] + s_wcnt[w][d] + rank[it];
             if (lp < (uint32_t)PART) {
-                s_keys[lp] = key[it];
+                if constexpr (NARROW) {
+                    const uint64_t kk = (uint64_t)key[it] >> out_shift;
+                    if ((kk >> (64 - val_bits)) != 0u) report_error(key_err, kErrKeyRange);
+                    if (val_limit != 0u && val[it] >= val_limit) report_error(key_err, kErrValRange);
+                    s_keys[lp] = (K)((kk << val_bits) | val[it]);
+                } else {
+                    s_keys[lp] = key[it];
+                }
                 if (!SPLIT) s_vals[lp] = val[it];
             }
         }
+    }
+    if (NARROW && tid < 256) {
+        // digit tid's elements are [s_loff[tid], next digit's offset): it owns
+        // the 32-element blocks that start inside that range
+        const uint32_t lo = s_loff[tid], hi = tid == 255 ? s_count : s_loff[tid + 1];
+        for (uint32_t b = (lo + 31u) >> 5; (b << 5) < hi; ++b) s_blk[b] = (uint8_t)tid;
     }
     if (tid < 256) {
         if (part_offs != nullptr) {
@@ -390,10 +428,14 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
             if (RUNS) {
                 // run [a, b) of key k: + b at its last key, - a at its first
                 // (modulo 2^32; a run of one adds 1)
-                const bool first = j == 0 || s_keys[j - 1] != k;
-                const bool last = j == count - 1 || s_keys[j + 1] != k;
+                const K r = k >> run_shift;
+                const bool first = j == 0 || (s_keys[j - 1] >> run_shift) != r;
+                const bool last = j == count - 1 || (s_keys[j + 1] >> run_shift) != r;
                 const uint32_t delta = (last ? (uint32_t)j + 1u : 0u) - (first ? (uint32_t)j : 0u);
-                if (first || last) atomicAdd(&run_cnt[(uint32_t)k], delta);
+                if (first || last) {
+                    if (r < (K)run_limit) atomicAdd(&run_cnt[(uint32_t)r], delta);
+                    else report_error(key_err, kErrKeyRange);
+                }
             }
         }
     } else {
@@ -405,19 +447,33 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
             gq[q] = 0xFFFFFFFFu;
             if (j < count) {
                 const K k = s_keys[j];
-                const uint32_t g = s_gpos[digit_of(k, shift, mask)] + (uint32_t)j;
+                uint32_t d;
+                if constexpr (NARROW) {
+                    d = s_blk[j >> 5];
+                    while (d < 255u && s_loff[d + 1] <= (uint32_t)j) ++d;
+                } else {
+                    d = digit_of(k, shift, mask);
+                }
+                const uint32_t g = s_gpos[d] + (uint32_t)j;
                 gq[q] = g;
                 if (!RUNS && (int64_t)g < n) kout[g] = k;
+                if (KONLY && RUNS && (int64_t)g < n)
+                    vout[g] = (uint32_t)k & (uint32_t)(0xFFFFFFFFull >> (32 - val_bits));
                 if (RUNS) {
                     // run [a, b) of key k: + b at its last key, - a at its first
-                    const bool first = j == 0 || s_keys[j - 1] != k;
-                    const bool last = j == count - 1 || s_keys[j + 1] != k;
+                    const K r = k >> run_shift;
+                    const bool first = j == 0 || (s_keys[j - 1] >> run_shift) != r;
+                    const bool last = j == count - 1 || (s_keys[j + 1] >> run_shift) != r;
                     const uint32_t delta =
                         (last ? (uint32_t)j + 1u : 0u) - (first ? (uint32_t)j : 0u);
-                    if (first || last) atomicAdd(&run_cnt[(uint32_t)k], delta);
+                    if (first || last) {
+                        if (r < (K)run_limit) atomicAdd(&run_cnt[(uint32_t)r], delta);
+                        else report_error(key_err, kErrKeyRange);
+                    }
                 }
             }
         }
+        if constexpr (KONLY || NARROW) return;  // the values left with the keys
         __syncthreads();  // the keys are out: their LDS space takes the values
 #pragma unroll
         for (int it = 0; it < ITEMS; ++it) {
@@ -459,13 +515,27 @@ __global__ void k_iota_u32(uint32_t* p, size_t n) {
     if (i < n) p[i] = (uint32_t)i;
 }
 
+// How a pass writes its keys: narrow (64-bit keys and values in, one 64-bit
+// word (key >> out_shift) << 32 | value out), konly (those words in and out)
+// and, for a RUNS pass, the runs' shift and tile limit.
+struct PassOut {
+    bool narrow = false;
+    bool konly = false;
+    int out_shift = 0;
+    int run_shift = 0;
+    uint32_t run_limit = 0xFFFFFFFFu;
+    uint32_t* key_err = nullptr;  // kErrKeyRange of narrowing and run counting
+    int val_bits = 32;            // the value field of the joined words
+    uint32_t val_limit = 0u;      // values must be below it (0: any)
+};
+
 // A digit pass with partition shape CFG.
 template <typename K, typename CFG>
 hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uint32_t* vout,
                       int64_t n_cap, const uint32_t* n_dev, int shift, int bits,
                       const uint32_t* hist_pass, SortTemp& tmp, uint32_t* ticket, hipStream_t st,
                       bool drop, uint32_t* next_hist, int next_shift, int next_bits,
-                      uint32_t* run_cnt, const uint32_t* part_offs) {
+                      uint32_t* run_cnt, const uint32_t* part_offs, const PassOut& po) {
     constexpr int T = CFG::T, I = CFG::I;
     constexpr bool SP = CFG::SPLIT;
     const unsigned grid = (unsigned)((n_cap + T * I - 1) / (T * I));
@@ -491,13 +561,30 @@ hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uin
         tmp.dirty[0] = tmp.dirty[1] = (uint32_t)std::min<size_t>(tmp.state_parts, 0xFFFFFFFFu);
     }
     const uint32_t epoch = ++tmp.epoch;
-#define GS_OS(IO, DD, DR, RU)                                                                    \
-    k_onesweep<K, IO, T, I, DD, DR, SP, RU><<<grid, T, 0, st>>>(kin, vin, kout, vout, n_cap,     \
-                                                                n_dev, shift, bits, hist_pass,   \
-                                                                state, ticket, epoch, clear_next,\
-                                                                tmp.ctl, next_hist, next_shift,  \
-                                                                next_bits, run_cnt, part_offs)
-    if (run_cnt != nullptr) {
+#define GS_OSN(IO, DD, DR, RU, NA, KO)                                                          \
+    k_onesweep<K, IO, T, I, DD, DR, SP, RU, NA, KO><<<grid, T, 0, st>>>(                        \
+        kin, vin, kout, vout, n_cap, n_dev, shift, bits, hist_pass, state, ticket, epoch,       \
+        clear_next, tmp.ctl, next_hist, next_shift, next_bits, run_cnt, part_offs, po.out_shift,\
+        po.run_shift, po.run_limit, po.key_err, po.val_bits, po.val_limit)
+#define GS_OS(IO, DD, DR, RU) GS_OSN(IO, DD, DR, RU, false, false)
+    if (po.narrow || po.konly) {
+        if constexpr (sizeof(K) == 8 && SP) {
+            if (iota || drop || (po.narrow && (po.konly || run_cnt != nullptr)))
+                return hipErrorInvalidValue;
+            if (po.narrow) {
+                if (d32) GS_OSN(false, true, false, false, true, false);
+                else GS_OSN(false, false, false, false, true, false);
+            } else if (run_cnt != nullptr) {
+                if (d32) GS_OSN(false, true, false, true, false, true);
+                else GS_OSN(false, false, false, true, false, true);
+            } else {
+                if (d32) GS_OSN(false, true, false, false, false, true);
+                else GS_OSN(false, false, false, false, false, true);
+            }
+        } else {
+            return hipErrorInvalidValue;
+        }
+    } else if (run_cnt != nullptr) {
         if (iota || sizeof(K) != 4) return hipErrorInvalidValue;
         if (drop) {  // a one-pass sort: it drops and counts
             if (d32) GS_OS(false, true, true, true); else GS_OS(false, false, true, true);
@@ -513,6 +600,7 @@ hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uin
         if (d32) GS_OS(false, true, false, false); else GS_OS(false, false, false, false);
     }
 #undef GS_OS
+#undef GS_OSN
     return hipGetLastError();
 }
 
@@ -526,14 +614,14 @@ hipError_t launch_pass(bool iota, const K* kin, const uint32_t* vin, K* kout, ui
                        const uint32_t* hist_pass, SortTemp& tmp, uint32_t* ticket,
                        hipStream_t st, bool drop = false, uint32_t* next_hist = nullptr,
                        int next_shift = 0, int next_bits = 0, uint32_t* run_cnt = nullptr,
-                       const uint32_t* part_offs = nullptr) {
+                       const uint32_t* part_offs = nullptr, const PassOut& po = PassOut()) {
     if constexpr (sizeof(K) == 8)
         return launch_cfg<K, Sweep64>(iota, kin, vin, kout, vout, n_cap, n_dev, shift, bits,
                                       hist_pass, tmp, ticket, st, drop, next_hist, next_shift,
-                                      next_bits, run_cnt, part_offs);
+                                      next_bits, run_cnt, part_offs, po);
     return launch_cfg<K, Sweep32>(iota, kin, vin, kout, vout, n_cap, n_dev, shift, bits,
                                   hist_pass, tmp, ticket, st, drop, next_hist, next_shift,
-                                  next_bits, run_cnt, part_offs);
+                                  next_bits, run_cnt, part_offs, po);
 }
 
 template <typename K>
@@ -608,7 +696,8 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
                          SortTemp& tmp, hipStream_t st, bool vals_iota, K** keys_final,
                          uint32_t** vals_final, const uint32_t* n_kept_dev,
                          uint32_t* chain_hist = nullptr, bool pass_events = false,
-                         uint32_t* run_cnt = nullptr, const uint32_t* first_offs = nullptr) {
+                         uint32_t* run_cnt = nullptr, const uint32_t* first_offs = nullptr,
+                         uint32_t run_limit = 0xFFFFFFFFu) {
     *keys_final = keys;
     *vals_final = vals;
     if (n_cap <= 0) return hipSuccess;
@@ -620,6 +709,8 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
     K* kalt = static_cast<K*>(tmp.keys_alt);
     uint32_t* valt = tmp.vals_alt;
     const int dw = sort_digit_width(end_bit - begin_bit);
+    PassOut po;
+    po.run_limit = run_limit;
     for (int p = 0; p < npass; ++p) {
         const int shift = begin_bit + dw * p;
         const int bits = std::min(dw, end_bit - shift);
@@ -634,7 +725,7 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
                                       chain ? chain_hist + (p + 1) * 256 : nullptr, nshift,
                                       chain ? std::min(dw, end_bit - nshift) : 0,
                                       p + 1 == npass ? run_cnt : nullptr,
-                                      p == 0 ? first_offs : nullptr);
+                                      p == 0 ? first_offs : nullptr, po);
         if (timed) (void)hipEventRecord(tmp.pass_events[2 * p + 1], st);
         if (e != hipSuccess) return e;
         std::swap(kin, kalt);
@@ -652,13 +743,13 @@ hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const
                                 uint32_t* tickets, SortTemp& tmp, hipStream_t st, bool vals_iota,
                                 void** keys_final, uint32_t** vals_final,
                                 const uint32_t* n_kept_dev, uint32_t* run_cnt,
-                                const uint32_t* first_offs) {
+                                const uint32_t* first_offs, uint32_t run_limit) {
     if (key_bytes == 4) {
         uint32_t* kf = nullptr;
         hipError_t e = sort_dev_impl<uint32_t>(static_cast<uint32_t*>(keys), vals, n_cap, n_dev,
                                                begin_bit, end_bit, hist, tickets, tmp, st,
                                                vals_iota, &kf, vals_final, n_kept_dev, nullptr,
-                                               false, run_cnt, first_offs);
+                                               false, run_cnt, first_offs, run_limit);
         *keys_final = run_cnt != nullptr ? nullptr : kf;
         return e;
     }
@@ -689,9 +780,9 @@ hipError_t radix_sort_pairs_dev_chain(uint64_t* keys, uint32_t* vals, int64_t n,
     // the first pass's histogram only; the passes chain the others
     const unsigned grid = (unsigned)std::min<int64_t>(
         (n + kHistThreads * kHistItems - 1) / (kHistThreads * kHistItems), 2048);
-    k_hist<uint64_t><<<grid, kHistThreads, 0, st>>>(keys, n, begin_bit,
-                                                    std::min(end_bit, begin_bit + dw), 1, dw,
-                                                    hist);
+    k_hist<uint64_t, 1><<<grid, kHistThreads, 0, st>>>(keys, n, begin_bit,
+                                                       std::min(end_bit, begin_bit + dw), 1, dw,
+                                                       hist);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     uint64_t* kf = nullptr;
@@ -701,7 +792,86 @@ hipError_t radix_sort_pairs_dev_chain(uint64_t* keys, uint32_t* vals, int64_t n,
     return e;
 }
 
+hipError_t radix_sort_ids_dev_chain(uint64_t* keys, uint32_t* vals, int64_t n, int tile_bits,
+                                    uint64_t val_limit, uint32_t num_tiles, uint32_t* run_cnt,
+                                    uint32_t* key_err, uint32_t* hist, uint32_t* tickets,
+                                    SortTemp& tmp, hipStream_t st, int* passes_out) {
+    *passes_out = 0;
+    const int end_bit = 32 + tile_bits;
+    const int npass = (end_bit + 7) / 8;
+    if (tile_bits < 1 || npass > kMaxPasses || val_limit > ((uint64_t)1 << 32))
+        return hipErrorInvalidValue;
+    // the value field: the bits of val_limit - 1 (all 32 for no limit)
+    int val_bits = 32;
+    if (val_limit != 0) {
+        val_bits = 1;
+        while (val_bits < 32 && ((uint64_t)1 << val_bits) < val_limit) ++val_bits;
+    }
+    const int dw = sort_digit_width(end_bit);
+    // q passes over 64-bit keys with separate values, the last of them
+    // joining each key's bits [q*dw, end_bit) and its value into one word
+    // (the fewest passes after which they fit): key bit b >= q*dw sits at bit
+    // val_bits + b - q*dw of the word
+    int q = 1;
+    while (q < npass && end_bit - q * dw + val_bits > 64) ++q;
+    if (q >= npass) return hipErrorNotSupported;
+    if (n <= 0) return hipSuccess;
+    if (n >= (int64_t)1 << 32) return hipErrorInvalidValue;
+    const int nshift = q * dw;
+    const unsigned grid = (unsigned)std::min<int64_t>(
+        (n + kHistThreads * kHistItems - 1) / (kHistThreads * kHistItems), 2048);
+    k_hist<uint64_t, 1><<<grid, kHistThreads, 0, st>>>(keys, n, 0, dw, 1, dw, hist);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // keys (and then the joined words) ping-pong between keys and keys_alt,
+    // values between vals and vals_alt until they are joined; the last pass
+    // writes the sorted values into vals
+    uint64_t* k64[2] = {keys, static_cast<uint64_t*>(tmp.keys_alt)};
+    uint32_t* vb[2] = {vals, tmp.vals_alt};
+    int ki = 0, vi = 0;
+    for (int p = 0; p < npass; ++p) {
+        const bool wide = p < q;
+        const int at = wide ? 0 : val_bits - nshift;  // key bit b of this pass's input: at b + at
+        const int shift = dw * p + at;
+        const int bits = std::min(dw, end_bit - dw * p);
+        const bool last = p + 1 == npass;
+        // the next pass's digits, counted from this pass's input keys
+        const int next_shift = dw * (p + 1) + at;
+        const int next_bits = last ? 0 : std::min(dw, end_bit - dw * (p + 1));
+        uint32_t* nh = last ? nullptr : hist + (p + 1) * 256;
+        PassOut po;
+        po.key_err = key_err;
+        po.val_bits = val_bits;
+        po.val_limit = val_limit == ((uint64_t)1 << 32) ? 0u : (uint32_t)val_limit;
+        const bool timed = tmp.pass_events != nullptr && p < tmp.max_timed_passes;
+        if (timed) (void)hipEventRecord(tmp.pass_events[2 * p], st);
+        if (wide) {
+            po.narrow = p + 1 == q;
+            po.out_shift = nshift;
+            e = launch_pass<uint64_t>(false, k64[ki], vb[vi], k64[ki ^ 1], vb[vi ^ 1], n, nullptr,
+                                      shift, bits, hist + p * 256, tmp, tickets + p, st, false,
+                                      nh, next_shift, next_bits, nullptr, nullptr, po);
+            vi ^= 1;
+        } else {
+            po.konly = true;
+            po.run_shift = 32 + at;  // the tile field of the joined word
+            po.run_limit = num_tiles;
+            e = launch_pass<uint64_t>(false, k64[ki], nullptr, k64[ki ^ 1],
+                                      last ? vals : nullptr, n, nullptr, shift, bits,
+                                      hist + p * 256, tmp, tickets + p, st, false, nh,
+                                      next_shift, next_bits, last ? run_cnt : nullptr, nullptr,
+                                      po);
+        }
+        if (timed) (void)hipEventRecord(tmp.pass_events[2 * p + 1], st);
+        if (e != hipSuccess) return e;
+        ki ^= 1;
+        ++*passes_out;
+    }
+    return hipSuccess;
+}
+
 size_t sort_partitions(int64_t n) { return (size_t)((n + kMinPart - 1) / kMinPart); }
+
 
 hipError_t launch_digit_hist_u64(const uint64_t* keys, int64_t n, int begin_bit, int end_bit,
                                  uint32_t* hist, hipStream_t st) {

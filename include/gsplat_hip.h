@@ -269,8 +269,23 @@ int gs_last_sort_pass_ms(gs_ctx* ctx, float* ms, int max_passes);
  * tile id >= num_tiles gives GS_E_INVALID. */
 int gs_sort_tile_depth_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* vals, int64_t n,
                            int64_t num_tiles, uint32_t* tile_ranges, int* passes_out);
+/* The same sort with the outputs of the reference's sort_and_bin
+ * (src/gsplat_cpu/sort.h:11-31, sort.cpp:89-165): the sorted values (ids, in
+ * place: the input values in, the values in sorted key order out) and
+ * tile_ranges; the sorted keys are not produced and `keys` is overwritten
+ * (scratch). num_gaussians is sort_and_bin's M: every id is below it (0: any
+ * 32-bit id). The key bits of the digits already sorted are dropped as soon as
+ * the rest and the id fit 64 bits: the later passes move each key's remaining
+ * bits and its id as one 8-byte word (one store stream instead of two), and
+ * the last writes only the ids (it counts each tile's keys instead of writing
+ * keys). A key with a tile id >= num_tiles, or with any bit set above the tile
+ * field, or an id >= num_gaussians gives GS_E_INVALID. More than 2^24 tiles:
+ * sorted as by gs_sort_tile_depth_dev (the ids are not checked). */
+int gs_sort_tile_depth_ids_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* ids, int64_t n,
+                               int64_t num_gaussians, int64_t num_tiles, uint32_t* tile_ranges,
+                               int* passes_out);
 /* Device time (ms) of the range extraction of the last gs_sort_tile_depth_dev
- * call when timing is on (0 otherwise). */
+ * or gs_sort_tile_depth_ids_dev call when timing is on (0 otherwise). */
 float gs_last_ranges_ms(gs_ctx* ctx);
 /* gs_sort_tile_depth_dev with no allocation of any kind. It has no counterpart
  * in the reference: it is for callers that cannot allocate (tight serving
