@@ -1004,12 +1004,14 @@ struct gs_ctx {
         sort.ctl = cnt + C_CTL;
         // depth order of the visible Gaussians (stable: ties keep index order)
         // (values: the projection's packed ones when tp.idx_bits is set, else
-        // the compact indices 0..M-1)
+        // the compact indices 0..M-1); the sorted depth keys are not needed, so
+        // the last pass writes the values only
         void* kf = nullptr;
         uint32_t* order = nullptr;
         HIPCHK(gs::radix_sort_pairs_dev(b_dkey.p, b_tmp_a.as<uint32_t>(), N, cnt + C_M, 4, 0, 32,
                                         fr + kFrDepthHist, cnt + C_DSORT_TICKETS, sort, st,
-                                        tp.idx_bits == 0, &kf, &order));
+                                        tp.idx_bits == 0, &kf, &order, nullptr, nullptr, nullptr,
+                                        0xFFFFFFFFu, false));
         record(2);
         HIPCHK(gs::launch_rect_count_scan(b_rc.as<float4>(), 2, order, N, cnt + C_M, tp,
                                           b_offs.as<uint32_t>(), b_bstart.as<uint32_t>(),

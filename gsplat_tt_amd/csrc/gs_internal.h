@@ -149,6 +149,8 @@ hipError_t radix_sort_pairs(void* keys, uint32_t* vals, int64_t n, int key_bytes
 // passes sort min(n_cap, *n_kept_dev) keys, and `hist` counts kept keys only.
 // run_cnt (u32 keys only, optional): the sorted keys are not written (*keys_final = nullptr); run_cnt[k] (cleared by the caller) gains
 // the number of keys equal to k, for launch_ranges_from_counts.
+// keys_out = false (u32 keys): the last pass writes the sorted values only
+// (*keys_final = nullptr).
 // first_offs (u32 keys only, optional): the first pass's output positions per
 // partition of kSortPartition32 keys and digit (2^w words per partition, w the
 // pass's digit width; launch_part_offsets): that pass needs no look-back.
@@ -161,7 +163,7 @@ hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const
                                 const uint32_t* n_kept_dev = nullptr,
                                 uint32_t* run_cnt = nullptr,
                                 const uint32_t* first_offs = nullptr,
-                                uint32_t run_limit = 0xFFFFFFFFu);
+                                uint32_t run_limit = 0xFFFFFFFFu, bool keys_out = true);
 
 // The 64-bit-key sort of radix_sort_pairs_dev over exactly n keys, with no
 // producer histogram: a histogram kernel counts the first pass's digits and

@@ -422,7 +422,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
             const uint32_t d = digit_of(k, shift, mask);
             const uint32_t g = s_gpos[d] + (uint32_t)j;
             if ((int64_t)g < n) {
-                if (!RUNS) kout[g] = k;
+                if (!RUNS && kout != nullptr) kout[g] = k;
                 vout[g] = s_vals[j];
             }
             if (RUNS) {
@@ -456,7 +456,7 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
                 }
                 const uint32_t g = s_gpos[d] + (uint32_t)j;
                 gq[q] = g;
-                if (!RUNS && (int64_t)g < n) kout[g] = k;
+                if (!RUNS && kout != nullptr && (int64_t)g < n) kout[g] = k;
                 if (KONLY && RUNS && (int64_t)g < n)
                     vout[g] = (uint32_t)k & (uint32_t)(0xFFFFFFFFull >> (32 - val_bits));
                 if (RUNS) {
@@ -697,7 +697,7 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
                          uint32_t** vals_final, const uint32_t* n_kept_dev,
                          uint32_t* chain_hist = nullptr, bool pass_events = false,
                          uint32_t* run_cnt = nullptr, const uint32_t* first_offs = nullptr,
-                         uint32_t run_limit = 0xFFFFFFFFu) {
+                         uint32_t run_limit = 0xFFFFFFFFu, bool keys_out = true) {
     *keys_final = keys;
     *vals_final = vals;
     if (n_cap <= 0) return hipSuccess;
@@ -720,7 +720,8 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
         const int nshift = shift + dw;
         const bool timed = pass_events && tmp.pass_events != nullptr && p < tmp.max_timed_passes;
         if (timed) (void)hipEventRecord(tmp.pass_events[2 * p], st);
-        hipError_t e = launch_pass<K>(p == 0 && vals_iota, kin, vin, kalt, valt, n_cap, cnt,
+        K* kdst = (p + 1 == npass && !keys_out) ? nullptr : kalt;
+        hipError_t e = launch_pass<K>(p == 0 && vals_iota, kin, vin, kdst, valt, n_cap, cnt,
                                       shift, bits, hist + p * 256, tmp, tickets + p, st, drop,
                                       chain ? chain_hist + (p + 1) * 256 : nullptr, nshift,
                                       chain ? std::min(dw, end_bit - nshift) : 0,
@@ -731,7 +732,7 @@ hipError_t sort_dev_impl(K* keys, uint32_t* vals, int64_t n_cap, const uint32_t*
         std::swap(kin, kalt);
         std::swap(vin, valt);
     }
-    *keys_final = kin;
+    *keys_final = keys_out ? kin : nullptr;
     *vals_final = vin;
     return hipSuccess;
 }
@@ -743,13 +744,13 @@ hipError_t radix_sort_pairs_dev(void* keys, uint32_t* vals, int64_t n_cap, const
                                 uint32_t* tickets, SortTemp& tmp, hipStream_t st, bool vals_iota,
                                 void** keys_final, uint32_t** vals_final,
                                 const uint32_t* n_kept_dev, uint32_t* run_cnt,
-                                const uint32_t* first_offs, uint32_t run_limit) {
+                                const uint32_t* first_offs, uint32_t run_limit, bool keys_out) {
     if (key_bytes == 4) {
         uint32_t* kf = nullptr;
         hipError_t e = sort_dev_impl<uint32_t>(static_cast<uint32_t*>(keys), vals, n_cap, n_dev,
                                                begin_bit, end_bit, hist, tickets, tmp, st,
                                                vals_iota, &kf, vals_final, n_kept_dev, nullptr,
-                                               false, run_cnt, first_offs, run_limit);
+                                               false, run_cnt, first_offs, run_limit, keys_out);
         *keys_final = run_cnt != nullptr ? nullptr : kf;
         return e;
     }
