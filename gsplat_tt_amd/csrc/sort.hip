@@ -267,7 +267,26 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     if (clear_next != nullptr && tid < 256) clear_next[(size_t)blockIdx.x * 256 + tid] = 0u;
     for (int i = tid; i < WAVES * 256; i += THREADS) (&s_wcnt[0][0])[i] = 0;
     if (next_hist != nullptr && tid < 256) s_nh[tid] = 0u;
+    // A pass whose digit is the same for all n keys (one histogram bin holds
+    // them all, e.g. the exponent byte of depths within one binade) leaves the
+    // order as it is, the sort being stable: every partition then copies its
+    // keys in place, with no ranking and no look-back (all partitions see the
+    // same histogram, so none waits on another). The first four waves vote,
+    // one ballot each.
+    constexpr bool kIdentityOk = !DROP && !RUNS && !NARROW && !KONLY;
+    __shared__ uint32_t s_vote[kIdentityOk ? 4 : 1];
+    if constexpr (kIdentityOk) {
+        if (tid < 256) {
+            const int64_t nn = n_dev ? min(n_cap, (int64_t)*n_dev) : n_cap;
+            const bool v = next_hist == nullptr && part_offs == nullptr &&
+                           (int64_t)g_hist_pass[tid] == nn;
+            const uint64_t b = __ballot(v);
+            if (lane == 0) s_vote[w] = b != 0ull ? 1u : 0u;
+        }
+    }
     __syncthreads();
+    bool identity = false;
+    if constexpr (kIdentityOk) identity = (s_vote[0] | s_vote[1] | s_vote[2] | s_vote[3]) != 0u;
     const uint32_t vid = s_vid;
     // after an earlier give-up or a capacity overflow the keys may be partial:
     // sort nothing (this workgroup's row of the next pass's descriptors is
@@ -278,6 +297,17 @@ __global__ __launch_bounds__(THREADS) void k_onesweep(
     const int64_t n = n_dev ? min(n_cap, (int64_t)*n_dev) : n_cap;
     if (part_base >= n) return;  // tickets are in order: no later partition has keys
     const int64_t wave_base = part_base + (int64_t)w * (ITEMS * GS_WAVE);
+    if (identity) {
+#pragma unroll
+        for (int it = 0; it < ITEMS; ++it) {
+            const int64_t idx = wave_base + it * GS_WAVE + lane;
+            if (idx < n) {
+                if (kout != nullptr) kout[idx] = kin[idx];
+                vout[idx] = IOTA ? (uint32_t)idx : vin[idx];
+            }
+        }
+        return;
+    }
 
     K key[ITEMS];
     uint32_t val[ITEMS];
