@@ -248,6 +248,9 @@ struct gs_ctx {
     ~gs_ctx() {
         for (gs_ctx* p : peers) delete p;
         if (st) (void)hipStreamSynchronize(st);
+        // an announced frame's ring image (its writer has finished: both
+        // slots' streams are synchronised above)
+        if (spec_lease) gs::LeaseTable::get().release(spec_lease);
         drop_graph();
         for (DevBuf* b : {&b_mean, &b_cov, &b_opac, &b_col, &b_terms, &b_upload, &b_rc,
                           &b_dkey, &b_brec, &b_src, &b_valid, &b_offs, &b_bstart, &b_pair_tile, &b_pair_id,
@@ -823,6 +826,12 @@ struct gs_ctx {
     uint64_t spec_gen = 0;
     DevBuf b_spec;                // output of an announced frame (per slot)
     gs_stats spec_st{};
+    // An announced frame of render_out_ring writes its image by DMA straight
+    // into a ring buffer leased for it when it is enqueued (no copy when the
+    // next call takes it; the lease passes to the caller then, and is released
+    // when the frame is dropped instead).
+    gs::PinnedImage* spec_im = nullptr;
+    uint64_t spec_lease = 0;
 
     // Zero-copy output (render/host/out_ring.h, render.cpp:598-612): the frame's
     // image is copied by DMA into a pinned buffer of the ring and handed over
@@ -835,32 +844,111 @@ struct gs_ctx {
     }
     static void pinned_free(void* p) { (void)hipHostFree(p); }
 
-    void render_out_ring(const gs_view* v, const gs_view* next, gs_out_image* img,
-                         gs_stats* stats) {
-        REQUIRE(img != nullptr, "render_out_ring: null image");
-        check_view(v);
-        if (!ring) ring.reset(new gs::OutRing(pinned_alloc, pinned_free, ring_cap));
+    static size_t view_pitch(const gs_view* v) {
         const size_t eb = v->out_format == GS_OUT_F32 ? 4 : (v->out_format == GS_OUT_BF16 ? 2 : 1);
-        const size_t pitch = (size_t)v->image_width * 3 * eb;
-        const size_t bytes = pitch * v->image_height;
+        return (size_t)v->image_width * 3 * eb;
+    }
+
+    // A ring image of `bytes`, leased at once so that no other acquire hands
+    // it out while a frame writes it.
+    gs::PinnedImage* ring_take(size_t bytes, uint64_t* lease) {
         gs::PinnedImage* im = nullptr;
         try {
             im = ring->acquire(bytes);
         } catch (const std::bad_alloc&) {
             throw GsError(GS_E_DEVICE, "render_out_ring: pinned host allocation failed");
         }
-        render_next(v, im->p, false, next, stats);
+        *lease = gs::LeaseTable::get().lease(im);
+        return im;
+    }
+
+    // render_next into the output ring: the view's image is a ring buffer
+    // filled by DMA, and the announced next view's frame writes into a ring
+    // buffer of its own, so a call that takes the announced frame only waits
+    // for it (its image is already in host memory).
+    void render_out_ring(const gs_view* v, const gs_view* next, gs_out_image* img,
+                         gs_stats* stats) {
+        REQUIRE(img != nullptr, "render_out_ring: null image");
+        check_view(v);
+        if (next) check_view(next);
+        if (!ring) ring.reset(new gs::OutRing(pinned_alloc, pinned_free, ring_cap));
+        const size_t pitch = view_pitch(v);
+        const size_t bytes = pitch * v->image_height;
+        ensure_peers(2);
+        gs_ctx* peer = peers[0];
+        const bool hit = spec_slot != nullptr && spec_im != nullptr && spec_gen == scene_gen &&
+                         std::memcmp(&spec_view, v, sizeof(gs_view)) == 0;
+        gs_ctx* cur;
+        gs::PinnedImage* im;
+        uint64_t lease = 0;
+        if (hit) {
+            cur = spec_slot;  // this view's frame is already in flight there
+            im = spec_im;
+            lease = spec_lease;
+            spec_slot = nullptr;
+            spec_im = nullptr;
+            spec_lease = 0;
+        } else {
+            drain_spec();
+            cur = this;
+            im = ring_take(bytes, &lease);
+            try {
+                cur->render_begin(v, im->p, false, stats, false);
+            } catch (...) {
+                gs::LeaseTable::get().release(lease);
+                throw;
+            }
+            peer->sd = sd;  // terms for v's floors
+        }
+        try {
+            // announce the next view on the other slot (same floors: shared terms)
+            if (next != nullptr && next->contrib_floor == v->contrib_floor &&
+                next->mb_contrib_floor == v->mb_contrib_floor && next->k_cap == v->k_cap) {
+                gs_ctx* other = cur == this ? peer : this;
+                uint64_t nl = 0;
+                gs::PinnedImage* nim = ring_take(view_pitch(next) * next->image_height, &nl);
+                try {
+                    other->render_begin(next, nim->p, false, &other->spec_st, true);
+                } catch (...) {
+                    gs::LeaseTable::get().release(nl);
+                    throw;
+                }
+                spec_slot = other;
+                spec_view = *next;
+                spec_gen = scene_gen;
+                spec_im = nim;
+                spec_lease = nl;
+            }
+            cur->render_end();
+        } catch (...) {
+            if (cur->pend.active) {  // the view's frame is dropped with its image
+                cur->pend.active = false;
+                cur->sync();
+            }
+            gs::LeaseTable::get().release(lease);
+            throw;
+        }
+        if (hit && stats) *stats = cur->spec_st;
         img->data = im->p;
         img->bytes = (int64_t)bytes;
         img->pitch = (int64_t)pitch;
-        img->lease = gs::LeaseTable::get().lease(im);
+        img->lease = lease;
     }
 
     void drain_spec() {
         if (spec_slot == nullptr) return;
         gs_ctx* s = spec_slot;
+        const uint64_t lease = spec_lease;
         spec_slot = nullptr;
-        s->render_end();
+        spec_im = nullptr;
+        spec_lease = 0;
+        try {
+            s->render_end();
+        } catch (...) {
+            if (lease) gs::LeaseTable::get().release(lease);
+            throw;
+        }
+        if (lease) gs::LeaseTable::get().release(lease);
     }
 
     void render_next(const gs_view* v, void* out, bool out_dev, const gs_view* next,
@@ -871,7 +959,9 @@ struct gs_ctx {
         ensure_peers(2);
         gs_ctx* peer = peers[0];
         gs_ctx* cur;
-        const bool hit = spec_slot != nullptr && spec_gen == scene_gen &&
+        // (a frame announced by render_out_ring writes into its ring image,
+        // not b_spec: it is dropped like any other miss)
+        const bool hit = spec_slot != nullptr && spec_im == nullptr && spec_gen == scene_gen &&
                          std::memcmp(&spec_view, v, sizeof(gs_view)) == 0;
         if (hit) {
             cur = spec_slot;  // this view's frame is already in flight there
