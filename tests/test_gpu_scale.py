@@ -189,6 +189,10 @@ def test_c3_6m_orbit_batch_graph_replay(c3_scene):
 
 
 def test_c4_50m_key_sort_with_tile_ranges(gpu_ctx):
+    """The 50M keys through the whole-key sort (sorted keys, ids, ranges) and
+    through the ids-and-ranges sort the benchmark times (ids below M = 50M, so
+    each key's unsorted bits and its id travel as one word after the first
+    pass): both equal numpy's stable order and the per-tile ranges."""
     print("C4 50M-key sort + ranges", flush=True)
     n, tiles = 50_000_000, 5000
     keys, vals = scenes.config4_keys(n=n, tiles=tiles)
@@ -203,12 +207,22 @@ def test_c4_50m_key_sort_with_tile_ranges(gpu_ctx):
         gpu_ctx.d2h(ko, dk)
         gpu_ctx.d2h(vo, dv)
         gpu_ctx.d2h(rg, dr)
+        print(f"C4 ids-and-ranges sort (M = {n})", flush=True)
+        gpu_ctx.h2d(dk, keys)
+        gpu_ctx.h2d(dv, vals)
+        passes_ids = gpu_ctx.sort_tile_depth_ids_dev(dk, dv, n, tiles, dr, num_gaussians=n)
+        vo_ids = np.empty(n, np.uint32)
+        rg_ids = np.empty((tiles, 2), np.uint32)
+        gpu_ctx.d2h(vo_ids, dv)
+        gpu_ctx.d2h(rg_ids, dr)
     finally:
         for p in (dk, dv, dr):
             gpu_ctx.dev_free(p)
-    print(f"C4: {passes} passes", flush=True)
+    print(f"C4: {passes} passes ({passes_ids} for ids and ranges)", flush=True)
+    assert passes == passes_ids == 6
     order = np.argsort(keys, kind="stable")
     assert np.array_equal(vo, order.astype(np.uint32))
+    assert np.array_equal(vo_ids, vo) and np.array_equal(rg_ids, rg)
     assert np.array_equal(ko, keys[order])
     t = (ko >> np.uint64(32)).astype(np.int64)
     lo = np.searchsorted(t, np.arange(tiles), "left")
