@@ -2357,13 +2357,18 @@ int gs_sort_tile_depth_ids_dev(gs_ctx* ctx, uint64_t* keys, uint32_t* ids, int64
         ctx->ensure_sort(n, 8);
         ctx->b_tcnt.ensure((size_t)num_tiles * 4);
         uint32_t* ctl = ctx->b_cnt.as<uint32_t>() + gs_ctx::C_CTL;
-        ctx->ctl_reset(ctl);
         ctx->sort.ctl = ctl;
         uint32_t* tcnt = ctx->b_tcnt.as<uint32_t>();
         uint32_t* key_err = ctl + 2;  // a key-range flag that does not stop the passes
-        HIPCHK(gs::launch_fill_u32(key_err, 0u, 1, ctx->st));
-        HIPCHK(gs::launch_fill_u32(ctx->sort.hist, 0u, gs::sort_hist_words(), ctx->st));
-        HIPCHK(gs::launch_fill_u32(tcnt, 0u, (size_t)num_tiles, ctx->st));
+        {
+            // the control words (flags, spin limit, key-range flag), the
+            // histograms with the pass tickets and the tile counts: one launch
+            uint32_t* p[5] = {ctl, ctl + 1, key_err, ctx->sort.hist, tcnt};
+            const uint32_t v[5] = {0u, ctx->spin_limit, 0u, 0u, 0u};
+            const uint32_t w[5] = {1u, 1u, 1u, (uint32_t)gs::sort_hist_words(),
+                                   (uint32_t)num_tiles};
+            HIPCHK(gs::launch_fill_ranges(p, v, w, 5, ctx->st));
+        }
         int passes = 0;
         const hipError_t e = gs::radix_sort_ids_dev_chain(
             keys, ids, n, tb, (uint64_t)num_gaussians, (uint32_t)num_tiles, tcnt, key_err,

@@ -295,6 +295,9 @@ hipError_t launch_part_offsets(const uint32_t* part, int cols, uint32_t rows_cap
 constexpr uint32_t kEmitPartition = 2048;   // candidates per emit partition
 constexpr uint32_t kProjPartition = 2048;   // Gaussians per project partition
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t st);
+// Up to six fills (n[r] words at p[r] set to v[r]) in one launch.
+hipError_t launch_fill_ranges(uint32_t* const* p, const uint32_t* v, const uint32_t* n, int count,
+                              hipStream_t st);
 hipError_t launch_make_keys64(const uint32_t* gid, const uint32_t* tid, const float* depths,
                               uint32_t p, uint64_t* keys, hipStream_t st);
 hipError_t launch_tile_ranges64(const uint64_t* keys, uint32_t p, uint32_t* ranges,

@@ -536,6 +536,26 @@ constexpr int kMinPart = Sweep32::T * Sweep32::I;  // the smallest partition of 
 static_assert(kMinPart == (int)kSortPartition32, "first-pass offsets index these partitions");
 static_assert(kMinPart <= Sweep64::T * Sweep64::I, "kMinPart sizes the look-back state");
 
+// Up to kFillRanges fills in one launch: range r is n[r] words at p[r] set to
+// v[r] (one thread per word of the concatenated ranges).
+constexpr int kFillRanges = 6;
+struct FillRanges {
+    uint32_t* p[kFillRanges];
+    uint32_t v[kFillRanges];
+    uint32_t n[kFillRanges];
+};
+__global__ void k_fill_ranges(FillRanges f) {
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+#pragma unroll
+    for (int r = 0; r < kFillRanges; ++r) {
+        if (i < f.n[r]) {
+            f.p[r][i] = f.v[r];
+            return;
+        }
+        i -= f.n[r];
+    }
+}
+
 __global__ void k_fill_u32(uint32_t* p, uint32_t v, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -940,6 +960,23 @@ hipError_t radix_sort_pairs(void* keys, uint32_t* vals, int64_t n, int key_bytes
         return e;
     }
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_fill_ranges(uint32_t* const* p, const uint32_t* v, const uint32_t* n, int count,
+                              hipStream_t st) {
+    if (count < 0 || count > kFillRanges) return hipErrorInvalidValue;
+    FillRanges f{};
+    uint64_t total = 0;
+    for (int r = 0; r < count; ++r) {
+        f.p[r] = p[r];
+        f.v[r] = v[r];
+        f.n[r] = n[r];
+        total += n[r];
+    }
+    if (total == 0) return hipSuccess;
+    if (total > 0xFFFFFFFFull) return hipErrorInvalidValue;
+    k_fill_ranges<<<(unsigned)((total + 255) / 256), 256, 0, st>>>(f);
+    return hipGetLastError();
 }
 
 hipError_t launch_fill_u32(uint32_t* p, uint32_t v, size_t n, hipStream_t st) {
