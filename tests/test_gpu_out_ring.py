@@ -156,3 +156,35 @@ def test_render_clean_zero_copy(orbit, monkeypatch):
     d = rv(cams[0])  # the announced view, completed from the second slot
     assert np.array_equal(d, plain[0])
     assert np.array_equal(view_of_a, plain[0][10:20]) and np.array_equal(b, plain[1])
+
+
+def test_ring_announced_view_missed_and_dropped(orbit):
+    """An announced view's frame writes into a ring image leased for it: when
+    the next call asks for another view, that frame is completed and its image
+    returns to the ring (no lease left behind), and the call's own image is
+    right; a context closed with an announced frame pending releases it too."""
+    scene, cams, cov = orbit
+    ctx = _ctx(scene, cov)
+    try:
+        views = [L.make_view(c.w2c, c.K, c.height, c.width, tile_size=16, output="u8")
+                 for c in cams]
+        refs = [ctx.render(v)[0] for v in views]
+        ctx.out_ring_config(3)
+        a, _ = ctx.render_ring(views[0], views[1])   # views[1] announced
+        assert np.array_equal(a, refs[0])
+        b, _ = ctx.render_ring(views[2], views[3])   # a miss: views[1]'s frame is dropped
+        assert np.array_equal(b, refs[2])
+        c, _ = ctx.render_ring(views[3])             # the announced one, taken
+        assert np.array_equal(c, refs[3])
+        d = ctx.render(views[4])[0]                  # another entry point between
+        assert np.array_equal(d, refs[4])
+        del a, b, c
+        gc.collect()
+        assert ctx.out_ring_info()[1] == 0  # every lease released, the internal ones too
+        e, _ = ctx.render_ring(views[5], views[0])   # left announced at close
+        assert np.array_equal(e, refs[5])
+    finally:
+        ctx.close()
+    assert np.array_equal(e, refs[5])  # the caller's image outlives the context
+    del e
+    gc.collect()
