@@ -274,6 +274,14 @@ struct gs_ctx {
     }
 
     void sync() { HIPCHK(hipStreamSynchronize(st)); }
+    // Drops a frame that an error interrupted: waits for what it enqueued
+    // (a copy into its output may be in flight) without throwing, so that the
+    // caller can then hand its output buffer back.
+    void abandon_frame() noexcept {
+        if (!pend.active) return;
+        pend.active = false;
+        (void)hipStreamSynchronize(st);
+    }
 
     // ------------------------------------------------------------ scene
     void set_scene(const gs_scene* s) {
@@ -679,8 +687,9 @@ struct gs_ctx {
         try {
             settle_attempts();
         } catch (...) {
-            // no frame stays pending, and the caller's floor's terms are back
-            pend.active = false;
+            // no frame stays pending (a re-run that an error interrupted is
+            // waited for), and the caller's floor's terms are back
+            abandon_frame();
             restore_terms();
             throw;
         }
@@ -895,6 +904,7 @@ struct gs_ctx {
             try {
                 cur->render_begin(v, im->p, false, stats, false);
             } catch (...) {
+                cur->abandon_frame();
                 gs::LeaseTable::get().release(lease);
                 throw;
             }
@@ -910,6 +920,7 @@ struct gs_ctx {
                 try {
                     other->render_begin(next, nim->p, false, &other->spec_st, true);
                 } catch (...) {
+                    other->abandon_frame();
                     gs::LeaseTable::get().release(nl);
                     throw;
                 }
@@ -921,10 +932,7 @@ struct gs_ctx {
             }
             cur->render_end();
         } catch (...) {
-            if (cur->pend.active) {  // the view's frame is dropped with its image
-                cur->pend.active = false;
-                cur->sync();
-            }
+            cur->abandon_frame();  // the view's frame is dropped with its image
             gs::LeaseTable::get().release(lease);
             throw;
         }
@@ -1014,20 +1022,28 @@ struct gs_ctx {
         ensure_terms(&views[0]);
         const int S = std::min(n, kFramesInFlight);
         ensure_peers(S);
-        for (int i = 0; i < n; ++i) {
-            gs_ctx* c = slot(i % S);
-            if (i >= S) c->render_end();  // frame i-S used this slot
-            c->batch_frame = true;
-            try {
-                c->render_begin(&views[i], outs[i], out_dev, stats ? &stats[i] : nullptr, true);
-            } catch (...) {
+        try {
+            for (int i = 0; i < n; ++i) {
+                gs_ctx* c = slot(i % S);
+                if (i >= S) c->render_end();  // frame i-S used this slot
+                c->batch_frame = true;
+                try {
+                    c->render_begin(&views[i], outs[i], out_dev, stats ? &stats[i] : nullptr,
+                                    true);
+                } catch (...) {
+                    c->batch_frame = false;
+                    throw;
+                }
                 c->batch_frame = false;
-                throw;
+                c->pend.batch_index = i;
             }
-            c->batch_frame = false;
-            c->pend.batch_index = i;
+            for (int i = std::max(0, n - S); i < n; ++i) slot(i % S)->render_end();
+        } catch (...) {
+            // the other frames still in flight write into the caller's
+            // outputs: they are finished before the error returns
+            for (int k = 0; k < S; ++k) slot(k)->abandon_frame();
+            throw;
         }
-        for (int i = std::max(0, n - S); i < n; ++i) slot(i % S)->render_end();
     }
 
     // Enqueues one frame (project -> depth sort -> tile assign -> tile sort ->

@@ -103,3 +103,37 @@ def test_pair_limit_with_the_cull_disabled_fails(gpu_ctx):
         gpu_ctx.set_pair_limit(0)
     _, st1 = gpu_ctx.render(view)
     assert st1["pairs_pre"] == st0["pairs_pre"]
+
+
+def test_failing_frame_in_a_batch_finishes_the_others(gpu_ctx):
+    """A frame of a gs_render_batch that fails (the cull disabled, more
+    candidates than the pair limit) fails the call only after every other
+    frame still in flight has finished writing its output: the outputs do not
+    change after the error returns, and the next batch renders every view."""
+    print("overflow: failing frame in a batch of 6", flush=True)
+    scene, cams = scenes.config1()
+    cov = O.cov3d(scene.scales, scene.quats)
+    gpu_ctx.set_scene(scene.means, cov, scene.opacities, scene.colors)
+    cam = cams[0]
+    H, W = cam.height, cam.width
+    views = []
+    for k in range(6):
+        w2c = np.array(cam.w2c, np.float32).copy()
+        w2c[0, 3] += 0.05 * k
+        views.append(L.make_view(w2c, cam.K, H, W, tile_size=16, output="f32",
+                                 cull_disabled=(k == 2)))
+    direct = [gpu_ctx.render(v) for v in views]
+    outs = [np.zeros((H, W, 3), np.float32) for _ in views]
+    try:
+        gpu_ctx.set_pair_limit(int(direct[2][1]["pairs_pre"] // 2))
+        with pytest.raises(L.GsError, match="pair limit"):
+            gpu_ctx.render_batch(views, outs, out_on_device=False)
+        snap = [o.copy() for o in outs]
+    finally:
+        gpu_ctx.set_pair_limit(0)
+    gpu_ctx.render(views[0])
+    for k in range(6):
+        assert np.array_equal(outs[k], snap[k]), k
+    sts = gpu_ctx.render_batch(views, outs, out_on_device=False)
+    for k, st in enumerate(sts):
+        assert st["floor_retries"] == 0 and np.array_equal(outs[k], direct[k][0]), k
