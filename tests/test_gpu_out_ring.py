@@ -188,3 +188,35 @@ def test_ring_announced_view_missed_and_dropped(orbit):
     assert np.array_equal(e, refs[5])  # the caller's image outlives the context
     del e
     gc.collect()
+
+
+def test_ring_announced_view_that_fails(orbit):
+    """An announced frame that fails when taken (the cull disabled, more
+    candidates than the pair limit) raises in the call that takes it, and the
+    ring image leased for it goes back to the ring; the context renders the
+    view once the limit is lifted."""
+    scene, cams, cov = orbit
+    ctx = _ctx(scene, cov)
+    try:
+        va = L.make_view(cams[0].w2c, cams[0].K, cams[0].height, cams[0].width, tile_size=16,
+                         output="u8")
+        vb = L.make_view(cams[1].w2c, cams[1].K, cams[1].height, cams[1].width, tile_size=16,
+                         output="u8", cull_disabled=True)
+        ref_b, st_b = ctx.render(vb)
+        try:
+            ctx.set_pair_limit(int(st_b["pairs_pre"] // 2))
+            a, _ = ctx.render_ring(va, vb)  # vb announced; va re-rendered at a coarser floor
+            with pytest.raises(L.GsError, match="pair limit"):
+                ctx.render_ring(vb)
+            assert ctx.out_ring_info()[1] == 1  # only `a` is held
+        finally:
+            ctx.set_pair_limit(0)
+        del a
+        gc.collect()
+        assert ctx.out_ring_info()[1] == 0
+        b, _ = ctx.render_ring(vb)
+        assert np.array_equal(b, ref_b)
+        del b
+        gc.collect()
+    finally:
+        ctx.close()
