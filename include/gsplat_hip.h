@@ -119,7 +119,9 @@ int gs_render(gs_ctx* ctx, const gs_view* view, void* out, int out_on_device, gs
  * ones (the cross-view pipelining of render/host/xview.h and the next_extrinsics
  * argument of render/host/render.cpp:263-273, for a known list of views).
  * outs[i] receives view i; stats (optional) is an array of n. Every view must
- * share contrib_floor, mb_contrib_floor and k_cap. */
+ * share contrib_floor, mb_contrib_floor and k_cap. When a frame fails, every
+ * frame of the batch still in flight has finished writing its output before
+ * the error is returned. */
 int gs_render_batch(gs_ctx* ctx, const gs_view* views, int n, void* const* outs,
                     int out_on_device, gs_stats* stats);
 /* gs_render of `view`, and - with next_view - the next view's frame enqueued on
