@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <atomic>
 #include <chrono>
 #include <climits>
@@ -458,6 +459,7 @@ struct gs_ctx {
             HIPCHK(hipMemsetAsync(b_state.p, 0, b_state.cap, st));
             sort.epoch = 0;
             sort.dirty[0] = sort.dirty[1] = 0u;
+            sort.clean[0] = sort.clean[1] = 0u;
             sort.half = 0;
         }
         sort.state_parts = b_state.cap / (256 * sizeof(uint64_t));
@@ -1192,6 +1194,13 @@ struct gs_ctx {
     // frame). Frames with timing,
     // microblock statistics or the chunk skip, a capacity re-run and sorts of
     // 2^30 keys or more (epoch-tagged descriptors) are enqueued directly.
+    // The sort's look-back bookkeeping (the half in use, each half's rows that
+    // may hold descriptors): the clearing launches of a captured frame follow
+    // from it, so a graph replays only from the bookkeeping it was captured in.
+    using SortMarks = std::array<uint32_t, 5>;
+    SortMarks sort_marks() const {
+        return {(uint32_t)sort.half, sort.dirty[0], sort.dirty[1], sort.clean[0], sort.clean[1]};
+    }
     struct FrameGraph {
         hipGraph_t graph = nullptr;
         hipGraphExec_t exec = nullptr;
@@ -1203,8 +1212,7 @@ struct gs_ctx {
         int deg = -2;
         uint64_t pcap = 0, gen = 0;
         uint32_t spin = 0;
-        int half = 0;
-        uint32_t dirty0 = 0, dirty1 = 0;
+        SortMarks marks{};
         int misses = 0;  // captures of this shape in a row that were not replayable
     } fg;
 
@@ -1263,8 +1271,7 @@ struct gs_ctx {
         // odd pass count flips its half every frame: above 2^16 tiles the tile
         // sort has three passes) is enqueued directly after two such captures
         if (same_shape && fg.proj == nullptr && fg.misses >= 2) return false;
-        if (fg.exec != nullptr && fg.proj != nullptr && same_shape && fg.half == sort.half &&
-            fg.dirty0 == sort.dirty[0] && fg.dirty1 == sort.dirty[1]) {
+        if (fg.exec != nullptr && fg.proj != nullptr && same_shape && fg.marks == sort_marks()) {
             const gs::ProjParams p = frame_proj_params(&pend.v, L, N, pend.tiles_x, pend.tiles_y);
             HIPCHK(gs::graph_set_project_params(fg.exec, fg.proj, p));
             HIPCHK(hipGraphLaunch(fg.exec, st));
@@ -1285,9 +1292,7 @@ struct gs_ctx {
         g.pcap = pair_cap;
         g.gen = gen;
         g.spin = spin_limit;
-        g.half = sort.half;
-        g.dirty0 = sort.dirty[0];
-        g.dirty1 = sort.dirty[1];
+        g.marks = sort_marks();
         auto capture = [&](hipGraph_t* out) {
             HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
             try {
@@ -1301,8 +1306,7 @@ struct gs_ctx {
             HIPCHK(hipStreamEndCapture(st, out));
         };
         capture(&g.graph);
-        if ((sort.half != g.half || sort.dirty[0] != g.dirty0 || sort.dirty[1] != g.dirty1) &&
-            buffers_key() == gen) {
+        if (sort_marks() != g.marks && buffers_key() == gen) {
             // The frame moved the sort's look-back bookkeeping (a slot's first
             // frame of a shape leaves more rows marked than it found). The
             // graph is dropped unlaunched, the whole descriptor buffer is
@@ -1313,9 +1317,7 @@ struct gs_ctx {
             (void)hipGraphDestroy(g.graph);
             g.graph = nullptr;
             HIPCHK(gs::launch_fill_u32(b_state.as<uint32_t>(), 0u, b_state.cap / 4, st));
-            g.half = sort.half;
-            g.dirty0 = sort.dirty[0];
-            g.dirty1 = sort.dirty[1];
+            g.marks = sort_marks();
             capture(&g.graph);
         }
         hipError_t e = hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0);
@@ -1329,8 +1331,7 @@ struct gs_ctx {
         // replayable only from the sort state it was captured in, with the
         // buffers it captured, and with a projection node to set the view on
         ++fg.misses;  // until a projection node is found below
-        if (sort.half == g.half && sort.dirty[0] == g.dirty0 && sort.dirty[1] == g.dirty1 &&
-            buffers_key() == gen) {
+        if (sort_marks() == g.marks && buffers_key() == gen) {
             size_t nn = 0;
             HIPCHK(hipGraphGetNodes(fg.graph, nullptr, &nn));
             std::vector<hipGraphNode_t> nodes(nn);

@@ -114,10 +114,12 @@ struct SortTemp {
     uint32_t epoch = 0;            // bumped per pass; tags descriptors (no clearing)
     // 32-bit descriptors (below 2^30 keys) use the two halves of `state` in
     // turn: a pass clears, row by row, the half that the next pass uses, so no
-    // pass needs a clearing kernel. dirty[h]: leading partition rows of half h
-    // that may hold descriptors (cleared by a kernel before that half is used).
+    // pass needs a clearing kernel. Rows [clean[h], dirty[h]) of half h may
+    // hold descriptors; a pass clears by a kernel those of them below its own
+    // row count before it uses the half.
     size_t state_parts = 0;        // partition rows per half (state bytes / 2048)
     uint32_t dirty[2] = {0u, 0u};
+    uint32_t clean[2] = {0u, 0u};
     int half = 0;
     hipEvent_t* pass_events = nullptr;  // optional: 2 per pass (start, stop)
     int max_timed_passes = 0;

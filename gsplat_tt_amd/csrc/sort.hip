@@ -594,22 +594,30 @@ hipError_t launch_cfg(bool iota, const K* kin, const uint32_t* vin, K* kout, uin
     uint32_t* state = reinterpret_cast<uint32_t*>(tmp.state);
     uint32_t* clear_next = nullptr;
     if (d32 && tmp.state_parts >= grid) {
+        const int h = tmp.half;
         const size_t half_words = tmp.state_parts * 256;
-        uint32_t* cur = state + (size_t)tmp.half * half_words;
-        clear_next = state + (size_t)(tmp.half ^ 1) * half_words;
-        if (tmp.dirty[tmp.half] != 0u) {
-            const size_t words = (size_t)tmp.dirty[tmp.half] * 256;
-            k_fill_u32<<<(unsigned)((words + 255) / 256), 256, 0, st>>>(cur, 0u, words);
+        uint32_t* cur = state + (size_t)h * half_words;
+        clear_next = state + (size_t)(h ^ 1) * half_words;
+        // the rows this pass uses that may hold descriptors
+        const uint32_t lo = tmp.clean[h], hi = std::min<uint32_t>(tmp.dirty[h], grid);
+        if (hi > lo) {
+            const size_t words = (size_t)(hi - lo) * 256;
+            k_fill_u32<<<(unsigned)((words + 255) / 256), 256, 0, st>>>(cur + (size_t)lo * 256,
+                                                                         0u, words);
         }
-        // this pass dirties rows [0, grid) of its half and clears them in the other
-        tmp.dirty[tmp.half] = grid;
-        if (grid >= tmp.dirty[tmp.half ^ 1]) tmp.dirty[tmp.half ^ 1] = 0u;
+        // this pass fills rows [0, grid) of its half (rows past them keep what
+        // they held) and clears them in the other
+        tmp.dirty[h] = std::max<uint32_t>(tmp.dirty[h], grid);
+        tmp.clean[h] = 0u;
+        tmp.clean[h ^ 1] = std::max<uint32_t>(tmp.clean[h ^ 1], grid);
+        if (tmp.clean[h ^ 1] >= tmp.dirty[h ^ 1]) tmp.clean[h ^ 1] = tmp.dirty[h ^ 1] = 0u;
         tmp.half ^= 1;
         state = cur;
     } else {
         const size_t words = (size_t)grid * 256 * (d32 ? 1 : 2);
         k_fill_u32<<<(unsigned)((words + 255) / 256), 256, 0, st>>>(state, 0u, words);
         tmp.dirty[0] = tmp.dirty[1] = (uint32_t)std::min<size_t>(tmp.state_parts, 0xFFFFFFFFu);
+        tmp.clean[0] = tmp.clean[1] = 0u;
     }
     const uint32_t epoch = ++tmp.epoch;
 #define GS_OSN(IO, DD, DR, RU, NA, KO)                                                          \
